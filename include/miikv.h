@@ -1,0 +1,212 @@
+/*
+ * miikv — MI355X-native (gfx950) quantized KV-cache path: C ABI.
+ *
+ * Launch-only, asynchronous entry points with plain pointers and sizes.  The
+ * caller owns every device buffer (including the workspace); nothing here
+ * allocates device memory.  Each entry point returns a miikv_status: 0 on
+ * success, > 0 for an invalid argument (nothing was launched), < 0 for a HIP
+ * error (the negated hipError_t).  The reference aborts the process on invalid
+ * arguments (include/miinfer/hip_check.hpp:11-38); this ABI reports instead.
+ *
+ * Streams are passed as `void*` holding a hipStream_t (NULL = default stream).
+ * Device-state pointers (miikv_decode_state / miikv_prefill_state) live in
+ * device memory and are read by the kernels, so calls that take them can be
+ * captured into a HIP graph and replayed while the position advances on the
+ * device, as the reference does (include/miinfer/qwen3_gpu_primitives.hpp:30-45).
+ *
+ * ---------------------------------------------------------------------------
+ * Cache layout in HBM (q8_0: 32-value blocks, one fp16 scale per block)
+ * ---------------------------------------------------------------------------
+ * The cache is a set of pages of `page_tokens` tokens (a multiple of 64).  A
+ * CONTIGUOUS cache is the special case of a single page whose page_tokens is the
+ * capacity, which reproduces the reference's [kv_head][capacity][head_dim]
+ * ordering (include/miinfer/prefill_v2/kv_cache.hpp:24-46).  A PAGED cache maps
+ * logical page i of sequence b to physical page block_table[b*table_stride + i].
+ *
+ * Each of the four planes is [page][kv_head][slab]; one slab holds page_tokens
+ * tokens of one kv head:
+ *   k_scales, v_scales slab: [page_tokens][head_dim/32] fp16 (row-major)
+ *   k_codes slab (int8), MFMA-A-operand tiling in 16-token tiles:
+ *       token t = 16*T + m, dim d = 64*c + 32*e + 8*g + j  (m<16, e<2, g<4, j<8)
+ *       byte offset = T*(16*head_dim) + c*1024 + g*256 + m*16 + e*8 + j
+ *   v_codes slab (int8), token-contiguous per dim in 64-token chunks:
+ *       token t = 64*C + 16*J + 4*G + I  (J<4, G<4, I<4)
+ *       byte offset = C*(64*head_dim) + d*64 + G*16 + J*4 + I
+ * miikv_export_canonical() converts any token range back to row-major codes.
+ */
+#ifndef MIIKV_H
+#define MIIKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MIIKV_ABI_VERSION 1u
+#define MIIKV_QBLOCK 32u
+
+typedef int miikv_status;
+enum {
+    MIIKV_OK = 0,
+    MIIKV_EINVAL = 1,       /* invalid argument: nothing launched */
+    MIIKV_EUNSUPPORTED = 2, /* valid but not implemented (e.g. head_dim 64) */
+    MIIKV_EWORKSPACE = 3,   /* workspace missing or too small */
+};
+
+enum { MIIKV_LAYOUT_CONTIGUOUS = 0, MIIKV_LAYOUT_PAGED = 1 };
+
+/* Mirrors KvCacheQuantMode (include/miinfer/prefill_v2/kv_cache.hpp:16-21).
+ * Only MIIKV_KV_Q8_Q8 is implemented by this library. */
+enum { MIIKV_KV_FP16_FP16 = 0, MIIKV_KV_Q8_FP16 = 1, MIIKV_KV_FP16_Q8 = 2, MIIKV_KV_Q8_Q8 = 3 };
+
+enum { MIIKV_DTYPE_F16 = 0, MIIKV_DTYPE_F32 = 1 };
+
+/* Non-owning view of one attention layer's KV cache.
+ * Replaces AttentionKvCacheView (include/miinfer/prefill_v2/kv_cache.hpp:24-46),
+ * adding the block table for paged sequences. */
+typedef struct miikv_view {
+    int8_t* k_codes;
+    uint16_t* k_scales; /* fp16 bits */
+    int8_t* v_codes;
+    uint16_t* v_scales; /* fp16 bits */
+    uint32_t layout;      /* MIIKV_LAYOUT_* */
+    uint32_t quant_mode;  /* MIIKV_KV_* (must be MIIKV_KV_Q8_Q8) */
+    uint32_t kv_heads;
+    uint32_t head_dim;    /* 128 or 256 */
+    uint32_t page_tokens; /* multiple of 64; CONTIGUOUS: the capacity */
+    uint32_t num_pages;   /* CONTIGUOUS: 1 */
+    const int32_t* block_table; /* PAGED: device [batch][table_stride]; CONTIGUOUS: NULL */
+    uint32_t table_stride;      /* PAGED: entries per sequence row */
+    uint32_t reserved;
+} miikv_view;
+
+/* Mirrors DeviceDecodeState (include/miinfer/qwen3_gpu_primitives.hpp:30-37). */
+typedef struct __attribute__((aligned(64))) miikv_decode_state {
+    uint32_t current_token;
+    uint32_t position; /* position of the token being decoded; context = position + 1 */
+    uint32_t generated;
+    uint32_t stop;
+    uint32_t max_generated;
+    uint32_t pad[11];
+} miikv_decode_state;
+
+/* Mirrors DevicePrefillState (include/miinfer/qwen3_gpu_primitives.hpp:39-45). */
+typedef struct __attribute__((aligned(64))) miikv_prefill_state {
+    uint32_t base_position;
+    uint32_t token_count;
+    uint32_t total_length;
+    uint32_t kv_capacity;
+    uint32_t pad[12];
+} miikv_prefill_state;
+
+/* A generic device-to-device copy segment for miikv_copy_segments. */
+typedef struct miikv_segment {
+    void* dst;
+    const void* src;
+    uint64_t bytes;
+} miikv_segment;
+
+/* ---- library ------------------------------------------------------------- */
+
+uint32_t miikv_abi_version(void);
+const char* miikv_status_string(miikv_status status);
+
+/* Bytes of each plane for a view's geometry (codes and scales, per K or V). */
+miikv_status miikv_plane_bytes(const miikv_view* view, uint64_t* code_bytes, uint64_t* scale_bytes);
+
+/* ---- q8_0 append --------------------------------------------------------- */
+
+/* Quantize `token_count` fp16 K and V rows (layout [token][kv_head][head_dim])
+ * into the cache of sequence `seq` at positions base_position .. +token_count-1.
+ * If prefill_state is non-NULL, base_position/token_count are read from it on
+ * the device (token_count must then be an upper bound; rows beyond the device
+ * value are skipped); else if decode_state is non-NULL, one row is stored at
+ * decode_state->position.
+ * Replaces launch_qwen35_decoupled_k_norm_rope_kv_store_batch_quant
+ * (include/miinfer/qwen3_gpu_primitives.hpp:695-717) for pre-normalised fp16
+ * rows; the per-row absmax/127 rule (gfx906/kernels/qwen3_primitives.hip:
+ * 7285-7322) is applied per 32-value block. */
+miikv_status miikv_append_f16(const miikv_view* view, const uint16_t* k, const uint16_t* v,
+                              uint32_t token_count, uint32_t base_position, uint32_t seq,
+                              const miikv_prefill_state* prefill_state,
+                              const miikv_decode_state* decode_state, void* stream);
+
+/* Batched decode append: one fp16 K/V row per sequence (layout [batch][kv_head]
+ * [head_dim]); sequence b's row goes to position d_positions[b] (device array).
+ * No reference counterpart for batching: the reference decodes one sequence
+ * (qwen3_primitives.hip:7239-7241); each row follows the same rule. */
+miikv_status miikv_append_batch_f16(const miikv_view* view, const uint16_t* k, const uint16_t* v,
+                                    uint32_t batch, const uint32_t* d_positions, void* stream);
+
+/* ---- split-K GQA decode attention ---------------------------------------- */
+
+/* Workspace bytes needed by miikv_decode_attn for `batch` sequences of at most
+ * `max_context` tokens.  The workspace must be zeroed once with
+ * miikv_workspace_init before first use; the kernels leave it re-usable. */
+uint64_t miikv_decode_workspace_bytes(const miikv_view* view, uint32_t q_heads, uint32_t batch,
+                                      uint32_t max_context);
+miikv_status miikv_workspace_init(void* workspace, uint64_t bytes, void* stream);
+
+/* Single-token GQA attention for `batch` sequences over the q8_0 cache.
+ *   q       device [batch][q_heads][head_dim], fp16 or fp32 (q_dtype)
+ *   context length of sequence b: d_lengths[b] if d_lengths != NULL, else
+ *           decode_state->position + 1 (batch must be 1)
+ *   max_context  host upper bound on every context length (sizes the grid)
+ *   out     device [batch][q_heads][head_dim] fp32 (nullable)
+ *   gate    device [batch][q_heads][head_dim] fp32 (nullable); gated_out =
+ *           out * sigmoid(gate) (nullable).  At least one output is required.
+ * Replaces launch_qwen35_tiled_online_attention_quant_dynamic
+ * (include/miinfer/qwen3_gpu_primitives.hpp:719-741; kernels
+ * gfx906/kernels/qwen3_primitives.hip:7371-7548 and 2295-2385) with an explicit
+ * workspace instead of module-static split scratch. */
+miikv_status miikv_decode_attn(const miikv_view* view, const void* q, uint32_t q_dtype,
+                               uint32_t q_heads, float scale, uint32_t batch,
+                               const uint32_t* d_lengths, const miikv_decode_state* decode_state,
+                               uint32_t max_context, float* out, const float* gate,
+                               float* gated_out, void* workspace, uint64_t workspace_bytes,
+                               void* stream);
+
+/* ---- export / import ----------------------------------------------------- */
+
+/* Copy tokens [t0, t0+count) of sequence `seq` out of the tiled cache into
+ * canonical row-major buffers: codes [kv_heads][count][head_dim] and scales
+ * [kv_heads][count][head_dim/32] (any pointer may be NULL to skip that plane).
+ * This is the device half of download_raw (src/prefill_v2/kv_cache.cpp:227-297). */
+miikv_status miikv_export_canonical(const miikv_view* view, uint32_t seq, uint32_t t0,
+                                    uint32_t count, int8_t* k_codes, uint16_t* k_scales,
+                                    int8_t* v_codes, uint16_t* v_scales, void* stream);
+
+/* Inverse of miikv_export_canonical (device half of upload_raw,
+ * src/prefill_v2/kv_cache.cpp:299-369). */
+miikv_status miikv_import_canonical(const miikv_view* view, uint32_t seq, uint32_t t0,
+                                    uint32_t count, const int8_t* k_codes,
+                                    const uint16_t* k_scales, const int8_t* v_codes,
+                                    const uint16_t* v_scales, void* stream);
+
+/* ---- prefix-state reuse --------------------------------------------------- */
+
+/* Copy n physical pages (all four planes) src_pages[i] -> dst_pages[i]
+ * (device int32 arrays), byte for byte.  Block-granular KV copy used by
+ * copy-on-write forks.  No reference counterpart: the reference keeps a single
+ * contiguous cache in place (src/prefill_v2/model.cpp:752-846). */
+miikv_status miikv_copy_pages(const miikv_view* view, const int32_t* d_src_pages,
+                              const int32_t* d_dst_pages, uint32_t n, void* stream);
+
+/* Execute n device-to-device copies described by a DEVICE array of segments in
+ * one launch.  Replaces the 2*48 hipMemcpyAsync calls of
+ * GdnCheckpointStorage::capture/restore (src/prefill_v2/reusable_context.cpp:65-128). */
+miikv_status miikv_copy_segments(const miikv_segment* d_segments, uint32_t n, void* stream);
+
+/* Clone `bytes` of src into each of n destinations (device array of pointers):
+ * the recurrent-state clone of forked sessions.  bytes must be a multiple of 16
+ * and every pointer 16-byte aligned. */
+miikv_status miikv_clone_state(void* const* d_dsts, const void* src, uint64_t bytes, uint32_t n,
+                               void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MIIKV_H */

@@ -1,0 +1,372 @@
+// q8_0 append, canonical export/import, page copy, segment copy and state clone.
+#include "miikv_common.hpp"
+
+#include <cmath>
+
+namespace miikv {
+
+// Host-side validation of a view (shared with the decode launcher).
+int validate_view(const miikv_view* v) {
+    if (v == nullptr) return MIIKV_EINVAL;
+    if (v->k_codes == nullptr || v->k_scales == nullptr || v->v_codes == nullptr || v->v_scales == nullptr)
+        return MIIKV_EINVAL;
+    if (v->quant_mode != MIIKV_KV_Q8_Q8) return MIIKV_EUNSUPPORTED;
+    if (v->head_dim != 128 && v->head_dim != 256) return MIIKV_EUNSUPPORTED;
+    if (v->kv_heads == 0 || v->page_tokens == 0 || v->page_tokens % kChunk != 0) return MIIKV_EINVAL;
+    if (v->layout == MIIKV_LAYOUT_CONTIGUOUS) {
+        if (v->num_pages != 1) return MIIKV_EINVAL;
+    } else if (v->layout == MIIKV_LAYOUT_PAGED) {
+        if (v->block_table == nullptr || v->table_stride == 0 || v->num_pages == 0) return MIIKV_EINVAL;
+    } else {
+        return MIIKV_EINVAL;
+    }
+    return MIIKV_OK;
+}
+
+// Largest logical token count a sequence of this view can hold.
+uint64_t view_seq_capacity(const miikv_view* v) {
+    if (v->layout == MIIKV_LAYOUT_CONTIGUOUS) return v->page_tokens;
+    return static_cast<uint64_t>(v->table_stride) * v->page_tokens;
+}
+
+namespace {
+
+// One thread per (row, 16-dim group); a row is (token, kv_head).  Adjacent
+// lanes (2i, 2i+1) hold the two halves of one 32-value block.
+__global__ void __launch_bounds__(256) append_kernel(
+    Geo g, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, uint32_t token_count,
+    uint32_t base_position, uint32_t seq, const miikv_prefill_state* __restrict__ ps,
+    const miikv_decode_state* __restrict__ ds, const uint32_t* __restrict__ positions) {
+    if (ps != nullptr) {
+        base_position = ps->base_position;
+        token_count = min(token_count, ps->token_count);
+    } else if (ds != nullptr) {
+        base_position = ds->position;
+        token_count = 1;
+    }
+    const uint32_t D = g.head_dim;
+    const uint32_t groups = D / 16;
+    const uint64_t gid = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const uint64_t row = gid / groups;
+    const uint32_t q16 = static_cast<uint32_t>(gid % groups);
+    const uint32_t token = static_cast<uint32_t>(row / g.kv_heads);
+    const uint32_t head = static_cast<uint32_t>(row % g.kv_heads);
+    if (token >= token_count) return;  // whole (even, odd) pairs exit together
+
+    uint32_t pos;
+    if (positions != nullptr) {  // batched decode: row `token` is sequence `token`
+        seq = token;
+        pos = positions[token];
+    } else {
+        pos = base_position + token;
+    }
+    const uint64_t limit = (g.layout == MIIKV_LAYOUT_PAGED)
+                               ? static_cast<uint64_t>(g.table_stride) * g.page_tokens
+                               : g.page_tokens;
+    const bool in_range = pos < limit;
+
+    const size_t src = static_cast<size_t>(row) * D + q16 * 16;
+    float xk[16], xv[16];
+    {
+        const uint4 a = *reinterpret_cast<const uint4*>(k + src);
+        const uint4 b = *reinterpret_cast<const uint4*>(k + src + 8);
+        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            xk[2 * i] = f16_bits_to_f32(static_cast<uint16_t>(w[i] & 0xffffu));
+            xk[2 * i + 1] = f16_bits_to_f32(static_cast<uint16_t>(w[i] >> 16));
+        }
+    }
+    {
+        const uint4 a = *reinterpret_cast<const uint4*>(v + src);
+        const uint4 b = *reinterpret_cast<const uint4*>(v + src + 8);
+        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            xv[2 * i] = f16_bits_to_f32(static_cast<uint16_t>(w[i] & 0xffffu));
+            xv[2 * i + 1] = f16_bits_to_f32(static_cast<uint16_t>(w[i] >> 16));
+        }
+    }
+    int8_t qk[16], qv[16];
+    float sk, sv;
+    quantize16(xk, qk, sk);  // both lanes of the pair reach the shuffles
+    quantize16(xv, qv, sv);
+    if (!in_range) return;
+
+    const size_t slab = slab_of(g, seq, pos, head);
+    const uint32_t tp = pos % g.page_tokens;
+    const size_t slab_bytes = static_cast<size_t>(g.page_tokens) * D;
+    const uint32_t d0 = q16 * 16;
+
+    // K: dims d0..d0+7 and d0+8..d0+15 are two 8-byte runs of the tiled layout.
+    int8_t* kslab = g.k_codes + slab * slab_bytes;
+    uint32_t packed[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        packed[w] = (static_cast<uint32_t>(static_cast<uint8_t>(qk[4 * w]))) |
+                    (static_cast<uint32_t>(static_cast<uint8_t>(qk[4 * w + 1])) << 8) |
+                    (static_cast<uint32_t>(static_cast<uint8_t>(qk[4 * w + 2])) << 16) |
+                    (static_cast<uint32_t>(static_cast<uint8_t>(qk[4 * w + 3])) << 24);
+    }
+    *reinterpret_cast<uint2*>(kslab + k_code_offset(tp, d0, D)) = make_uint2(packed[0], packed[1]);
+    *reinterpret_cast<uint2*>(kslab + k_code_offset(tp, d0 + 8, D)) = make_uint2(packed[2], packed[3]);
+
+    // V: each dim is its own token-contiguous run; one byte per dim.
+    int8_t* vslab = g.v_codes + slab * slab_bytes;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) vslab[v_code_offset(tp, d0 + i, D)] = qv[i];
+
+    if ((q16 & 1) == 0) {
+        const size_t sidx = (slab * g.page_tokens + tp) * (D / 32) + d0 / 32;
+        g.k_scales[sidx] = f32_to_f16_bits(sk);
+        g.v_scales[sidx] = f32_to_f16_bits(sv);
+    }
+}
+
+// Tiled -> canonical (export) or canonical -> tiled (import), one thread per
+// (token, kv_head, 16-dim group).
+template <bool EXPORT>
+__global__ void __launch_bounds__(256) canonical_kernel(
+    Geo g, uint32_t seq, uint32_t t0, uint32_t count, int8_t* kc, uint16_t* ks, int8_t* vc,
+    uint16_t* vs) {
+    const uint32_t D = g.head_dim;
+    const uint32_t groups = D / 16;
+    const uint64_t gid = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const uint64_t total = static_cast<uint64_t>(count) * g.kv_heads * groups;
+    if (gid >= total) return;
+    const uint32_t q16 = static_cast<uint32_t>(gid % groups);
+    const uint64_t r = gid / groups;
+    const uint32_t t = static_cast<uint32_t>(r % count);
+    const uint32_t head = static_cast<uint32_t>(r / count);
+    const uint32_t pos = t0 + t;
+    const size_t slab = slab_of(g, seq, pos, head);
+    const uint32_t tp = pos % g.page_tokens;
+    const size_t slab_bytes = static_cast<size_t>(g.page_tokens) * D;
+    const uint32_t d0 = q16 * 16;
+    const size_t crow = (static_cast<size_t>(head) * count + t) * D + d0;
+    int8_t* kslab = g.k_codes + slab * slab_bytes;
+    int8_t* vslab = g.v_codes + slab * slab_bytes;
+    const size_t sidx = (slab * g.page_tokens + tp) * (D / 32) + d0 / 32;
+    const size_t csidx = (static_cast<size_t>(head) * count + t) * (D / 32) + d0 / 32;
+    if (EXPORT) {
+        if (kc != nullptr) {
+            const uint2 a = *reinterpret_cast<const uint2*>(kslab + k_code_offset(tp, d0, D));
+            const uint2 b = *reinterpret_cast<const uint2*>(kslab + k_code_offset(tp, d0 + 8, D));
+            *reinterpret_cast<uint4*>(kc + crow) = make_uint4(a.x, a.y, b.x, b.y);
+        }
+        if (vc != nullptr) {
+            uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                w[i / 4] |= static_cast<uint32_t>(static_cast<uint8_t>(vslab[v_code_offset(tp, d0 + i, D)]))
+                            << (8 * (i % 4));
+            *reinterpret_cast<uint4*>(vc + crow) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+        if ((q16 & 1) == 0) {
+            if (ks != nullptr) ks[csidx] = g.k_scales[sidx];
+            if (vs != nullptr) vs[csidx] = g.v_scales[sidx];
+        }
+    } else {
+        if (kc != nullptr) {
+            const uint4 a = *reinterpret_cast<const uint4*>(kc + crow);
+            *reinterpret_cast<uint2*>(kslab + k_code_offset(tp, d0, D)) = make_uint2(a.x, a.y);
+            *reinterpret_cast<uint2*>(kslab + k_code_offset(tp, d0 + 8, D)) = make_uint2(a.z, a.w);
+        }
+        if (vc != nullptr) {
+            const uint4 a = *reinterpret_cast<const uint4*>(vc + crow);
+            const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                vslab[v_code_offset(tp, d0 + i, D)] = static_cast<int8_t>((w[i / 4] >> (8 * (i % 4))) & 0xffu);
+        }
+        if ((q16 & 1) == 0) {
+            if (ks != nullptr) g.k_scales[sidx] = ks[csidx];
+            if (vs != nullptr) g.v_scales[sidx] = vs[csidx];
+        }
+    }
+}
+
+// Copy [src, src+bytes) to dst with 16-byte vectors; `bytes` is a multiple of 16.
+__device__ __forceinline__ void copy16(uint4* __restrict__ dst, const uint4* __restrict__ src, uint64_t n16,
+                                       uint64_t start, uint64_t stride) {
+    for (uint64_t i = start; i < n16; i += stride) dst[i] = src[i];
+}
+
+// grid (blocks, n_pages): block y copies page src_pages[y] -> dst_pages[y], all four planes.
+__global__ void __launch_bounds__(256) copy_pages_kernel(Geo g, const int32_t* __restrict__ srcp,
+                                                         const int32_t* __restrict__ dstp) {
+    const uint32_t i = blockIdx.y;
+    const size_t s = static_cast<size_t>(srcp[i]);
+    const size_t d = static_cast<size_t>(dstp[i]);
+    const uint64_t code_bytes = static_cast<uint64_t>(g.kv_heads) * g.page_tokens * g.head_dim;
+    const uint64_t scale_bytes = static_cast<uint64_t>(g.kv_heads) * g.page_tokens * (g.head_dim / 32) * 2;
+    const uint64_t start = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    copy16(reinterpret_cast<uint4*>(g.k_codes + d * code_bytes),
+           reinterpret_cast<const uint4*>(g.k_codes + s * code_bytes), code_bytes / 16, start, stride);
+    copy16(reinterpret_cast<uint4*>(g.v_codes + d * code_bytes),
+           reinterpret_cast<const uint4*>(g.v_codes + s * code_bytes), code_bytes / 16, start, stride);
+    copy16(reinterpret_cast<uint4*>(reinterpret_cast<uint8_t*>(g.k_scales) + d * scale_bytes),
+           reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(g.k_scales) + s * scale_bytes),
+           scale_bytes / 16, start, stride);
+    copy16(reinterpret_cast<uint4*>(reinterpret_cast<uint8_t*>(g.v_scales) + d * scale_bytes),
+           reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(g.v_scales) + s * scale_bytes),
+           scale_bytes / 16, start, stride);
+}
+
+// grid (blocks, n): block y copies segment y.  16-byte path when both ends and
+// the size are 16-byte aligned, byte path otherwise.
+__global__ void __launch_bounds__(256) copy_segments_kernel(const miikv_segment* __restrict__ segs) {
+    const miikv_segment sg = segs[blockIdx.y];
+    const uint64_t start = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    const bool aligned = ((reinterpret_cast<uintptr_t>(sg.dst) | reinterpret_cast<uintptr_t>(sg.src) | sg.bytes) & 15u) == 0;
+    if (aligned) {
+        copy16(reinterpret_cast<uint4*>(sg.dst), reinterpret_cast<const uint4*>(sg.src), sg.bytes / 16, start, stride);
+    } else {
+        uint8_t* d = reinterpret_cast<uint8_t*>(sg.dst);
+        const uint8_t* s = reinterpret_cast<const uint8_t*>(sg.src);
+        for (uint64_t i = start; i < sg.bytes; i += stride) d[i] = s[i];
+    }
+}
+
+// Each thread reads one 16-byte vector of the source once and writes it to
+// every destination, so the source is fetched from HBM once per clone batch.
+__global__ void __launch_bounds__(256) clone_state_kernel(void* const* __restrict__ dsts,
+                                                          const uint4* __restrict__ src, uint64_t n16,
+                                                          uint32_t n) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n16; i += stride) {
+        const uint4 x = src[i];
+        for (uint32_t k = 0; k < n; ++k) reinterpret_cast<uint4*>(dsts[k])[i] = x;
+    }
+}
+
+int launch_status() { return hip_status(hipGetLastError()); }
+
+}  // namespace
+}  // namespace miikv
+
+using namespace miikv;
+
+extern "C" uint32_t miikv_abi_version(void) { return MIIKV_ABI_VERSION; }
+
+extern "C" const char* miikv_status_string(miikv_status s) {
+    switch (s) {
+        case MIIKV_OK: return "ok";
+        case MIIKV_EINVAL: return "invalid argument";
+        case MIIKV_EUNSUPPORTED: return "unsupported configuration";
+        case MIIKV_EWORKSPACE: return "workspace missing or too small";
+        default: return s < 0 ? hipGetErrorString(static_cast<hipError_t>(-s)) : "unknown status";
+    }
+}
+
+extern "C" miikv_status miikv_plane_bytes(const miikv_view* view, uint64_t* code_bytes, uint64_t* scale_bytes) {
+    const int st = validate_view(view);
+    if (st != MIIKV_OK) return st;
+    const uint64_t tokens = static_cast<uint64_t>(view->num_pages) * view->page_tokens * view->kv_heads;
+    if (code_bytes) *code_bytes = tokens * view->head_dim;
+    if (scale_bytes) *scale_bytes = tokens * (view->head_dim / 32) * 2;
+    return MIIKV_OK;
+}
+
+static miikv_status launch_append(const miikv_view* view, const uint16_t* k, const uint16_t* v, uint32_t rows_tokens,
+                                  uint32_t base, uint32_t seq, const miikv_prefill_state* ps,
+                                  const miikv_decode_state* ds, const uint32_t* positions, void* stream) {
+    const uint64_t threads = static_cast<uint64_t>(rows_tokens) * view->kv_heads * (view->head_dim / 16);
+    if (threads == 0) return MIIKV_OK;
+    const uint64_t blocks = (threads + 255) / 256;
+    if (blocks > 0x7fffffffu) return MIIKV_EINVAL;
+    hipLaunchKernelGGL(append_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), make_geo(*view), k, v, rows_tokens, base, seq, ps, ds,
+                       positions);
+    return launch_status();
+}
+
+extern "C" miikv_status miikv_append_f16(const miikv_view* view, const uint16_t* k, const uint16_t* v,
+                                         uint32_t token_count, uint32_t base_position, uint32_t seq,
+                                         const miikv_prefill_state* prefill_state,
+                                         const miikv_decode_state* decode_state, void* stream) {
+    const int st = validate_view(view);
+    if (st != MIIKV_OK) return st;
+    if (k == nullptr || v == nullptr) return MIIKV_EINVAL;
+    if (decode_state != nullptr && prefill_state == nullptr) token_count = 1;
+    if (prefill_state == nullptr && decode_state == nullptr &&
+        static_cast<uint64_t>(base_position) + token_count > view_seq_capacity(view))
+        return MIIKV_EINVAL;
+    if (view->layout == MIIKV_LAYOUT_CONTIGUOUS && seq != 0) return MIIKV_EINVAL;
+    return launch_append(view, k, v, token_count, base_position, seq, prefill_state, decode_state, nullptr, stream);
+}
+
+extern "C" miikv_status miikv_append_batch_f16(const miikv_view* view, const uint16_t* k, const uint16_t* v,
+                                               uint32_t batch, const uint32_t* d_positions, void* stream) {
+    const int st = validate_view(view);
+    if (st != MIIKV_OK) return st;
+    if (k == nullptr || v == nullptr || d_positions == nullptr) return MIIKV_EINVAL;
+    if (view->layout == MIIKV_LAYOUT_CONTIGUOUS && batch > 1) return MIIKV_EINVAL;
+    return launch_append(view, k, v, batch, 0, 0, nullptr, nullptr, d_positions, stream);
+}
+
+template <bool EXPORT>
+static miikv_status launch_canonical(const miikv_view* view, uint32_t seq, uint32_t t0, uint32_t count, int8_t* kc,
+                                     uint16_t* ks, int8_t* vc, uint16_t* vs, void* stream) {
+    const int st = validate_view(view);
+    if (st != MIIKV_OK) return st;
+    if (static_cast<uint64_t>(t0) + count > view_seq_capacity(view)) return MIIKV_EINVAL;
+    if (view->layout == MIIKV_LAYOUT_CONTIGUOUS && seq != 0) return MIIKV_EINVAL;
+    const uint64_t threads = static_cast<uint64_t>(count) * view->kv_heads * (view->head_dim / 16);
+    if (threads == 0) return MIIKV_OK;
+    const uint64_t blocks = (threads + 255) / 256;
+    hipLaunchKernelGGL(canonical_kernel<EXPORT>, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), make_geo(*view), seq, t0, count, kc, ks, vc, vs);
+    return launch_status();
+}
+
+extern "C" miikv_status miikv_export_canonical(const miikv_view* view, uint32_t seq, uint32_t t0, uint32_t count,
+                                               int8_t* k_codes, uint16_t* k_scales, int8_t* v_codes,
+                                               uint16_t* v_scales, void* stream) {
+    return launch_canonical<true>(view, seq, t0, count, k_codes, k_scales, v_codes, v_scales, stream);
+}
+
+extern "C" miikv_status miikv_import_canonical(const miikv_view* view, uint32_t seq, uint32_t t0, uint32_t count,
+                                               const int8_t* k_codes, const uint16_t* k_scales,
+                                               const int8_t* v_codes, const uint16_t* v_scales, void* stream) {
+    return launch_canonical<false>(view, seq, t0, count, const_cast<int8_t*>(k_codes),
+                                   const_cast<uint16_t*>(k_scales), const_cast<int8_t*>(v_codes),
+                                   const_cast<uint16_t*>(v_scales), stream);
+}
+
+extern "C" miikv_status miikv_copy_pages(const miikv_view* view, const int32_t* d_src_pages,
+                                         const int32_t* d_dst_pages, uint32_t n, void* stream) {
+    const int st = validate_view(view);
+    if (st != MIIKV_OK) return st;
+    if (n == 0) return MIIKV_OK;
+    if (d_src_pages == nullptr || d_dst_pages == nullptr || n > 65535u) return MIIKV_EINVAL;
+    const uint64_t code16 = static_cast<uint64_t>(view->kv_heads) * view->page_tokens * view->head_dim / 16;
+    uint32_t blocks = static_cast<uint32_t>((code16 + 255) / 256);
+    if (blocks > 64) blocks = 64;
+    hipLaunchKernelGGL(copy_pages_kernel, dim3(blocks, n), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       make_geo(*view), d_src_pages, d_dst_pages);
+    return launch_status();
+}
+
+extern "C" miikv_status miikv_copy_segments(const miikv_segment* d_segments, uint32_t n, void* stream) {
+    if (n == 0) return MIIKV_OK;
+    if (d_segments == nullptr || n > 65535u) return MIIKV_EINVAL;
+    hipLaunchKernelGGL(copy_segments_kernel, dim3(128, n), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       d_segments);
+    return launch_status();
+}
+
+extern "C" miikv_status miikv_clone_state(void* const* d_dsts, const void* src, uint64_t bytes, uint32_t n,
+                                          void* stream) {
+    if (n == 0 || bytes == 0) return MIIKV_OK;
+    if (d_dsts == nullptr || src == nullptr || (bytes & 15u) != 0 || (reinterpret_cast<uintptr_t>(src) & 15u) != 0)
+        return MIIKV_EINVAL;
+    const uint64_t n16 = bytes / 16;
+    uint64_t blocks = (n16 + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(clone_state_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), d_dsts, reinterpret_cast<const uint4*>(src), n16, n);
+    return launch_status();
+}

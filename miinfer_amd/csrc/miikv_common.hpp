@@ -1,0 +1,144 @@
+// Shared device helpers for the miikv kernels (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "miikv.h"
+
+namespace miikv {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kWave = 64;
+constexpr uint32_t kChunk = 64;   // tokens per V chunk / per wave step
+constexpr uint32_t kTile = 16;    // tokens per K tile (MFMA M/N)
+
+// Geometry of a cache view, passed by value to kernels.
+struct Geo {
+    int8_t* k_codes;
+    uint16_t* k_scales;
+    int8_t* v_codes;
+    uint16_t* v_scales;
+    const int32_t* table;
+    uint32_t layout;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t page_tokens;
+    uint32_t table_stride;
+};
+
+inline Geo make_geo(const miikv_view& v) {
+    Geo g;
+    g.k_codes = v.k_codes;
+    g.k_scales = v.k_scales;
+    g.v_codes = v.v_codes;
+    g.v_scales = v.v_scales;
+    g.table = v.block_table;
+    g.layout = v.layout;
+    g.kv_heads = v.kv_heads;
+    g.head_dim = v.head_dim;
+    g.page_tokens = v.page_tokens;
+    g.table_stride = v.table_stride;
+    return g;
+}
+
+// Slab index (page * kv_heads + head) holding token `pos` of sequence `seq`.
+__device__ __forceinline__ size_t slab_of(const Geo& g, uint32_t seq, uint32_t pos, uint32_t head) {
+    uint32_t page = 0;
+    if (g.layout == MIIKV_LAYOUT_PAGED) {
+        page = static_cast<uint32_t>(g.table[static_cast<size_t>(seq) * g.table_stride + pos / g.page_tokens]);
+    }
+    return static_cast<size_t>(page) * g.kv_heads + head;
+}
+
+// Byte offset of (token tp within the slab, dim d) in a K-code slab.
+__device__ __forceinline__ uint32_t k_code_offset(uint32_t tp, uint32_t d, uint32_t D) {
+    const uint32_t T = tp >> 4, m = tp & 15;
+    const uint32_t c = d >> 6, e = (d >> 5) & 1, gq = (d >> 3) & 3, j = d & 7;
+    return T * (16 * D) + c * 1024 + gq * 256 + m * 16 + e * 8 + j;
+}
+
+// Byte offset of (token tp within the slab, dim d) in a V-code slab.
+__device__ __forceinline__ uint32_t v_code_offset(uint32_t tp, uint32_t d, uint32_t D) {
+    const uint32_t C = tp >> 6, J = (tp >> 4) & 3, G = (tp >> 2) & 3, I = tp & 3;
+    return C * (64 * D) + d * 64 + G * 16 + J * 4 + I;
+}
+
+// q8_0 quantization of 16 values held by this lane; its partner lane (lane ^ 1)
+// holds the other 16 values of the same 32-value block.  Rule of
+// gfx906/kernels/qwen3_primitives.hip:7285-7322 applied per block.
+__device__ __forceinline__ void quantize16(const float (&x)[16], int8_t (&q)[16], float& scale_out) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(x[i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    const float scale = (amax > 0.0f) ? (amax / 127.0f) : 1.0f;
+    const float inv = (scale > 0.0f) ? (1.0f / scale) : 1.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        int r = __float2int_rn(x[i] * inv);
+        r = max(-128, min(127, r));
+        q[i] = static_cast<int8_t>(r);
+    }
+    scale_out = scale;
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float x) {
+    __half h = __float2half_rn(x);
+    return __half_as_ushort(h);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
+    return __half2float(__ushort_as_half(b));
+}
+
+// Four signed int8 codes (one dword) -> four exact fp16 values, two per dword.
+// u = c ^ 0x80 = c + 128; the fp16 with bits 0x6400|u equals 1024 + u, so
+// subtracting 1152 yields c exactly.
+__device__ __forceinline__ void codes4_to_half(uint32_t w, half2v& lo, half2v& hi) {
+    const uint32_t u = w ^ 0x80808080u;
+    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    const half2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    lo = __builtin_bit_cast(half2v, a) - bias;
+    hi = __builtin_bit_cast(half2v, b) - bias;
+}
+
+// Eight codes (two dwords) -> half8 in code order.
+__device__ __forceinline__ half8 codes8_to_half8(uint32_t w0, uint32_t w1) {
+    half2v a, b, c, d;
+    codes4_to_half(w0, a, b);
+    codes4_to_half(w1, c, d);
+    half8 r;
+    r[0] = a[0]; r[1] = a[1]; r[2] = b[0]; r[3] = b[1];
+    r[4] = c[0]; r[5] = c[1]; r[6] = d[0]; r[7] = d[1];
+    return r;
+}
+
+// Four codes (one dword) -> half4 in code order.
+__device__ __forceinline__ half4 codes4_to_half4(uint32_t w) {
+    half2v a, b;
+    codes4_to_half(w, a, b);
+    half4 r;
+    r[0] = a[0]; r[1] = a[1]; r[2] = b[0]; r[3] = b[1];
+    return r;
+}
+
+__device__ __forceinline__ float4v mfma_16x16x32(half8 a, half8 b, float4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float4v mfma_16x16x16(half4 a, half4 b, float4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+inline int hip_status(hipError_t e) { return e == hipSuccess ? MIIKV_OK : -static_cast<int>(e); }
+
+}  // namespace miikv

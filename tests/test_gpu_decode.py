@@ -1,0 +1,152 @@
+"""Split-K GQA decode attention over the q8_0 cache vs the fp32 oracle (GPU).
+
+Tolerance: max-abs 2e-3 and relative 1e-2 (tests/helpers.py)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.helpers import assert_attention_close, randn_f16
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a, gpu):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+
+
+def _filled_contiguous(gpu, rng, hk, d, cap, n):
+    import miinfer_amd as m
+    cache = m.KvCache.contiguous(hk, d, cap)
+    k = randn_f16(rng, (n, hk, d))
+    v = randn_f16(rng, (n, hk, d))
+    if n:
+        cache.append(_dev(k, gpu), _dev(v, gpu))
+    kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+    vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+    return cache, (kc, ks, vc, vs)
+
+
+@pytest.mark.parametrize("length", [1, 2, 17, 63, 64, 65, 300, 1024, 4096])
+def test_decode_c2_shape(gpu, length):
+    import miinfer_amd as m
+    hq, hk, d = 32, 8, 128
+    rng = np.random.default_rng(length)
+    cache, ref = _filled_contiguous(gpu, rng, hk, d, 4096, length)
+    q = randn_f16(rng, (1, hq, d))
+    lens = _dev(np.array([length], np.int32), gpu)
+    out, _ = m.decode_attention(cache, _dev(q, gpu), lengths=lens, max_context=4096)
+    torch.cuda.synchronize()
+    expect = oracle.attention_q8(q[0].astype(np.float32), *ref, length, hq, 1 / math.sqrt(d))
+    assert_attention_close(out[0].cpu().numpy(), expect, f"L={length}")
+
+
+def test_decode_c2_32k_with_gate_and_state(gpu):
+    import miinfer_amd as m
+    hq, hk, d, length = 32, 8, 128, 32768
+    rng = np.random.default_rng(2)
+    cache, ref = _filled_contiguous(gpu, rng, hk, d, length, length)
+    q = randn_f16(rng, (1, hq, d))
+    gate = rng.standard_normal((1, hq, d)).astype(np.float32)
+    ds = m.make_decode_state(length - 1, device=gpu)
+    out, gated = m.decode_attention(cache, _dev(q, gpu), decode_state=ds, gate=_dev(gate, gpu),
+                                    out=torch.empty((1, hq, d), device=gpu))
+    torch.cuda.synchronize()
+    expect = oracle.attention_q8(q[0].astype(np.float32), *ref, length, hq, 1 / math.sqrt(d))
+    assert_attention_close(out[0].cpu().numpy(), expect, "32k")
+    assert_attention_close(gated[0].cpu().numpy(), expect / (1 + np.exp(-gate[0])), "32k gated")
+
+
+def test_decode_fp32_query(gpu):
+    import miinfer_amd as m
+    hq, hk, d, length = 32, 8, 128, 777
+    rng = np.random.default_rng(3)
+    cache, ref = _filled_contiguous(gpu, rng, hk, d, 1024, length)
+    q = rng.standard_normal((1, hq, d)).astype(np.float32)  # not fp16-representable
+    lens = _dev(np.array([length], np.int32), gpu)
+    out, _ = m.decode_attention(cache, _dev(q, gpu), lengths=lens, max_context=1024)
+    torch.cuda.synchronize()
+    expect = oracle.attention_q8(q[0], *ref, length, hq, 1 / math.sqrt(d))
+    assert_attention_close(out[0].cpu().numpy(), expect, "fp32 q")
+
+
+def test_decode_replays_are_byte_identical(gpu):
+    """The reference requires byte-identical replays
+    (tests/qwen3_cached_attention_determinism_gpu_test.cpp:52-114); the arrival counters
+    must also be left at zero for the next call."""
+    import miinfer_amd as m
+    hq, hk, d, length = 32, 8, 128, 5000
+    rng = np.random.default_rng(4)
+    cache, _ = _filled_contiguous(gpu, rng, hk, d, 8192, length)
+    q = _dev(randn_f16(rng, (1, hq, d)), gpu)
+    lens = _dev(np.array([length], np.int32), gpu)
+    ws = m.DecodeWorkspace(cache, hq, 1, 8192)
+    outs = []
+    for _ in range(16):
+        o, _ = m.decode_attention(cache, q, lengths=lens, max_context=8192, workspace=ws)
+        outs.append(o.clone())
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+
+
+def test_decode_zero_length_gives_zeros(gpu):
+    import miinfer_amd as m
+    cache, _ = _filled_contiguous(gpu, np.random.default_rng(5), 8, 128, 256, 10)
+    q = torch.ones((1, 32, 128), dtype=torch.float16, device=gpu)
+    out = torch.full((1, 32, 128), 7.0, device=gpu)
+    m.decode_attention(cache, q, lengths=torch.zeros(1, dtype=torch.int32, device=gpu),
+                       max_context=256, out=out)
+    torch.cuda.synchronize()
+    assert not out.any()
+
+
+@pytest.mark.parametrize("hq,hk,d", [(24, 4, 256), (32, 8, 128)])
+def test_decode_paged_batched(gpu, hq, hk, d):
+    """Config-3 style: sequences of ragged length in 256-token pages behind a random table."""
+    import miinfer_amd as m
+    rng = np.random.default_rng(hq + d)
+    pt = 256
+    lens = [1, 255, 256, 257, 3000, 1100]
+    pages = [(n + pt) // pt for n in lens]  # room for one more token
+    stride = max(pages)
+    total = sum(pages)
+    perm = rng.permutation(total).astype(np.int32)
+    table = np.zeros((len(lens), stride), np.int32)
+    o = 0
+    for s, p in enumerate(pages):
+        table[s, :p] = perm[o:o + p]
+        o += p
+    cache = m.KvCache.paged_cache(hk, d, total, _dev(table, gpu), page_tokens=pt)
+    refs = []
+    for s, n in enumerate(lens):
+        k = randn_f16(rng, (n, hk, d))
+        v = randn_f16(rng, (n, hk, d))
+        cache.append(_dev(k, gpu), _dev(v, gpu), base_position=0, seq=s)
+        kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+        vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+        refs.append((kc, ks, vc, vs))
+    q = randn_f16(rng, (len(lens), hq, d))
+    max_ctx = stride * pt
+    out, _ = m.decode_attention(cache, _dev(q, gpu), lengths=_dev(np.array(lens, np.int32), gpu),
+                                max_context=max_ctx)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    for s, n in enumerate(lens):
+        expect = oracle.attention_q8(q[s].astype(np.float32), *refs[s], n, hq, 1 / math.sqrt(d))
+        assert_attention_close(out[s], expect, f"seq {s} L={n}")
+
+
+def test_decode_rejects_bad_arguments(gpu):
+    import miinfer_amd as m
+    cache, _ = _filled_contiguous(gpu, np.random.default_rng(6), 8, 128, 256, 4)
+    q = torch.zeros((1, 30, 128), dtype=torch.float16, device=gpu)  # 30 % 8 != 0
+    with pytest.raises((m.MiikvError, ValueError)):
+        m.decode_attention(cache, q, lengths=torch.ones(1, dtype=torch.int32, device=gpu),
+                           max_context=256)
+    q = torch.zeros((1, 32, 128), dtype=torch.float16, device=gpu)
+    with pytest.raises(m.MiikvError):  # max_context beyond capacity
+        m.decode_attention(cache, q, lengths=torch.ones(1, dtype=torch.int32, device=gpu),
+                           max_context=512)
