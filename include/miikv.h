@@ -143,8 +143,9 @@ miikv_status miikv_append_batch_f16(const miikv_view* view, const uint16_t* k, c
 /* ---- split-K GQA decode attention ---------------------------------------- */
 
 /* Workspace bytes needed by miikv_decode_attn for `batch` sequences of at most
- * `max_context` tokens.  The workspace must be zeroed once with
- * miikv_workspace_init before first use; the kernels leave it re-usable. */
+ * `max_context` tokens (per-split partial softmax records).  Its contents need
+ * no initialisation; miikv_workspace_init zero-fills a buffer with a kernel
+ * (no memset node), e.g. for reproducible dumps. */
 uint64_t miikv_decode_workspace_bytes(const miikv_view* view, uint32_t q_heads, uint32_t batch,
                                       uint32_t max_context);
 miikv_status miikv_workspace_init(void* workspace, uint64_t bytes, void* stream);

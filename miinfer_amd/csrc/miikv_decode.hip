@@ -18,11 +18,13 @@
 // block.  Softmax runs in the log2 domain (scores pre-multiplied by
 // scale * log2(e)) with exp2.
 //
-// Cross-wave combine goes through LDS; cross-split combine is done by the last
-// workgroup of each (sequence, kv head) to finish (an arrival counter in the
-// caller's workspace, reset by that workgroup), so one launch produces the
-// final output.  Partial softmax state follows the reference combine
-// (gfx906/kernels/qwen3_primitives.hip:2295-2385): g = max m_s,
+// Cross-wave combine goes through LDS; each workgroup writes one partial record
+// (m, l, unnormalised O) per split into the caller's workspace, and a second,
+// wide kernel merges the splits.  Two launches on one stream need no
+// cross-workgroup synchronisation: a grid-wide arrival counter would need an
+// agent-scope release (an L2 write-back on every XCD) per workgroup, which
+// measured slower than the second launch.  The merge follows the reference
+// combine (gfx906/kernels/qwen3_primitives.hip:2295-2385): g = max m_s,
 // L = sum l_s e^{m_s-g}, out = sum acc_s e^{m_s-g} / L, 0 when L == 0,
 // gated = out * sigmoid(gate).
 #include "miikv_common.hpp"
@@ -52,7 +54,6 @@ struct DecodeArgs {
     uint32_t max_context;
     uint32_t cpw;         // chunks per wave
     uint32_t max_splits;  // == gridDim.x
-    uint32_t* counters;   // [batch][kv_heads]
     float* part;          // [batch][kv_heads][max_splits][group*(D+2)]
     float* out;
     const float* gate;
@@ -66,6 +67,11 @@ __device__ __forceinline__ float wave_max_xor_16_32(float x) {
 }
 
 __device__ __forceinline__ float exp2_safe(float x) { return exp2f(x); }  // exp2(-inf) == 0
+
+// Floats in one split's partial record: O [G*D], m [G], l [G], padded to 4.
+__host__ __device__ __forceinline__ uint32_t record_floats(uint32_t G, uint32_t D) {
+    return G * D + ((2 * G + 3) / 4) * 4;
+}
 
 template <uint32_t D, bool QF32>
 __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
@@ -89,17 +95,7 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
     if (L > a.max_context) L = a.max_context;
     const uint32_t tps = kWavesPerWg * a.cpw * kChunk;
     const uint32_t nsplit = (L + tps - 1) / tps;
-    const size_t out_row0 = (static_cast<size_t>(b) * a.q_heads + static_cast<size_t>(h) * G) * D;
-    if (L == 0) {
-        if (split == 0) {
-            for (uint32_t i = tid; i < G * D; i += blockDim.x) {
-                if (a.out) a.out[out_row0 + i] = 0.0f;
-                if (a.gated_out) a.gated_out[out_row0 + i] = 0.0f;
-            }
-        }
-        return;
-    }
-    if (split >= nsplit) return;
+    if (split >= nsplit) return;  // includes L == 0 (the combine kernel writes zeros)
 
     // ---- Q fragments (B operand of the QK MFMA): lane (g4, n) holds head n,
     // dims 32*blk + 8*g4 .. +7 of every block.
@@ -141,7 +137,11 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
 
     const uint32_t nchunks = (L + kChunk - 1) / kChunk;
     const uint32_t c_begin = (split * kWavesPerWg + wave) * a.cpw;
+#ifdef MIIKV_EXP_NO_LOOP
+    const uint32_t c_end = c_begin;
+#else
     const uint32_t c_end = min(c_begin + a.cpw, nchunks);
+#endif
     const size_t slab_bytes = static_cast<size_t>(geo.page_tokens) * D;
 
     for (uint32_t c = c_begin; c < c_end; ++c) {
@@ -256,9 +256,7 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
     float* s_m = smem;                          // [4][16]
     float* s_l = smem + 64;                     // [4][16]
     float* s_O = smem + 128;                    // [4][G][D]
-    float* s_f = s_O + kWavesPerWg * G * D;     // [64][16] split factors
-    __shared__ float s_M[16], s_L[16];
-    __shared__ uint32_t s_last;
+    __shared__ float s_M[16];
     if (g4 == 0) {
         s_m[wave * 16 + n] = m_run;
         s_l[wave * 16 + n] = l_run;
@@ -271,9 +269,11 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
     }
     __syncthreads();
 
-    const uint32_t rec = G * (D + 2);
+    // Partial record of one split: [O: G*D][m: G][l: G] padded to a multiple of 4 floats,
+    // so every record starts 16-byte aligned.
+    const uint32_t rec = record_floats(G, D);
     float* part = a.part + ((static_cast<size_t>(b) * geo.kv_heads + h) * a.max_splits) * rec;
-    float* mine = part + static_cast<size_t>(split) * rec;  // [m G][l G][O G*D]
+    float* mine = part + static_cast<size_t>(split) * rec;
     if (tid < G) {
         float M = -INFINITY;
         for (uint32_t w = 0; w < kWavesPerWg; ++w) M = fmaxf(M, s_m[w * 16 + tid]);
@@ -283,8 +283,8 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
             if (mw != -INFINITY) Ls += s_l[w * 16 + tid] * exp2_safe(mw - M);
         }
         s_M[tid] = M;
-        mine[tid] = M;
-        mine[G + tid] = Ls;
+        mine[G * D + tid] = M;
+        mine[G * D + G + tid] = Ls;
     }
     __syncthreads();
     for (uint32_t idx = tid; idx < G * D; idx += blockDim.x) {
@@ -294,72 +294,96 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
             const float mw = s_m[w * 16 + hn];
             if (mw != -INFINITY) o += s_O[w * G * D + idx] * exp2_safe(mw - s_M[hn]);
         }
-        mine[2 * G + idx] = o;
+        mine[idx] = o;
     }
 
     // ---- publish, and let the last workgroup of this (sequence, kv head) finish.
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t prev = atomicAdd(&a.counters[static_cast<size_t>(b) * geo.kv_heads + h], 1u);
-        s_last = (prev == nsplit - 1) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (s_last == 0) return;
-    __threadfence();
+}
 
-    if (tid < G) {
-        float M = -INFINITY;
-        for (uint32_t sp = 0; sp < nsplit; ++sp) M = fmaxf(M, part[static_cast<size_t>(sp) * rec + tid]);
-        float Ls = 0.0f;
-        for (uint32_t sp = 0; sp < nsplit; ++sp) {
-            const float* r = part + static_cast<size_t>(sp) * rec;
-            Ls += r[G + tid] * exp2_safe(r[tid] - M);
-        }
-        s_M[tid] = M;
-        s_L[tid] = Ls;
+
+
+// Cross-split combine.  Workgroup (sequence * kv_heads + head, element block of 64)
+// reads the partial records of every split of that (sequence, kv head): thread
+// (e4 = tid & 15, sg = tid >> 4) folds splits sg, sg+16, ... for 4 consecutive
+// elements with its own running max, so its loads are independent; the 16 split
+// groups are merged in a fixed order through LDS (deterministic result).
+template <uint32_t D>
+__global__ void __launch_bounds__(256) combine_kernel(DecodeArgs a) {
+    const uint32_t bh = blockIdx.x;
+    const uint32_t b = bh / a.g.kv_heads;
+    const uint32_t h = bh % a.g.kv_heads;
+    const uint32_t G = a.group;
+    const uint32_t GD = G * D;
+    const uint32_t e0 = blockIdx.y * 64;
+    if (e0 >= GD) return;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t e4 = tid & 15;
+    const uint32_t sg = tid >> 4;
+    const uint32_t e = e0 + e4 * 4;
+    const bool active = e < GD;
+    const uint32_t hn = active ? e / D : 0;
+    const size_t out_row0 = (static_cast<size_t>(b) * a.q_heads + static_cast<size_t>(h) * G) * D;
+
+    uint32_t L = a.len_ptr[static_cast<size_t>(b) * a.len_stride] + a.len_add;
+    if (L > a.max_context) L = a.max_context;
+    const uint32_t tps = kWavesPerWg * a.cpw * kChunk;
+    const uint32_t nsplit = (L + tps - 1) / tps;
+    const uint32_t rec = record_floats(G, D);
+    const float* part = a.part + (static_cast<size_t>(bh) * a.max_splits) * rec;
+
+    float mloc = -INFINITY;
+    float lsum = 0.0f;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 4
+    for (uint32_t sp = sg; sp < nsplit; sp += 16) {
+        const float* r = part + static_cast<size_t>(sp) * rec;
+        const float ms = r[GD + hn];
+        const float ls = r[GD + G + hn];
+        const float4 v = active ? *reinterpret_cast<const float4*>(r + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float mn = fmaxf(mloc, ms);
+        const float fo = exp2_safe(mloc - mn);  // 0 on the first split
+        const float fs = exp2_safe(ms - mn);
+        mloc = mn;
+        lsum = lsum * fo + ls * fs;
+        acc.x = acc.x * fo + v.x * fs;
+        acc.y = acc.y * fo + v.y * fs;
+        acc.z = acc.z * fo + v.z * fs;
+        acc.w = acc.w * fo + v.w * fs;
     }
+    __shared__ float4 s_acc[16][16];
+    __shared__ float s_gm[16][16];
+    __shared__ float s_gl[16][16];
+    s_acc[sg][e4] = acc;
+    s_gm[sg][e4] = mloc;
+    s_gl[sg][e4] = lsum;
     __syncthreads();
-    // Accumulate in blocks of 64 splits with the factors staged in LDS.
-    constexpr uint32_t kMaxPerThread = 16;  // G*D <= 16*256 elements over 256 threads
-    float acc[kMaxPerThread];
-    const uint32_t per = (G * D + blockDim.x - 1) / blockDim.x;
+    if (sg != 0 || !active) return;
+    float M = -INFINITY;
 #pragma unroll
-    for (uint32_t k = 0; k < kMaxPerThread; ++k) acc[k] = 0.0f;
-    for (uint32_t s0 = 0; s0 < nsplit; s0 += 64) {
-        const uint32_t sn = min(64u, nsplit - s0);
-        for (uint32_t idx = tid; idx < sn * G; idx += blockDim.x) {
-            const uint32_t sp = idx / G, hn = idx % G;
-            const float ms = part[static_cast<size_t>(s0 + sp) * rec + hn];
-            s_f[sp * 16 + hn] = exp2_safe(ms - s_M[hn]);
-        }
-        __syncthreads();
-        for (uint32_t k = 0; k < per && k < kMaxPerThread; ++k) {
-            const uint32_t idx = tid + k * blockDim.x;
-            if (idx < G * D) {
-                const uint32_t hn = idx / D;
-                float o = acc[k];
-                for (uint32_t sp = 0; sp < sn; ++sp)
-                    o += part[static_cast<size_t>(s0 + sp) * rec + 2 * G + idx] * s_f[sp * 16 + hn];
-                acc[k] = o;
-            }
-        }
-        __syncthreads();
+    for (uint32_t g = 0; g < 16; ++g) M = fmaxf(M, s_gm[g][e4]);
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float Ls = 0.0f;
+#pragma unroll
+    for (uint32_t g = 0; g < 16; ++g) {
+        const float mg = s_gm[g][e4];
+        if (mg == -INFINITY) continue;  // split group without splits
+        const float f = exp2_safe(mg - M);
+        const float4 v = s_acc[g][e4];
+        o.x += f * v.x;
+        o.y += f * v.y;
+        o.z += f * v.z;
+        o.w += f * v.w;
+        Ls += f * s_gl[g][e4];
     }
-    for (uint32_t k = 0; k < per && k < kMaxPerThread; ++k) {
-        const uint32_t idx = tid + k * blockDim.x;
-        if (idx < G * D) {
-            const uint32_t hn = idx / D;
-            const float Ls = s_L[hn];
-            const float val = Ls > 0.0f ? acc[k] / Ls : 0.0f;
-            if (a.out) a.out[out_row0 + idx] = val;
-            if (a.gate && a.gated_out) {
-                const float gv = a.gate[out_row0 + idx];
-                a.gated_out[out_row0 + idx] = val * (1.0f / (1.0f + expf(-gv)));
-            }
-        }
+    // out = acc / L, 0 when L == 0 (qwen3_primitives.hip:2349); gated = out * sigmoid(gate).
+    const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
+    const float vals[4] = {o.x * inv, o.y * inv, o.z * inv, o.w * inv};
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) {
+        const size_t oi = out_row0 + e + k;
+        if (a.out) a.out[oi] = vals[k];
+        if (a.gate && a.gated_out) a.gated_out[oi] = vals[k] * (1.0f / (1.0f + expf(-a.gate[oi])));
     }
-    if (tid == 0) a.counters[static_cast<size_t>(b) * geo.kv_heads + h] = 0u;
 }
 
 struct Plan {
@@ -381,8 +405,8 @@ Plan make_plan(const miikv_view* v, uint32_t q_heads, uint32_t batch, uint32_t m
     p.splits = static_cast<uint32_t>((static_cast<uint64_t>(max_context) + tps - 1) / tps);
     if (p.splits == 0) p.splits = 1;
     const uint64_t G = q_heads / v->kv_heads;
-    p.counter_bytes = ((static_cast<uint64_t>(batch) * v->kv_heads * 4 + 255) / 256) * 256;
-    p.part_bytes = static_cast<uint64_t>(batch) * v->kv_heads * p.splits * G * (v->head_dim + 2) * 4;
+    p.counter_bytes = 0;
+    p.part_bytes = static_cast<uint64_t>(batch) * v->kv_heads * p.splits * record_floats(G, v->head_dim) * 4;
     p.part_bytes = (p.part_bytes + 255) / 256 * 256;
     return p;
 }
@@ -438,7 +462,8 @@ extern "C" miikv_status miikv_decode_attn(const miikv_view* view, const void* q,
     if (view->layout == MIIKV_LAYOUT_CONTIGUOUS && batch != 1) return MIIKV_EINVAL;
     const Plan p = make_plan(view, q_heads, batch, max_context);
     if (workspace == nullptr || workspace_bytes < p.counter_bytes + p.part_bytes) return MIIKV_EWORKSPACE;
-    if (p.splits > 65535u || batch > 65535u) return MIIKV_EINVAL;
+    if (p.splits > 65535u || batch > 65535u || static_cast<uint64_t>(batch) * view->kv_heads > 0x7fffffffu)
+        return MIIKV_EINVAL;
 
     DecodeArgs a;
     a.g = make_geo(*view);
@@ -458,23 +483,25 @@ extern "C" miikv_status miikv_decode_attn(const miikv_view* view, const void* q,
     a.max_context = max_context;
     a.cpw = p.cpw;
     a.max_splits = p.splits;
-    a.counters = static_cast<uint32_t*>(workspace);
     a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + p.counter_bytes);
     a.out = out;
     a.gate = gate;
     a.gated_out = gated_out;
 
-    const size_t lds = (128 + kWavesPerWg * G * view->head_dim + 64 * 16) * sizeof(float);
+    const size_t lds = (128 + kWavesPerWg * G * view->head_dim) * sizeof(float);
     if (lds > 64 * 1024) return MIIKV_EUNSUPPORTED;
     const dim3 grid(p.splits, view->kv_heads, batch);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool f32 = q_dtype == MIIKV_DTYPE_F32;
+    const dim3 cgrid(batch * view->kv_heads, (G * view->head_dim + 63) / 64);
     if (view->head_dim == 128) {
         if (f32) hipLaunchKernelGGL((decode_kernel<128, true>), grid, dim3(256), lds, s, a);
         else hipLaunchKernelGGL((decode_kernel<128, false>), grid, dim3(256), lds, s, a);
+        hipLaunchKernelGGL((combine_kernel<128>), cgrid, dim3(256), 0, s, a);
     } else {
         if (f32) hipLaunchKernelGGL((decode_kernel<256, true>), grid, dim3(256), lds, s, a);
         else hipLaunchKernelGGL((decode_kernel<256, false>), grid, dim3(256), lds, s, a);
+        hipLaunchKernelGGL((combine_kernel<256>), cgrid, dim3(256), 0, s, a);
     }
     return hip_status(hipGetLastError());
 }
