@@ -29,9 +29,9 @@
  *   k_codes slab (int8), MFMA-A-operand tiling in 16-token tiles:
  *       token t = 16*T + m, dim d = 64*c + 32*e + 8*g + j  (m<16, e<2, g<4, j<8)
  *       byte offset = T*(16*head_dim) + c*1024 + g*256 + m*16 + e*8 + j
- *   v_codes slab (int8), token-contiguous per dim in 64-token chunks:
- *       token t = 64*C + 16*J + 4*G + I  (J<4, G<4, I<4)
- *       byte offset = C*(64*head_dim) + d*64 + G*16 + J*4 + I
+ *   v_codes slab (int8), token-contiguous per dim in 32-token groups:
+ *       token t = 32*H + 16*J + 4*G + I  (J<2, G<4, I<4)
+ *       byte offset = H*(32*head_dim) + d*32 + G*8 + J*4 + I
  * miikv_export_canonical() converts any token range back to row-major codes.
  */
 #ifndef MIIKV_H

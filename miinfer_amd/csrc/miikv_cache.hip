@@ -12,7 +12,7 @@ int validate_view(const miikv_view* v) {
         return MIIKV_EINVAL;
     if (v->quant_mode != MIIKV_KV_Q8_Q8) return MIIKV_EUNSUPPORTED;
     if (v->head_dim != 128 && v->head_dim != 256) return MIIKV_EUNSUPPORTED;
-    if (v->kv_heads == 0 || v->page_tokens == 0 || v->page_tokens % kChunk != 0) return MIIKV_EINVAL;
+    if (v->kv_heads == 0 || v->page_tokens == 0 || v->page_tokens % 64 != 0) return MIIKV_EINVAL;
     if (v->layout == MIIKV_LAYOUT_CONTIGUOUS) {
         if (v->num_pages != 1) return MIIKV_EINVAL;
     } else if (v->layout == MIIKV_LAYOUT_PAGED) {

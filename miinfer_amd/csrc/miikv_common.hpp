@@ -17,7 +17,7 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kWave = 64;
-constexpr uint32_t kChunk = 64;   // tokens per V chunk / per wave step
+constexpr uint32_t kChunk = 32;   // tokens per wave step (one V group, two K tiles)
 constexpr uint32_t kTile = 16;    // tokens per K tile (MFMA M/N)
 
 // Geometry of a cache view, passed by value to kernels.
@@ -32,6 +32,7 @@ struct Geo {
     uint32_t head_dim;
     uint32_t page_tokens;
     uint32_t table_stride;
+    uint32_t num_pages;
 };
 
 inline Geo make_geo(const miikv_view& v) {
@@ -46,6 +47,7 @@ inline Geo make_geo(const miikv_view& v) {
     g.head_dim = v.head_dim;
     g.page_tokens = v.page_tokens;
     g.table_stride = v.table_stride;
+    g.num_pages = v.num_pages;
     return g;
 }
 
@@ -58,6 +60,17 @@ __device__ __forceinline__ size_t slab_of(const Geo& g, uint32_t seq, uint32_t p
     return static_cast<size_t>(page) * g.kv_heads + head;
 }
 
+// As slab_of, with the page index clamped into [0, num_pages): for speculative
+// loads whose table entry may not be set yet (the data is discarded).
+__device__ __forceinline__ size_t slab_of_clamped(const Geo& g, uint32_t seq, uint32_t pos, uint32_t head) {
+    uint32_t page = 0;
+    if (g.layout == MIIKV_LAYOUT_PAGED) {
+        page = static_cast<uint32_t>(g.table[static_cast<size_t>(seq) * g.table_stride + pos / g.page_tokens]);
+        page = min(page, g.num_pages - 1);
+    }
+    return static_cast<size_t>(page) * g.kv_heads + head;
+}
+
 // Byte offset of (token tp within the slab, dim d) in a K-code slab.
 __device__ __forceinline__ uint32_t k_code_offset(uint32_t tp, uint32_t d, uint32_t D) {
     const uint32_t T = tp >> 4, m = tp & 15;
@@ -65,10 +78,11 @@ __device__ __forceinline__ uint32_t k_code_offset(uint32_t tp, uint32_t d, uint3
     return T * (16 * D) + c * 1024 + gq * 256 + m * 16 + e * 8 + j;
 }
 
-// Byte offset of (token tp within the slab, dim d) in a V-code slab.
+// Byte offset of (token tp within the slab, dim d) in a V-code slab: 32-token
+// groups, token-contiguous per dim, tokens ordered (G, J, I) for t = 16J + 4G + I.
 __device__ __forceinline__ uint32_t v_code_offset(uint32_t tp, uint32_t d, uint32_t D) {
-    const uint32_t C = tp >> 6, J = (tp >> 4) & 3, G = (tp >> 2) & 3, I = tp & 3;
-    return C * (64 * D) + d * 64 + G * 16 + J * 4 + I;
+    const uint32_t H = tp >> 5, J = (tp >> 4) & 1, G = (tp >> 2) & 3, I = tp & 3;
+    return H * (32 * D) + d * 32 + G * 8 + J * 4 + I;
 }
 
 // q8_0 quantization of 16 values held by this lane; its partner lane (lane ^ 1)
@@ -129,6 +143,25 @@ __device__ __forceinline__ half4 codes4_to_half4(uint32_t w) {
     half4 r;
     r[0] = a[0]; r[1] = a[1]; r[2] = b[0]; r[3] = b[1];
     return r;
+}
+
+// Biased variants: four codes -> fp16 (code + 1152), exact, without the subtraction.
+// Callers remove 1152 * (sum of the other operand) themselves.
+__device__ __forceinline__ half4 codes4_to_half4_biased(uint32_t w) {
+    const uint32_t u = w ^ 0x80808080u;
+    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    return __builtin_bit_cast(half4, make_uint2(a, b));
+}
+
+__device__ __forceinline__ half8 codes8_to_half8_biased(uint32_t w0, uint32_t w1) {
+    const uint32_t u0 = w0 ^ 0x80808080u;
+    const uint32_t u1 = w1 ^ 0x80808080u;
+    const uint4 r = make_uint4(__builtin_amdgcn_perm(0x64646464u, u0, 0x04010400u),
+                               __builtin_amdgcn_perm(0x64646464u, u0, 0x04030402u),
+                               __builtin_amdgcn_perm(0x64646464u, u1, 0x04010400u),
+                               __builtin_amdgcn_perm(0x64646464u, u1, 0x04030402u));
+    return __builtin_bit_cast(half8, r);
 }
 
 __device__ __forceinline__ float4v mfma_16x16x32(half8 a, half8 b, float4v c) {

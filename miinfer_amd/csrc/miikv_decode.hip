@@ -30,6 +30,8 @@
 #include "miikv_common.hpp"
 
 #include <cmath>
+#include <cstdlib>
+#include <type_traits>
 
 namespace miikv {
 
@@ -38,9 +40,24 @@ uint64_t view_seq_capacity(const miikv_view* v);
 
 namespace {
 
-constexpr uint32_t kWavesPerWg = 4;
+#ifndef MIIKV_WPW
+#define MIIKV_WPW 4
+#endif
+// Pipeline depth (32-token steps held in registers) and the occupancy it is tuned for.
+#ifndef MIIKV_RING_D128
+#define MIIKV_RING_D128 3
+#endif
+#ifndef MIIKV_WPE_D128
+#define MIIKV_WPE_D128 2
+#endif
+#ifndef MIIKV_RING_D256
+#define MIIKV_RING_D256 2
+#endif
+constexpr uint32_t kWavesPerWg = MIIKV_WPW;
 constexpr uint32_t kTargetWaves = 256 * 8;  // 256 CUs x 8 resident waves
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kCodeBias = 1152.0f;  // codes enter the MFMA as fp16(code + 1152)
+constexpr float kRescaleSlack = 6.0f;  // log2 units: p <= 64, and 64 * (65504/127) < 65504
 
 struct DecodeArgs {
     Geo g;
@@ -60,6 +77,19 @@ struct DecodeArgs {
     float* gated_out;
 };
 
+// Streaming loads of cache codes: each byte is read once per launch, so they are
+// issued nontemporal (measured ~5% faster than cached loads at 32k context).
+__device__ __forceinline__ uint4 load16(const int8_t* p) {
+    typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+    const u4v t = __builtin_nontemporal_load(reinterpret_cast<const u4v*>(p));
+    return make_uint4(t.x, t.y, t.z, t.w);
+}
+__device__ __forceinline__ uint2 load8(const int8_t* p) {
+    typedef unsigned int u2v __attribute__((ext_vector_type(2)));
+    const u2v t = __builtin_nontemporal_load(reinterpret_cast<const u2v*>(p));
+    return make_uint2(t.x, t.y);
+}
+
 __device__ __forceinline__ float wave_max_xor_16_32(float x) {
     x = fmaxf(x, __shfl_xor(x, 16, 64));
     x = fmaxf(x, __shfl_xor(x, 32, 64));
@@ -67,6 +97,13 @@ __device__ __forceinline__ float wave_max_xor_16_32(float x) {
 }
 
 __device__ __forceinline__ float exp2_safe(float x) { return exp2f(x); }  // exp2(-inf) == 0
+// Raw v_exp_f32: no denormal range fix-up (results below 2^-126 flush to 0, which
+// only drops probabilities that are already negligible); exp2(-inf) == 0.
+#ifdef MIIKV_EXP_EXP2F
+__device__ __forceinline__ float fast_exp2(float x) { return exp2f(x); }
+#else
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+#endif
 
 // Floats in one split's partial record: O [G*D], m [G], l [G], padded to 4.
 __host__ __device__ __forceinline__ uint32_t record_floats(uint32_t G, uint32_t D) {
@@ -74,10 +111,12 @@ __host__ __device__ __forceinline__ uint32_t record_floats(uint32_t G, uint32_t 
 }
 
 template <uint32_t D, bool QF32>
-__global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? MIIKV_WPE_D128 : 1)))
+decode_kernel(DecodeArgs a) {
     constexpr uint32_t NB = D / 32;   // q8_0 blocks per row
     constexpr uint32_t NC = D / 64;   // 16-byte K loads per tile row group
     constexpr uint32_t NM = D / 16;   // V M-tiles (16 dims each)
+    using ScaleVec = typename std::conditional<NB == 4, uint32_t, uint2>::type;  // NB/2 fp16 scales
     extern __shared__ float smem[];
 
     const uint32_t split = blockIdx.x;
@@ -91,6 +130,56 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
     const uint32_t G = a.group;
     const Geo& geo = a.g;
 
+    // Steps this wave may own, from the host bound alone: the first loads are issued
+    // before the context length arrives from memory.
+    const uint32_t c_begin = (split * kWavesPerWg + wave) * a.cpw;
+    const uint32_t nsteps_max = (a.max_context + kChunk - 1) / kChunk;
+    const uint32_t c_end_max = min(c_begin + a.cpw, nsteps_max);
+    const size_t slab_bytes = static_cast<size_t>(geo.page_tokens) * D;
+
+    // Registers of one 32-token step: two K tiles, one V group, their scales.
+    struct Step {
+        uint4 k[2][NC];
+        uint2 v[NM];
+        ScaleVec ks, vs;
+    };
+
+    // Load cursor: the page (slab) is looked up once per page, not per step.  Page
+    // indices are clamped into the pool, so a speculative load past the sequence end
+    // reads a valid (unused) page rather than whatever an unset table entry holds.
+    uint32_t ld_tok = c_begin * kChunk;
+    uint32_t ld_tp = ld_tok % geo.page_tokens;
+    size_t ld_slab = 0;
+    if (c_begin < c_end_max) ld_slab = slab_of_clamped(geo, b, ld_tok, h);
+    auto load_step = [&](Step& st) {
+        if (ld_tp == geo.page_tokens) {
+            ld_tp = 0;
+            ld_slab = slab_of_clamped(geo, b, ld_tok, h);
+        }
+        const int8_t* kb = geo.k_codes + ld_slab * slab_bytes + static_cast<size_t>(ld_tp) * D;
+        const int8_t* vb = geo.v_codes + ld_slab * slab_bytes + static_cast<size_t>(ld_tp) * D;
+        const size_t sc0 = (ld_slab * geo.page_tokens + ld_tp) * NB;
+#pragma unroll
+        for (uint32_t J = 0; J < 2; ++J)
+#pragma unroll
+            for (uint32_t cc = 0; cc < NC; ++cc)
+                st.k[J][cc] = load16(kb + J * 16 * D + cc * 1024 + g4 * 256 + n * 16);
+#pragma unroll
+        for (uint32_t mt = 0; mt < NM; ++mt)
+            st.v[mt] = load8(vb + (16 * mt + n) * 32 + g4 * 8);
+        st.ks = *reinterpret_cast<const ScaleVec*>(geo.k_scales + sc0 + lane * (NB / 2));
+        st.vs = *reinterpret_cast<const ScaleVec*>(geo.v_scales + sc0 + lane * (NB / 2));
+        ld_tok += kChunk;
+        ld_tp += kChunk;
+    };
+
+    // Ring of kRing step buffers; the first kRing-1 are loaded before L is known.
+    constexpr uint32_t kRing = (D == 128) ? MIIKV_RING_D128 : MIIKV_RING_D256;
+    Step S[kRing];
+#pragma unroll
+    for (uint32_t r = 0; r + 1 < kRing; ++r)
+        if (c_begin + r < c_end_max) load_step(S[r]);
+
     uint32_t L = a.len_ptr[static_cast<size_t>(b) * a.len_stride] + a.len_add;
     if (L > a.max_context) L = a.max_context;
     const uint32_t tps = kWavesPerWg * a.cpw * kChunk;
@@ -98,15 +187,19 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
     if (split >= nsplit) return;  // includes L == 0 (the combine kernel writes zeros)
 
     // ---- Q fragments (B operand of the QK MFMA): lane (g4, n) holds head n,
-    // dims 32*blk + 8*g4 .. +7 of every block.
+    // dims 32*blk + 8*g4 .. +7 of every block.  Codes enter the MFMA as fp16
+    // (code + 1152) (see codes4_to_half_biased), so each block's dot carries an
+    // extra 1152 * sum(q_blk); the accumulator starts at minus that amount.
     half8 qf[NB];
     half8 ql[QF32 ? NB : 1];
+    float kbias[NB];
     {
         const size_t qrow = (static_cast<size_t>(b) * a.q_heads + static_cast<size_t>(h) * G + n) * D;
 #pragma unroll
         for (uint32_t blk = 0; blk < NB; ++blk) {
             half8 v = {};
             half8 lo = {};
+            float qs = 0.0f;
             if (n < G) {
                 if (QF32) {
                     const float* qp = static_cast<const float*>(a.q) + qrow + blk * 32 + g4 * 8;
@@ -118,12 +211,18 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
                         const _Float16 hi = static_cast<_Float16>(xs[i]);
                         v[i] = hi;
                         lo[i] = static_cast<_Float16>(xs[i] - static_cast<float>(hi));
+                        qs += static_cast<float>(hi) + static_cast<float>(lo[i]);
                     }
                 } else {
                     const uint16_t* qp = static_cast<const uint16_t*>(a.q) + qrow + blk * 32 + g4 * 8;
                     v = __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(qp));
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) qs += static_cast<float>(v[i]);
                 }
             }
+            qs += __shfl_xor(qs, 16, 64);
+            qs += __shfl_xor(qs, 32, 64);
+            kbias[blk] = kCodeBias * qs;
             qf[blk] = v;
             if (QF32) ql[QF32 ? blk : 0] = lo;
         }
@@ -132,62 +231,72 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
     float m_run = -INFINITY;
     float l_run = 0.0f;
     float4v O[NM];
+    float4v vbias[NB];  // column sums of the PV B operand per block (removes the V code bias)
 #pragma unroll
     for (uint32_t mt = 0; mt < NM; ++mt) O[mt] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (uint32_t blk = 0; blk < NB; ++blk) vbias[blk] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+    const half4 ones = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
 
-    const uint32_t nchunks = (L + kChunk - 1) / kChunk;
-    const uint32_t c_begin = (split * kWavesPerWg + wave) * a.cpw;
+    const uint32_t nsteps = (L + kChunk - 1) / kChunk;
 #ifdef MIIKV_EXP_NO_LOOP
     const uint32_t c_end = c_begin;
 #else
-    const uint32_t c_end = min(c_begin + a.cpw, nchunks);
+    const uint32_t c_end = min(c_end_max, nsteps);
 #endif
-    const size_t slab_bytes = static_cast<size_t>(geo.page_tokens) * D;
+    // Per-wave LDS staging of one step's scales: [K: 32*NB][V: 32*NB] fp16.  Each lane
+    // loads NB/2 scales (no redundancy) and re-reads the 4*NB it needs from LDS.
+    uint16_t* s_sc = reinterpret_cast<uint16_t*>(smem + 32 * kWavesPerWg + kWavesPerWg * G * D) + wave * (2 * kChunk * NB);
 
-    for (uint32_t c = c_begin; c < c_end; ++c) {
+    // A step that reaches past L (only the sequence's last) is masked under a
+    // wave-uniform branch: its scores go to -inf and its V scales to 0 (the memory
+    // past L may hold anything, including non-finite scales).
+    auto compute_step = [&](uint32_t c, const Step& st) {
         const uint32_t tok0 = c * kChunk;
-        const size_t slab = slab_of(geo, b, tok0, h);
-        const uint32_t tp0 = tok0 % geo.page_tokens;
-        const int8_t* kb = geo.k_codes + slab * slab_bytes + static_cast<size_t>(tp0) * D;
-        const int8_t* vb = geo.v_codes + slab * slab_bytes + static_cast<size_t>(tp0) * D;
-        const uint16_t* ksb = geo.k_scales + (slab * geo.page_tokens + tp0) * NB;
-        const uint16_t* vsb = geo.v_scales + (slab * geo.page_tokens + tp0) * NB;
+#ifdef MIIKV_EXP_NO_COMPUTE
+        {
+            uint32_t x = reinterpret_cast<const uint32_t*>(&st.ks)[0] ^ reinterpret_cast<const uint32_t*>(&st.vs)[0];
+#pragma unroll
+            for (uint32_t J = 0; J < 2; ++J)
+#pragma unroll
+                for (uint32_t cc = 0; cc < NC; ++cc) x ^= st.k[J][cc].x ^ st.k[J][cc].y ^ st.k[J][cc].z ^ st.k[J][cc].w;
+#pragma unroll
+            for (uint32_t mt = 0; mt < NM; ++mt) x ^= st.v[mt].x ^ st.v[mt].y;
+            l_run += static_cast<float>(x & 1u);
+            m_run = 0.0f;
+            return;
+        }
+#endif
+        const bool tail = tok0 + kChunk > L;
+        *reinterpret_cast<ScaleVec*>(s_sc + lane * (NB / 2)) = st.ks;
+        ScaleVec vsv = st.vs;
+        if (tail && tok0 + lane / 2 >= L) vsv = ScaleVec{};
+        *reinterpret_cast<ScaleVec*>(s_sc + kChunk * NB + lane * (NB / 2)) = vsv;
 
-        // Issue all loads of the chunk up front.
-        uint4 kw[4][NC];
+        // ---- scores S^T[token][head], one MFMA per q8_0 block, block scale in fp32
+        float s[2][4];
 #pragma unroll
-        for (uint32_t J = 0; J < 4; ++J)
+        for (uint32_t J = 0; J < 2; ++J) {
+            uint4 ksw[NB / 2];  // scales of tokens 16J + 4*g4 + i, all blocks
 #pragma unroll
-            for (uint32_t cc = 0; cc < NC; ++cc)
-                kw[J][cc] = *reinterpret_cast<const uint4*>(kb + J * 16 * D + cc * 1024 + g4 * 256 + n * 16);
-        uint4 vw[NM];
-#pragma unroll
-        for (uint32_t mt = 0; mt < NM; ++mt)
-            vw[mt] = *reinterpret_cast<const uint4*>(vb + (16 * mt + n) * 64 + g4 * 16);
-        // Scales of tokens 16J + 4*g4 + i (i < 4), all blocks: 4*NB halves.
-        uint4 ksw[4][NB / 2];
-        uint4 vsw[4][NB / 2];
-#pragma unroll
-        for (uint32_t J = 0; J < 4; ++J)
-#pragma unroll
-            for (uint32_t w = 0; w < NB / 2; ++w) {
-                ksw[J][w] = *reinterpret_cast<const uint4*>(ksb + (16 * J + 4 * g4) * NB + w * 8);
-                vsw[J][w] = *reinterpret_cast<const uint4*>(vsb + (16 * J + 4 * g4) * NB + w * 8);
-            }
-
-        // ---- scores
-        float s[4][4];
-#pragma unroll
-        for (uint32_t J = 0; J < 4; ++J) {
-            const uint16_t* ks16 = reinterpret_cast<const uint16_t*>(&ksw[J][0]);
+            for (uint32_t w = 0; w < NB / 2; ++w)
+                ksw[w] = *reinterpret_cast<const uint4*>(s_sc + (16 * J + 4 * g4) * NB + w * 8);
+            const uint16_t* ks16 = reinterpret_cast<const uint16_t*>(&ksw[0]);
             float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (uint32_t cc = 0; cc < NC; ++cc) {
-                const uint4 w = kw[J][cc];
-                const half8 a0 = codes8_to_half8(w.x, w.y);  // block 2cc
-                const half8 a1 = codes8_to_half8(w.z, w.w);  // block 2cc+1
-                float4v c0 = mfma_16x16x32(a0, qf[2 * cc], float4v{0.0f, 0.0f, 0.0f, 0.0f});
-                float4v c1 = mfma_16x16x32(a1, qf[2 * cc + 1], float4v{0.0f, 0.0f, 0.0f, 0.0f});
+                const uint4 w = st.k[J][cc];
+#ifdef MIIKV_EXP_NO_KBIAS
+                const half8 a0 = codes8_to_half8(w.x, w.y);
+                const half8 a1 = codes8_to_half8(w.z, w.w);
+                const float b0 = 0.0f, b1 = 0.0f;
+#else
+                const half8 a0 = codes8_to_half8_biased(w.x, w.y);  // block 2cc
+                const half8 a1 = codes8_to_half8_biased(w.z, w.w);  // block 2cc+1
+                const float b0 = -kbias[2 * cc], b1 = -kbias[2 * cc + 1];
+#endif
+                float4v c0 = mfma_16x16x32(a0, qf[2 * cc], float4v{b0, b0, b0, b0});
+                float4v c1 = mfma_16x16x32(a1, qf[2 * cc + 1], float4v{b1, b1, b1, b1});
                 if (QF32) {
                     c0 = mfma_16x16x32(a0, ql[QF32 ? 2 * cc : 0], c0);
                     c1 = mfma_16x16x32(a1, ql[QF32 ? 2 * cc + 1 : 0], c1);
@@ -200,62 +309,99 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
             }
 #pragma unroll
             for (uint32_t i = 0; i < 4; ++i) {
-                const bool valid = tok0 + 16 * J + 4 * g4 + i < L;
-                s[J][i] = valid ? acc[i] * a.scale_log2 : -INFINITY;
+                s[J][i] = acc[i] * a.scale_log2;
             }
         }
 
-        // ---- online softmax (per head n; the 4 lane groups share m)
+        if (tail) {
+#pragma unroll
+            for (uint32_t J = 0; J < 2; ++J)
+#pragma unroll
+                for (uint32_t i = 0; i < 4; ++i)
+                    if (tok0 + 16 * J + 4 * g4 + i >= L) s[J][i] = -INFINITY;
+        }
+
+        // ---- online softmax with a lazy running max: the accumulators are rescaled only
+        // when a column's step max exceeds its running max by more than kRescaleSlack
+        // (log2 units), so p <= 2^kRescaleSlack and p * scale stays inside fp16 range.
         float cmax = s[0][0];
 #pragma unroll
-        for (uint32_t J = 0; J < 4; ++J)
+        for (uint32_t J = 0; J < 2; ++J)
 #pragma unroll
             for (uint32_t i = 0; i < 4; ++i) cmax = fmaxf(cmax, s[J][i]);
         cmax = wave_max_xor_16_32(cmax);
-        const float m_new = fmaxf(m_run, cmax);
-        const float alpha = exp2_safe(m_run - m_new);
-        m_run = m_new;
+        const bool grow = cmax > m_run + kRescaleSlack;
+        if (__any(grow)) {
+            const float m_new = grow ? cmax : m_run;
+            const float alpha = fast_exp2(m_run - m_new);
+            m_run = m_new;
+            l_run *= alpha;
+#pragma unroll
+            for (uint32_t mt = 0; mt < NM; ++mt) O[mt] *= alpha;
+#pragma unroll
+            for (uint32_t blk = 0; blk < NB; ++blk) vbias[blk] *= alpha;
+        }
         float psum = 0.0f;
 #pragma unroll
-        for (uint32_t J = 0; J < 4; ++J)
+        for (uint32_t J = 0; J < 2; ++J)
 #pragma unroll
             for (uint32_t i = 0; i < 4; ++i) {
-                s[J][i] = exp2_safe(s[J][i] - m_new);
+                s[J][i] = fast_exp2(s[J][i] - m_run);
                 psum += s[J][i];
             }
-        l_run = l_run * alpha + psum;
-#pragma unroll
-        for (uint32_t mt = 0; mt < NM; ++mt) O[mt] *= alpha;
+        l_run += psum;
 
-        // ---- O^T += V^T * (P^T scaled per block)
+        // ---- O^T += V^T * (P^T scaled per block); V codes enter as (code + 1152), the
+        // bias is removed at the end with the column sums accumulated in vbias.
 #pragma unroll
-        for (uint32_t J = 0; J < 4; ++J) {
-            const uint16_t* vs16 = reinterpret_cast<const uint16_t*>(&vsw[J][0]);
+        for (uint32_t J = 0; J < 2; ++J) {
+            uint4 vsw[NB / 2];
+#pragma unroll
+            for (uint32_t w = 0; w < NB / 2; ++w)
+                vsw[w] = *reinterpret_cast<const uint4*>(s_sc + kChunk * NB + (16 * J + 4 * g4) * NB + w * 8);
+            const uint16_t* vs16 = reinterpret_cast<const uint16_t*>(&vsw[0]);
 #pragma unroll
             for (uint32_t blk = 0; blk < NB; ++blk) {
                 half4 pb;
 #pragma unroll
                 for (uint32_t i = 0; i < 4; ++i) {
-                    const bool valid = tok0 + 16 * J + 4 * g4 + i < L;
-                    const float w = s[J][i] * f16_bits_to_f32(vs16[i * NB + blk]);
-                    pb[i] = static_cast<_Float16>(valid ? w : 0.0f);
+                    pb[i] = static_cast<_Float16>(s[J][i] * f16_bits_to_f32(vs16[i * NB + blk]));
                 }
 #pragma unroll
                 for (uint32_t sub = 0; sub < 2; ++sub) {
                     const uint32_t mt = 2 * blk + sub;
-                    const uint32_t word = (J == 0) ? vw[mt].x : (J == 1) ? vw[mt].y : (J == 2) ? vw[mt].z : vw[mt].w;
+                    const uint32_t word = J == 0 ? st.v[mt].x : st.v[mt].y;
+#ifdef MIIKV_EXP_NO_VBIAS
                     O[mt] = mfma_16x16x16(codes4_to_half4(word), pb, O[mt]);
                 }
+#else
+                    O[mt] = mfma_16x16x16(codes4_to_half4_biased(word), pb, O[mt]);
+                }
+                vbias[blk] = mfma_16x16x16(ones, pb, vbias[blk]);
+#endif
             }
         }
+    };
+
+    // Software pipeline over [c_begin, c_end): while step c computes, the loads of
+    // steps c+1 .. c+kRing-1 are in flight (fully unrolled so S[] stays in registers).
+    for (uint32_t c = c_begin; c < c_end; c += kRing) {
+#pragma unroll
+        for (uint32_t r = 0; r < kRing; ++r) {
+            if (c + r >= c_end) break;
+            if (c + r + kRing - 1 < c_end) load_step(S[(r + kRing - 1) % kRing]);
+            compute_step(c + r, S[r]);
+        }
     }
+#pragma unroll
+    for (uint32_t mt = 0; mt < NM; ++mt) O[mt] -= kCodeBias * vbias[mt / 2];
 
     // ---- wave-level sums, then cross-wave combine in LDS.
     l_run += __shfl_xor(l_run, 16, 64);
     l_run += __shfl_xor(l_run, 32, 64);
-    float* s_m = smem;                          // [4][16]
-    float* s_l = smem + 64;                     // [4][16]
-    float* s_O = smem + 128;                    // [4][G][D]
+    float* s_m = smem;                          // [waves][16]
+    float* s_l = smem + 16 * kWavesPerWg;       // [waves][16]
+    float* s_O = smem + 32 * kWavesPerWg;       // [waves][G][D]
     __shared__ float s_M[16];
     if (g4 == 0) {
         s_m[wave * 16 + n] = m_run;
@@ -324,31 +470,53 @@ __global__ void __launch_bounds__(256) combine_kernel(DecodeArgs a) {
     const uint32_t hn = active ? e / D : 0;
     const size_t out_row0 = (static_cast<size_t>(b) * a.q_heads + static_cast<size_t>(h) * G) * D;
 
+    const uint32_t rec = record_floats(G, D);
+    const float* part = a.part + (static_cast<size_t>(bh) * a.max_splits) * rec;
+
+    // The first kSpec records of this thread are fetched before the context length
+    // (and with it the split count) arrives; records past the count are ignored.
+    constexpr uint32_t kSpec = 4;
+    float ms[kSpec], ls[kSpec];
+    float4 vv[kSpec];
+#pragma unroll
+    for (uint32_t j = 0; j < kSpec; ++j) {
+        const uint32_t sp = sg + 16 * j;
+        ms[j] = -INFINITY;
+        ls[j] = 0.0f;
+        vv[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (sp < a.max_splits) {
+            const float* r = part + static_cast<size_t>(sp) * rec;
+            ms[j] = r[GD + hn];
+            ls[j] = r[GD + G + hn];
+            if (active) vv[j] = *reinterpret_cast<const float4*>(r + e);
+        }
+    }
     uint32_t L = a.len_ptr[static_cast<size_t>(b) * a.len_stride] + a.len_add;
     if (L > a.max_context) L = a.max_context;
     const uint32_t tps = kWavesPerWg * a.cpw * kChunk;
     const uint32_t nsplit = (L + tps - 1) / tps;
-    const uint32_t rec = record_floats(G, D);
-    const float* part = a.part + (static_cast<size_t>(bh) * a.max_splits) * rec;
 
     float mloc = -INFINITY;
     float lsum = 0.0f;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll 4
-    for (uint32_t sp = sg; sp < nsplit; sp += 16) {
-        const float* r = part + static_cast<size_t>(sp) * rec;
-        const float ms = r[GD + hn];
-        const float ls = r[GD + G + hn];
-        const float4 v = active ? *reinterpret_cast<const float4*>(r + e) : make_float4(0.f, 0.f, 0.f, 0.f);
-        const float mn = fmaxf(mloc, ms);
+    auto merge = [&](float m_s, float l_s, float4 v) {
+        const float mn = fmaxf(mloc, m_s);
         const float fo = exp2_safe(mloc - mn);  // 0 on the first split
-        const float fs = exp2_safe(ms - mn);
+        const float fs = exp2_safe(m_s - mn);
         mloc = mn;
-        lsum = lsum * fo + ls * fs;
+        lsum = lsum * fo + l_s * fs;
         acc.x = acc.x * fo + v.x * fs;
         acc.y = acc.y * fo + v.y * fs;
         acc.z = acc.z * fo + v.z * fs;
         acc.w = acc.w * fo + v.w * fs;
+    };
+#pragma unroll
+    for (uint32_t j = 0; j < kSpec; ++j)
+        if (sg + 16 * j < nsplit) merge(ms[j], ls[j], vv[j]);
+    for (uint32_t sp = sg + 16 * kSpec; sp < nsplit; sp += 16) {
+        const float* r = part + static_cast<size_t>(sp) * rec;
+        merge(r[GD + hn], r[GD + G + hn],
+              active ? *reinterpret_cast<const float4*>(r + e) : make_float4(0.f, 0.f, 0.f, 0.f));
     }
     __shared__ float4 s_acc[16][16];
     __shared__ float s_gm[16][16];
@@ -398,6 +566,14 @@ Plan make_plan(const miikv_view* v, uint32_t q_heads, uint32_t batch, uint32_t m
     const uint64_t chunks = (static_cast<uint64_t>(max_context) + kChunk - 1) / kChunk;
     const uint64_t waves = chunks * v->kv_heads * batch;
     uint64_t cpw = (waves + kTargetWaves - 1) / kTargetWaves;
+    // MIIKV_DECODE_STEPS_PER_WAVE fixes the 32-token steps per wave (split size =
+    // 4 waves x steps x 32 tokens), a tuning override in the spirit of the
+    // reference's MIINFER_ATTENTION_SPLITS (qwen3_primitives.hip:5229-5245).
+    static const uint64_t fixed_cpw = [] {
+        const char* e = std::getenv("MIIKV_DECODE_STEPS_PER_WAVE");
+        return e ? std::strtoull(e, nullptr, 10) : 0ull;
+    }();
+    if (fixed_cpw != 0) cpw = fixed_cpw;
     if (cpw < 1) cpw = 1;
     if (cpw > 64) cpw = 64;
     p.cpw = static_cast<uint32_t>(cpw);
@@ -488,19 +664,20 @@ extern "C" miikv_status miikv_decode_attn(const miikv_view* view, const void* q,
     a.gate = gate;
     a.gated_out = gated_out;
 
-    const size_t lds = (128 + kWavesPerWg * G * view->head_dim) * sizeof(float);
+    const size_t lds = (32 * kWavesPerWg + kWavesPerWg * G * view->head_dim) * sizeof(float) +
+                       kWavesPerWg * 2 * kChunk * (view->head_dim / 32) * sizeof(uint16_t);
     if (lds > 64 * 1024) return MIIKV_EUNSUPPORTED;
     const dim3 grid(p.splits, view->kv_heads, batch);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool f32 = q_dtype == MIIKV_DTYPE_F32;
     const dim3 cgrid(batch * view->kv_heads, (G * view->head_dim + 63) / 64);
     if (view->head_dim == 128) {
-        if (f32) hipLaunchKernelGGL((decode_kernel<128, true>), grid, dim3(256), lds, s, a);
-        else hipLaunchKernelGGL((decode_kernel<128, false>), grid, dim3(256), lds, s, a);
+        if (f32) hipLaunchKernelGGL((decode_kernel<128, true>), grid, dim3(64 * kWavesPerWg), lds, s, a);
+        else hipLaunchKernelGGL((decode_kernel<128, false>), grid, dim3(64 * kWavesPerWg), lds, s, a);
         hipLaunchKernelGGL((combine_kernel<128>), cgrid, dim3(256), 0, s, a);
     } else {
-        if (f32) hipLaunchKernelGGL((decode_kernel<256, true>), grid, dim3(256), lds, s, a);
-        else hipLaunchKernelGGL((decode_kernel<256, false>), grid, dim3(256), lds, s, a);
+        if (f32) hipLaunchKernelGGL((decode_kernel<256, true>), grid, dim3(64 * kWavesPerWg), lds, s, a);
+        else hipLaunchKernelGGL((decode_kernel<256, false>), grid, dim3(64 * kWavesPerWg), lds, s, a);
         hipLaunchKernelGGL((combine_kernel<256>), cgrid, dim3(256), 0, s, a);
     }
     return hip_status(hipGetLastError());
