@@ -72,6 +72,71 @@ def cpu_baseline(ctx_cpu: int = 32768) -> dict:
     }
 
 
+def calibrate_copy(dev) -> int:
+    """A plain 256 MiB device-to-device copy through miikv_copy_segments: its
+    FETCH_SIZE / WRITE_SIZE under rocprofv3 --pmc give the counter scale factor."""
+    import torch
+
+    import miinfer_amd as m
+    n = 256 << 20
+    src = torch.ones(n, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        m.copy_segments([(dst.data_ptr(), src.data_ptr(), n)], device=dev)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy_segments_kernel", "bytes_read": n, "bytes_written": n}))
+    return 0
+
+
+def stream_read_ceiling(dev, span_bytes: int, spans: int = 8, reps: int = 40) -> dict:
+    """Cold single-pass read of `span_bytes` (rotating over `spans` buffers so the
+    256 MB Infinity Cache does not serve it): the practical per-launch ceiling a
+    kernel streaming the same bytes can reach on this device."""
+    import ctypes
+
+    import torch
+
+    from miinfer_amd import _lib
+    blocks = 2048
+    span = span_bytes // (16 * blocks) * (16 * blocks)
+    buf = torch.ones(span * spans, dtype=torch.uint8, device=dev)
+    sink = torch.empty(blocks, dtype=torch.int32, device=dev)
+    lib = _lib.lib()
+    times = []
+    s = torch.cuda.current_stream()
+    for it in range(reps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        st = lib.miikv_stream_read(ctypes.c_void_p(buf.data_ptr() + (it % spans) * span), span,
+                                   ctypes.c_void_p(sink.data_ptr()), blocks,
+                                   ctypes.c_void_p(s.cuda_stream))
+        e1.record(s)
+        e1.synchronize()
+        if st:
+            raise RuntimeError(f"stream probe failed: {st}")
+        if it >= 8:
+            times.append(e0.elapsed_time(e1) * 1e3)
+    times.sort()
+    us = times[len(times) // 2]
+    del buf
+    return {"bytes": span, "median_us": round(us, 2), "GBs": round(span / (us * 1e-6) / 1e9, 1),
+            "note": "miikv_stream_read, 2048x256 threads, 16 B nontemporal loads, cold "
+                    "(rotating 8 spans), one launch per event pair"}
+
+
+def traffic_from_profile():
+    """HBM bytes per decode launch measured with rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, scaled by the copy calibration), from the committed summary."""
+    path = os.path.join(ROOT, "profiles", "decode_attn_c2_32k_pmc.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -81,6 +146,8 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only a 256 MiB device copy (known bytes) to calibrate PMC counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this path runs on a single MI355X "
@@ -93,6 +160,8 @@ def main() -> int:
     from miinfer_amd import _lib
 
     dev = torch.device("cuda:0")
+    if args.calibrate_copy:
+        return calibrate_copy(dev)
     ctx, nl = args.context, args.layers
     torch.manual_seed(0)
     caches = []
@@ -215,12 +284,14 @@ def main() -> int:
                                "append 1 row per kv head then attend",
                    "context": ctx, "layers_rotated": nl, "graph": use_graph,
                    "wall_s_timed": round(wall, 3)},
-        "roofline": {"bound": "hbm", "kernel": "decode_kernel<128,false>",
+        "roofline": {"bound": "hbm",
+                     "kernel": "miikv_decode_attn = decode_kernel<128,false> + combine_kernel<128>",
                      "achieved": round(dec_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(dec_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(dec_gbs / PEAK_HBM_GBS, 4), "traffic": traffic_from_profile(),
                      "algorithmic_bytes_per_launch": decode_bytes(ctx),
                      "avg_launch_us": round(us_dec, 3)},
     }
+    line["roofline"]["stream_read_ceiling"] = stream_read_ceiling(dev, decode_bytes(ctx))
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)

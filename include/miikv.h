@@ -206,6 +206,15 @@ miikv_status miikv_copy_segments(const miikv_segment* d_segments, uint32_t n, vo
 miikv_status miikv_clone_state(void* const* d_dsts, const void* src, uint64_t bytes, uint32_t n,
                                void* stream);
 
+/* ---- measurement probe --------------------------------------------------- */
+
+/* Read `bytes` from src once with 16-byte nontemporal loads over `blocks`
+ * workgroups of 256 threads (bytes must be a multiple of 16*blocks), writing
+ * one fold word per workgroup to sink[blocks].  A streaming-read ceiling for
+ * the roofline of the decode kernels; no reference counterpart. */
+miikv_status miikv_stream_read(const void* src, uint64_t bytes, uint32_t* sink, uint32_t blocks,
+                               void* stream);
+
 #ifdef __cplusplus
 }
 #endif

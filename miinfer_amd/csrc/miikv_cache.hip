@@ -242,6 +242,27 @@ __global__ void __launch_bounds__(256) clone_state_kernel(void* const* __restric
     }
 }
 
+// Read-only streaming probe: each workgroup reads a contiguous span with 16-byte
+// nontemporal loads (8 in flight per thread) and folds it into one word.
+__global__ void __launch_bounds__(256) stream_read_kernel(const uint4* __restrict__ src, uint64_t per_block,
+                                                          uint32_t* __restrict__ sink) {
+    typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+    const u4v* base = reinterpret_cast<const u4v*>(src) + blockIdx.x * per_block;
+    uint32_t acc = 0;
+    for (uint64_t i = threadIdx.x; i < per_block; i += 256 * 8) {
+        u4v v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const uint64_t j = i + static_cast<uint64_t>(u) * 256;
+            v[u] = j < per_block ? __builtin_nontemporal_load(base + j) : u4v{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    acc ^= __shfl_xor(acc, 1, 64);
+    if (threadIdx.x == 0) sink[blockIdx.x] = acc;
+}
+
 int launch_status() { return hip_status(hipGetLastError()); }
 
 }  // namespace
@@ -368,5 +389,15 @@ extern "C" miikv_status miikv_clone_state(void* const* d_dsts, const void* src, 
     if (blocks > 8192) blocks = 8192;
     hipLaunchKernelGGL(clone_state_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), d_dsts, reinterpret_cast<const uint4*>(src), n16, n);
+    return launch_status();
+}
+
+extern "C" miikv_status miikv_stream_read(const void* src, uint64_t bytes, uint32_t* sink, uint32_t blocks,
+                                          void* stream) {
+    if (src == nullptr || sink == nullptr || blocks == 0 || (bytes % (16ull * blocks)) != 0 ||
+        (reinterpret_cast<uintptr_t>(src) & 15u) != 0)
+        return MIIKV_EINVAL;
+    hipLaunchKernelGGL(stream_read_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       reinterpret_cast<const uint4*>(src), bytes / 16 / blocks, sink);
     return launch_status();
 }

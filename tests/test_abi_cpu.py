@@ -1,0 +1,134 @@
+"""The C-ABI library on the host (no GPU): it loads, exports every symbol that
+include/miikv.h declares, and rejects invalid arguments before launching
+anything (the reference aborts instead: include/miinfer/hip_check.hpp:11-38)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "miikv.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(miikv_[a-z0-9_]+)\s*\(", text)))
+
+
+def _lib():
+    import torch  # noqa: F401  (shares its HIP runtime with the library)
+
+    from miinfer_amd import _lib
+    return _lib
+
+
+def test_header_declares_the_boundary():
+    syms = _declared_symbols()
+    for must in ("miikv_append_f16", "miikv_decode_attn", "miikv_copy_pages", "miikv_clone_state",
+                 "miikv_export_canonical", "miikv_decode_workspace_bytes"):
+        assert must in syms
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib()
+    lib = ctypes.CDLL(L.LIB)
+    missing = [s for s in _declared_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+    # and the Python binding knows each of them
+    assert not [s for s in _declared_symbols() if s not in L.SIGNATURES]
+
+
+def _view(**over):
+    L = _lib()
+    v = L.MiikvView()
+    v.k_codes = v.v_codes = 0x1000
+    v.k_scales = v.v_scales = 0x2000
+    v.layout = L.LAYOUT_CONTIGUOUS
+    v.quant_mode = L.KV_Q8_Q8
+    v.kv_heads = 8
+    v.head_dim = 128
+    v.page_tokens = 4096
+    v.num_pages = 1
+    for k, val in over.items():
+        setattr(v, k, val)
+    return v
+
+
+def test_version_and_status_strings():
+    L = _lib()
+    lib = L.lib()
+    assert lib.miikv_abi_version() == 1
+    assert lib.miikv_status_string(L.MIIKV_EINVAL) == b"invalid argument"
+
+
+@pytest.mark.parametrize("over,status", [
+    ({"head_dim": 64}, 2), ({"quant_mode": 0}, 2), ({"page_tokens": 100}, 1),
+    ({"kv_heads": 0}, 1), ({"layout": 7}, 1), ({"num_pages": 2}, 1),
+    ({"layout": 1, "num_pages": 4}, 1),  # paged without a block table
+])
+def test_plane_bytes_validation(over, status):
+    L = _lib()
+    cb, sb = ctypes.c_uint64(), ctypes.c_uint64()
+    assert L.lib().miikv_plane_bytes(ctypes.byref(_view(**over)), ctypes.byref(cb),
+                                     ctypes.byref(sb)) == status
+
+
+def test_plane_bytes_geometry():
+    L = _lib()
+    cb, sb = ctypes.c_uint64(), ctypes.c_uint64()
+    assert L.lib().miikv_plane_bytes(ctypes.byref(_view()), ctypes.byref(cb), ctypes.byref(sb)) == 0
+    assert cb.value == 8 * 4096 * 128 and sb.value == 8 * 4096 * 4 * 2
+
+
+def test_decode_rejects_before_launch():
+    L = _lib()
+    lib = L.lib()
+    v = _view()
+    ws = ctypes.c_void_p(0x3000)
+    f = ctypes.c_float(0.1)
+    # q_heads not a multiple of kv_heads
+    assert lib.miikv_decode_attn(ctypes.byref(v), ctypes.c_void_p(0x10), 0, 30, f, 1,
+                                 ctypes.c_void_p(0x20), None, 4096, ctypes.c_void_p(0x30), None,
+                                 None, ws, 1 << 30, None) == L.MIIKV_EINVAL
+    # max_context above the capacity
+    assert lib.miikv_decode_attn(ctypes.byref(v), ctypes.c_void_p(0x10), 0, 32, f, 1,
+                                 ctypes.c_void_p(0x20), None, 8192, ctypes.c_void_p(0x30), None,
+                                 None, ws, 1 << 30, None) == L.MIIKV_EINVAL
+    # no length source
+    assert lib.miikv_decode_attn(ctypes.byref(v), ctypes.c_void_p(0x10), 0, 32, f, 1, None, None,
+                                 4096, ctypes.c_void_p(0x30), None, None, ws, 1 << 30,
+                                 None) == L.MIIKV_EINVAL
+    # workspace too small
+    need = lib.miikv_decode_workspace_bytes(ctypes.byref(v), 32, 1, 4096)
+    assert need > 0
+    assert lib.miikv_decode_attn(ctypes.byref(v), ctypes.c_void_p(0x10), 0, 32, f, 1,
+                                 ctypes.c_void_p(0x20), None, 4096, ctypes.c_void_p(0x30), None,
+                                 None, ws, need - 1, None) == L.MIIKV_EWORKSPACE
+    # a gate without gated output
+    assert lib.miikv_decode_attn(ctypes.byref(v), ctypes.c_void_p(0x10), 0, 32, f, 1,
+                                 ctypes.c_void_p(0x20), None, 4096, ctypes.c_void_p(0x30),
+                                 ctypes.c_void_p(0x40), None, ws, need, None) == L.MIIKV_EINVAL
+
+
+def test_append_rejects_before_launch():
+    L = _lib()
+    lib = L.lib()
+    v = _view()
+    p = ctypes.c_void_p(0x10)
+    assert lib.miikv_append_f16(ctypes.byref(v), p, p, 2, 4095, 0, None, None, None) == L.MIIKV_EINVAL
+    assert lib.miikv_append_f16(ctypes.byref(v), p, p, 1, 0, 1, None, None, None) == L.MIIKV_EINVAL
+    assert lib.miikv_append_f16(None, p, p, 1, 0, 0, None, None, None) == L.MIIKV_EINVAL
+    assert lib.miikv_clone_state(p, p, 17, 2, None) == L.MIIKV_EINVAL  # not a multiple of 16
+    assert lib.miikv_copy_segments(None, 3, None) == L.MIIKV_EINVAL
+
+
+def test_workspace_bytes_scales_with_geometry():
+    L = _lib()
+    lib = L.lib()
+    v = _view(page_tokens=32768)
+    small = lib.miikv_decode_workspace_bytes(ctypes.byref(v), 32, 1, 4096)
+    big = lib.miikv_decode_workspace_bytes(ctypes.byref(v), 32, 1, 32768)
+    assert 0 < small <= big and big % 256 == 0
+    assert lib.miikv_decode_workspace_bytes(ctypes.byref(v), 30, 1, 4096) == 0
