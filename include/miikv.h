@@ -169,6 +169,28 @@ miikv_status miikv_decode_attn(const miikv_view* view, const void* q, uint32_t q
                                float* gated_out, void* workspace, uint64_t workspace_bytes,
                                void* stream);
 
+/* ---- suffix (multi-token) attention over a cached prefix ----------------- */
+
+/* Causal attention of a token_count-token suffix whose rows already sit in the
+ * cache at positions base_position .. base_position+token_count-1 (append them
+ * first); token t attends to positions [0, base_position + t].
+ *   q    device [token_count][q_heads][head_dim], fp16 or fp32 (fp32 is rounded
+ *        to fp16 for the MFMA)
+ *   out / gated_out  device [token_count][q_heads][head_dim] fp32; gated_out =
+ *        out * sigmoid(gate).  At least one output is required.
+ * If prefill_state is non-NULL, base_position and token_count come from it on
+ * the device (token_count is then a host upper bound).
+ * Replaces launch_qwen35_splitk_suffix_attention_quant
+ * (include/miinfer/qwen3_gpu_primitives.hpp:670-693; kernels
+ * gfx906/kernels/qwen3_primitives.hip:6789-7207, 6637-6725). */
+uint64_t miikv_suffix_workspace_bytes(const miikv_view* view, uint32_t q_heads, uint32_t token_count);
+miikv_status miikv_suffix_attn(const miikv_view* view, const void* q, uint32_t q_dtype,
+                               uint32_t q_heads, float scale, uint32_t token_count,
+                               uint32_t base_position, uint32_t seq,
+                               const miikv_prefill_state* prefill_state, float* out,
+                               const float* gate, float* gated_out, void* workspace,
+                               uint64_t workspace_bytes, void* stream);
+
 /* ---- export / import ----------------------------------------------------- */
 
 /* Copy tokens [t0, t0+count) of sequence `seq` out of the tiled cache into

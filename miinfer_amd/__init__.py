@@ -13,9 +13,10 @@ from .kv import (  # noqa: F401
     decode_attention,
     make_decode_state,
     make_prefill_state,
+    suffix_attention,
 )
 
 __all__ = [
     "MiikvError", "lib", "KvCache", "DecodeWorkspace", "decode_attention", "clone_state",
-    "copy_segments", "make_decode_state", "make_prefill_state",
+    "copy_segments", "make_decode_state", "make_prefill_state", "suffix_attention",
 ]

@@ -76,6 +76,9 @@ SIGNATURES = {
     "miikv_copy_segments": (ctypes.c_int, [_P, _U32, _P]),
     "miikv_clone_state": (ctypes.c_int, [_P, _P, _U64, _U32, _P]),
     "miikv_stream_read": (ctypes.c_int, [_P, _U64, _P, _U32, _P]),
+    "miikv_suffix_workspace_bytes": (_U64, [_VP, _U32, _U32]),
+    "miikv_suffix_attn": (ctypes.c_int, [_VP, _P, _U32, _U32, ctypes.c_float, _U32, _U32, _U32, _P,
+                                          _P, _P, _P, _P, _U64, _P]),
 }
 
 _lib = None

@@ -19,6 +19,7 @@ ARCH = "gfx950"
 SOURCES = [
     "miikv_cache.hip",
     "miikv_decode.hip",
+    "miikv_suffix.hip",
 ]
 
 FLAGS = [

@@ -291,6 +291,36 @@ def decode_attention(cache: KvCache, q: torch.Tensor, scale: float | None = None
     return out, gated_out
 
 
+def suffix_attention(cache: KvCache, q: torch.Tensor, base_position: int, scale: float | None = None,
+                     *, seq: int = 0, prefill_state: torch.Tensor | None = None,
+                     gate: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                     gated_out: torch.Tensor | None = None, stream=None):
+    """Causal attention of a T-token suffix (rows already appended at base_position..)
+    over the cache.  q: [T, q_heads, head_dim] fp16/fp32.  Returns (out, gated_out)."""
+    t, q_heads, d = q.shape
+    if d != cache.head_dim or not q.is_contiguous() or q.dtype not in (torch.float16,
+                                                                        torch.float32):
+        raise ValueError("q must be contiguous fp16/fp32 [T, q_heads, head_dim]")
+    cache._check_seq(seq)
+    for tns in (gate, out, gated_out):
+        if tns is not None and (tuple(tns.shape) != (t, q_heads, d) or tns.dtype != torch.float32
+                                or not tns.is_contiguous()):
+            raise ValueError("gate/out/gated_out must be contiguous fp32 [T, q_heads, D]")
+    if prefill_state is not None and prefill_state.numel() * prefill_state.element_size() < 64:
+        raise ValueError("prefill_state must be a 64-byte device buffer")
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if out is None and gate is None:
+        out = torch.empty((t, q_heads, d), dtype=torch.float32, device=q.device)
+    if gate is not None and gated_out is None:
+        gated_out = torch.empty((t, q_heads, d), dtype=torch.float32, device=q.device)
+    qd = _lib.DTYPE_F16 if q.dtype == torch.float16 else _lib.DTYPE_F32
+    call("miikv_suffix_attn", cache.view, _ptr(q), qd, q_heads, float(scale), t, base_position,
+         seq, _ptr(prefill_state), _ptr(out), _ptr(gate), _ptr(gated_out), None, 0,
+         _stream(stream))
+    return out, gated_out
+
+
 def make_decode_state(position: int, device="cuda") -> torch.Tensor:
     """A 64-byte device DeviceDecodeState with `position` set (current_token 0)."""
     st = torch.zeros(16, dtype=torch.int32, device=device)

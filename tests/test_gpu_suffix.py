@@ -1,0 +1,90 @@
+"""Suffix attention over a cached q8_0 prefix (MFMA) vs the fp32 oracle (GPU).
+
+Tolerance: max-abs 2e-3 and relative 1e-2 (tests/helpers.py)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.helpers import assert_attention_close, randn_f16
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a, gpu):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+
+
+def _setup(gpu, rng, hq, hk, d, prefix, t, cap):
+    import miinfer_amd as m
+    cache = m.KvCache.contiguous(hk, d, cap)
+    k = randn_f16(rng, (prefix + t, hk, d))
+    v = randn_f16(rng, (prefix + t, hk, d))
+    if prefix:
+        cache.append(_dev(k[:prefix], gpu), _dev(v[:prefix], gpu), base_position=0)
+    cache.append(_dev(k[prefix:], gpu), _dev(v[prefix:], gpu), base_position=prefix)  # the suffix rows
+    kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+    vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+    return cache, (kc, ks, vc, vs)
+
+
+@pytest.mark.parametrize("hq,hk,d,prefix,t", [(24, 4, 256, 300, 40), (32, 8, 128, 1000, 64),
+                                              (24, 4, 256, 0, 17), (6, 1, 128, 64, 1),
+                                              (24, 4, 256, 257, 33)])
+def test_suffix_small(gpu, hq, hk, d, prefix, t):
+    import miinfer_amd as m
+    rng = np.random.default_rng(prefix + t + d)
+    cap = ((prefix + t + 63) // 64) * 64
+    cache, ref = _setup(gpu, rng, hq, hk, d, prefix, t, cap)
+    q = randn_f16(rng, (t, hq, d))
+    gate = rng.standard_normal((t, hq, d)).astype(np.float32)
+    out, gated = m.suffix_attention(cache, _dev(q, gpu), prefix, gate=_dev(gate, gpu),
+                                    out=torch.empty((t, hq, d), device=gpu))
+    torch.cuda.synchronize()
+    expect = oracle.suffix_attention_q8(q.astype(np.float32), *ref, prefix, hq, 1 / math.sqrt(d))
+    assert_attention_close(out.cpu().numpy(), expect, "suffix")
+    assert_attention_close(gated.cpu().numpy(), expect / (1 + np.exp(-gate)), "suffix gated")
+
+
+def test_suffix_config4_full_size_sampled_tokens(gpu):
+    """Config 4: 512 suffix tokens over an 8192-token prefix (24q/4kv/D256); the oracle
+    checks a sample of tokens (each is an independent causal row set)."""
+    import miinfer_amd as m
+    hq, hk, d, prefix, t = 24, 4, 256, 8192, 512
+    rng = np.random.default_rng(4)
+    cache, ref = _setup(gpu, rng, hq, hk, d, prefix, t, prefix + t)
+    q = randn_f16(rng, (t, hq, d))
+    out, _ = m.suffix_attention(cache, _dev(q, gpu), prefix)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    for tok in (0, 1, 63, 64, 255, 511):
+        expect = oracle.attention_q8(q[tok].astype(np.float32), *ref, prefix + tok + 1, hq,
+                                     1 / math.sqrt(d))
+        assert_attention_close(out[tok], expect, f"token {tok}")
+
+
+def test_suffix_prefill_state_and_paged(gpu):
+    import miinfer_amd as m
+    rng = np.random.default_rng(8)
+    hq, hk, d, pt = 24, 4, 256, 256
+    prefix, t = 700, 100
+    npages = (prefix + t + pt - 1) // pt
+    table = _dev(rng.permutation(npages + 2)[:npages].astype(np.int32).reshape(1, npages), gpu)
+    cache = m.KvCache.paged_cache(hk, d, npages + 2, table, page_tokens=pt)
+    k = randn_f16(rng, (prefix + t, hk, d))
+    v = randn_f16(rng, (prefix + t, hk, d))
+    cache.append(_dev(k, gpu), _dev(v, gpu), base_position=0)
+    kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+    vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+    q = randn_f16(rng, (t + 20, hq, d))  # host bound 120 rows, device says 100
+    ps = m.make_prefill_state(prefix, t, device=gpu)
+    out = torch.full((t + 20, hq, d), 5.0, device=gpu)
+    m.suffix_attention(cache, _dev(q, gpu), 0, prefill_state=ps, out=out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    expect = oracle.suffix_attention_q8(q[:t].astype(np.float32), kc, ks, vc, vs, prefix, hq,
+                                        1 / math.sqrt(d))
+    assert_attention_close(got[:t], expect, "paged suffix")
+    assert np.all(got[t:] == 5.0)  # rows past the device token count untouched
