@@ -72,6 +72,156 @@ def cpu_baseline(ctx_cpu: int = 32768) -> dict:
     }
 
 
+def _time_graph(fn, nsteps, warmup):
+    """Capture `fn(stream)` once in a graph, replay; returns (us per replay, replays)."""
+    import torch
+    stream = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        fn(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            g.replay()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(nsteps):
+            g.replay()
+        e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / nsteps, nsteps
+
+
+def bench_c3(dev, args) -> int:
+    """Config 3: batched paged decode, 24q/4kv/D256, 16 sequences with context lengths
+    uniform in [1024, 65536] (seeded), 256-token pages behind a random permutation
+    block table; each step appends one row per sequence, then attends."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    import miinfer_amd as m
+    from miinfer_amd import _lib
+    hq, hkv, d, pt, batch = 24, 4, 256, 256, 16
+    rng = np.random.default_rng(3)
+    lens = rng.integers(1024, 65536 + 1, size=batch)
+    pages = [(int(n) + pt) // pt for n in lens]  # room for the appended row
+    stride = max(pages)
+    perm = rng.permutation(sum(pages)).astype(np.int32)
+    table = np.zeros((batch, stride), np.int32)
+    o = 0
+    for b, p in enumerate(pages):
+        table[b, :p] = perm[o:o + p]
+        o += p
+    tab = torch.from_numpy(table).to(dev)
+    cache = m.KvCache.paged_cache(hkv, d, sum(pages), tab, page_tokens=pt, device=dev)
+    torch.manual_seed(0)
+    for b, n in enumerate(lens):
+        for t0 in range(0, int(n), 8192):
+            c = min(8192, int(n) - t0)
+            cache.append(torch.randn((c, hkv, d), device=dev).half(),
+                         torch.randn((c, hkv, d), device=dev).half(), base_position=t0, seq=b)
+    q = torch.randn((batch, hq, d), device=dev).half()
+    kn = torch.randn((batch, hkv, d), device=dev).half()
+    vn = torch.randn((batch, hkv, d), device=dev).half()
+    pos = torch.from_numpy(lens.astype(np.int32) - 1).to(dev)   # overwrite the last row
+    lengths = torch.from_numpy(lens.astype(np.int32)).to(dev)
+    max_ctx = stride * pt
+    out = torch.empty((batch, hq, d), device=dev)
+    ws = m.DecodeWorkspace(cache, hq, batch, max_ctx)
+    L = _lib.lib()
+    P = ctypes.c_void_p
+
+    def step(s):
+        st = L.miikv_append_batch_f16(cache.view, P(kn.data_ptr()), P(vn.data_ptr()), batch,
+                                      P(pos.data_ptr()), P(s.cuda_stream))
+        st |= L.miikv_decode_attn(cache.view, P(q.data_ptr()), _lib.DTYPE_F16, hq,
+                                  ctypes.c_float(1 / math.sqrt(d)), batch, P(lengths.data_ptr()),
+                                  None, max_ctx, P(out.data_ptr()), None, None, P(ws.buf.data_ptr()),
+                                  ws.bytes, P(s.cuda_stream))
+        assert st == 0, st
+
+    def dec(s):
+        st = L.miikv_decode_attn(cache.view, P(q.data_ptr()), _lib.DTYPE_F16, hq,
+                                 ctypes.c_float(1 / math.sqrt(d)), batch, P(lengths.data_ptr()),
+                                 None, max_ctx, P(out.data_ptr()), None, None, P(ws.buf.data_ptr()),
+                                 ws.bytes, P(s.cuda_stream))
+        assert st == 0, st
+    torch.cuda.synchronize()
+    us, n = _time_graph(step, max(10, args.steps // 10), 10)
+    us_dec, _ = _time_graph(dec, max(10, args.steps // 10), 10)
+    tokens = int(lens.sum())
+    dbytes = tokens * kv_bytes_per_token(hkv, d) + batch * hq * d * 6
+    print(json.dumps({
+        "metric": "paged batched decode-attn q8_0 KV GB/s (config 3)", "unit": "GB/s",
+        "value": round((dbytes + batch * append_bytes(hkv, d)) / (us * 1e-6) / 1e9, 1),
+        "us_per_step": round(us, 2), "steps": n, "n_gpus": 1,
+        "config": {"workload": "config 3: 16 seqs, 24q/4kv/D256, 256-token pages, random table",
+                   "context_tokens_total": tokens, "max_context": int(lens.max())},
+        "roofline": {"bound": "hbm", "kernel": "miikv_decode_attn (split + combine)",
+                     "achieved": round(dbytes / (us_dec * 1e-6) / 1e9, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(dbytes / (us_dec * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                     "algorithmic_bytes_per_launch": dbytes, "avg_launch_us": round(us_dec, 2)},
+    }), flush=True)
+    return 0
+
+
+def bench_c4(dev, args) -> int:
+    """Config 4: 512-token suffix (24q/4kv/D256) over an 8192-token q8_0 prefix: append the
+    512 new K/V rows, then causal suffix attention.  MFMA roofline over the visible pairs."""
+    import ctypes
+
+    import torch
+
+    import miinfer_amd as m
+    from miinfer_amd import _lib
+    hq, hkv, d, prefix, t = 24, 4, 256, 8192, 512
+    cache = m.KvCache.contiguous(hkv, d, prefix + t, device=dev)
+    torch.manual_seed(0)
+    cache.append(torch.randn((prefix, hkv, d), device=dev).half(),
+                 torch.randn((prefix, hkv, d), device=dev).half())
+    q = torch.randn((t, hq, d), device=dev).half()
+    kn = torch.randn((t, hkv, d), device=dev).half()
+    vn = torch.randn((t, hkv, d), device=dev).half()
+    out = torch.empty((t, hq, d), device=dev)
+    L = _lib.lib()
+    P = ctypes.c_void_p
+
+    def append(s):
+        assert L.miikv_append_f16(cache.view, P(kn.data_ptr()), P(vn.data_ptr()), t, prefix, 0,
+                                  None, None, P(s.cuda_stream)) == 0
+
+    def attn(s):
+        assert L.miikv_suffix_attn(cache.view, P(q.data_ptr()), _lib.DTYPE_F16, hq,
+                                   ctypes.c_float(1 / math.sqrt(d)), t, prefix, 0, None,
+                                   P(out.data_ptr()), None, None, None, 0, P(s.cuda_stream)) == 0
+
+    def step(s):
+        append(s)
+        attn(s)
+    torch.cuda.synchronize()
+    nrep = max(10, args.steps // 20)
+    us_step, _ = _time_graph(step, nrep, 5)
+    us_attn, _ = _time_graph(attn, nrep, 5)
+    us_app, _ = _time_graph(append, nrep, 5)
+    pairs = sum(prefix + i + 1 for i in range(t))
+    flops = 4 * hq * d * pairs
+    print(json.dumps({
+        "metric": "suffix attention over q8_0 prefix TFLOP/s (config 4)", "unit": "TFLOP/s",
+        "value": round(flops / (us_step * 1e-6) / 1e12, 2), "us_per_step": round(us_step, 2),
+        "n_gpus": 1,
+        "config": {"workload": "config 4: 512-token suffix over 8192-token prefix, 24q/4kv/D256"},
+        "roofline": {"bound": "mfma", "kernel": "suffix_kernel<256>",
+                     "achieved": round(flops / (us_attn * 1e-6) / 1e12, 2), "peak": 2500.0,
+                     "unit": "TFLOP/s", "frac": round(flops / (us_attn * 1e-6) / 1e12 / 2500.0, 4),
+                     "algorithmic_flops_per_launch": flops, "avg_launch_us": round(us_attn, 2)},
+        "append": {"us": round(us_app, 2), "rows": t * hkv,
+                   "GBs": round(t * append_bytes(hkv, d) / (us_app * 1e-6) / 1e9, 1)},
+    }), flush=True)
+    return 0
+
+
 def calibrate_copy(dev) -> int:
     """A plain 256 MiB device-to-device copy through miikv_copy_segments: its
     FETCH_SIZE / WRITE_SIZE under rocprofv3 --pmc give the counter scale factor."""
@@ -146,6 +296,9 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4"],
+                    help="c2 (default, the headline metric); c3 paged batched decode; c4 suffix "
+                         "attention (these print their own JSON line, not the headline)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a 256 MiB device copy (known bytes) to calibrate PMC counters")
     args = ap.parse_args()
@@ -162,6 +315,10 @@ def main() -> int:
     dev = torch.device("cuda:0")
     if args.calibrate_copy:
         return calibrate_copy(dev)
+    if args.workload == "c3":
+        return bench_c3(dev, args)
+    if args.workload == "c4":
+        return bench_c4(dev, args)
     ctx, nl = args.context, args.layers
     torch.manual_seed(0)
     caches = []

@@ -228,6 +228,59 @@ miikv_status miikv_copy_segments(const miikv_segment* d_segments, uint32_t n, vo
 miikv_status miikv_clone_state(void* const* d_dsts, const void* src, uint64_t bytes, uint32_t n,
                                void* stream);
 
+/* ---- prefix reuse: host-side policy (no device work) ---------------------- */
+
+/* Page pool with reference counts for paged caches.  Forked sequences share full
+ * pages; a partial last page is copied (copy-on-write) so the child can append.
+ * No reference counterpart: the reference keeps one contiguous cache per layer
+ * and reuses a prefix in place (src/prefill_v2/model.cpp:752-846). */
+typedef struct miikv_pool miikv_pool;
+miikv_pool* miikv_pool_create(uint32_t num_pages);
+void miikv_pool_destroy(miikv_pool* pool);
+int32_t miikv_pool_alloc(miikv_pool* pool);                 /* -1 when exhausted */
+miikv_status miikv_pool_ref(miikv_pool* pool, int32_t page);
+miikv_status miikv_pool_unref(miikv_pool* pool, int32_t page); /* frees at zero */
+uint32_t miikv_pool_refcount(const miikv_pool* pool, int32_t page);
+uint32_t miikv_pool_free_pages(const miikv_pool* pool);
+/* Fork a sequence of `length` tokens: child_row[0..pages) shares the parent's
+ * full pages (reference +1); a partial last page gets a fresh page and one
+ * (copy_src, copy_dst) pair to run with miikv_copy_pages. */
+miikv_status miikv_pool_fork(miikv_pool* pool, const int32_t* parent_row, uint32_t length,
+                             uint32_t page_tokens, int32_t* child_row, int32_t* copy_src,
+                             int32_t* copy_dst, uint32_t* n_copies);
+/* Before appending at `position` (the sequence's current length): allocate a
+ * fresh page at a page boundary, or copy a shared page (copy-on-write). */
+miikv_status miikv_pool_prepare_append(miikv_pool* pool, int32_t* row, uint32_t row_capacity,
+                                       uint32_t position, uint32_t page_tokens,
+                                       int32_t* copy_src, int32_t* copy_dst, uint32_t* n_copies);
+miikv_status miikv_pool_release(miikv_pool* pool, const int32_t* row, uint32_t length,
+                                uint32_t page_tokens);
+
+/* Prefix fingerprint and match policy.  Restates ReusableContext
+ * (include/miinfer/prefill_v2/reusable_context.hpp:17-129,
+ * src/prefill_v2/reusable_context.cpp:130-207); results keep its enum order. */
+#define MIIKV_STATE_LAYOUT_VERSION 20260925u
+enum {
+    MIIKV_MATCH_EXACT = 0,
+    MIIKV_MATCH_PREFIX_MISMATCH = 1,
+    MIIKV_MATCH_MODEL_MISMATCH = 2,
+    MIIKV_MATCH_QUANTIZATION_MISMATCH = 3,
+    MIIKV_MATCH_EMPTY_CACHE = 4,
+    MIIKV_MATCH_PROMPT_SHORTER = 5,
+    MIIKV_MATCH_VERSION_MISMATCH = 6,
+};
+typedef struct miikv_prefix_ctx miikv_prefix_ctx;
+uint64_t miikv_token_hash(const uint32_t* tokens, size_t count); /* FNV-1a 64 */
+miikv_prefix_ctx* miikv_prefix_create(const char* model_id, const char* quantization);
+void miikv_prefix_destroy(miikv_prefix_ctx* ctx);
+miikv_status miikv_prefix_save(miikv_prefix_ctx* ctx, const uint32_t* tokens, size_t count);
+int miikv_prefix_check(const miikv_prefix_ctx* ctx, const uint32_t* prompt, size_t count,
+                       const char* model_id, const char* quantization);
+void miikv_prefix_clear(miikv_prefix_ctx* ctx);
+uint32_t miikv_prefix_length(const miikv_prefix_ctx* ctx);
+uint64_t miikv_prefix_hash(const miikv_prefix_ctx* ctx);
+void miikv_prefix_set_layout_version(miikv_prefix_ctx* ctx, uint32_t version);
+
 /* ---- measurement probe --------------------------------------------------- */
 
 /* Read `bytes` from src once with 16-byte nontemporal loads over `blocks`

@@ -77,6 +77,25 @@ SIGNATURES = {
     "miikv_clone_state": (ctypes.c_int, [_P, _P, _U64, _U32, _P]),
     "miikv_stream_read": (ctypes.c_int, [_P, _U64, _P, _U32, _P]),
     "miikv_suffix_workspace_bytes": (_U64, [_VP, _U32, _U32]),
+    "miikv_pool_create": (_P, [_U32]),
+    "miikv_pool_destroy": (None, [_P]),
+    "miikv_pool_alloc": (ctypes.c_int32, [_P]),
+    "miikv_pool_ref": (ctypes.c_int, [_P, ctypes.c_int32]),
+    "miikv_pool_unref": (ctypes.c_int, [_P, ctypes.c_int32]),
+    "miikv_pool_refcount": (_U32, [_P, ctypes.c_int32]),
+    "miikv_pool_free_pages": (_U32, [_P]),
+    "miikv_pool_fork": (ctypes.c_int, [_P, _P, _U32, _U32, _P, _P, _P, _P]),
+    "miikv_pool_prepare_append": (ctypes.c_int, [_P, _P, _U32, _U32, _U32, _P, _P, _P]),
+    "miikv_pool_release": (ctypes.c_int, [_P, _P, _U32, _U32]),
+    "miikv_token_hash": (_U64, [_P, ctypes.c_size_t]),
+    "miikv_prefix_create": (_P, [ctypes.c_char_p, ctypes.c_char_p]),
+    "miikv_prefix_destroy": (None, [_P]),
+    "miikv_prefix_save": (ctypes.c_int, [_P, _P, ctypes.c_size_t]),
+    "miikv_prefix_check": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_char_p, ctypes.c_char_p]),
+    "miikv_prefix_clear": (None, [_P]),
+    "miikv_prefix_length": (_U32, [_P]),
+    "miikv_prefix_hash": (_U64, [_P]),
+    "miikv_prefix_set_layout_version": (None, [_P, _U32]),
     "miikv_suffix_attn": (ctypes.c_int, [_VP, _P, _U32, _U32, ctypes.c_float, _U32, _U32, _U32, _P,
                                           _P, _P, _P, _P, _U64, _P]),
 }

@@ -20,6 +20,7 @@ SOURCES = [
     "miikv_cache.hip",
     "miikv_decode.hip",
     "miikv_suffix.hip",
+    "miikv_host.cpp",
 ]
 
 FLAGS = [

@@ -53,6 +53,12 @@ namespace {
 #ifndef MIIKV_RING_D256
 #define MIIKV_RING_D256 2
 #endif
+#ifndef MIIKV_WPE_D256
+#define MIIKV_WPE_D256 1
+#endif
+#ifndef MIIKV_VBIAS_D256
+#define MIIKV_VBIAS_D256 1
+#endif
 constexpr uint32_t kWavesPerWg = MIIKV_WPW;
 constexpr uint32_t kTargetWaves = 256 * 8;  // 256 CUs x 8 resident waves
 constexpr float kLog2e = 1.4426950408889634f;
@@ -111,12 +117,15 @@ __host__ __device__ __forceinline__ uint32_t record_floats(uint32_t G, uint32_t 
 }
 
 template <uint32_t D, bool QF32>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? MIIKV_WPE_D128 : 1)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? MIIKV_WPE_D128 : MIIKV_WPE_D256)))
 decode_kernel(DecodeArgs a) {
     constexpr uint32_t NB = D / 32;   // q8_0 blocks per row
     constexpr uint32_t NC = D / 64;   // 16-byte K loads per tile row group
     constexpr uint32_t NM = D / 16;   // V M-tiles (16 dims each)
     using ScaleVec = typename std::conditional<NB == 4, uint32_t, uint2>::type;  // NB/2 fp16 scales
+    // V codes enter the PV MFMA biased (one v_perm per two codes) and the bias is removed
+    // with column sums, or exactly (perm + subtract): the fold costs NB accumulators.
+    constexpr bool kVBias = (D == 128) ? true : (MIIKV_VBIAS_D256 != 0);
     extern __shared__ float smem[];
 
     const uint32_t split = blockIdx.x;
@@ -231,11 +240,11 @@ decode_kernel(DecodeArgs a) {
     float m_run = -INFINITY;
     float l_run = 0.0f;
     float4v O[NM];
-    float4v vbias[NB];  // column sums of the PV B operand per block (removes the V code bias)
+    float4v vbias[kVBias ? NB : 1];  // column sums of the PV B operand per block (V code bias)
 #pragma unroll
     for (uint32_t mt = 0; mt < NM; ++mt) O[mt] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (uint32_t blk = 0; blk < NB; ++blk) vbias[blk] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t blk = 0; blk < (kVBias ? NB : 1); ++blk) vbias[blk] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
     const half4 ones = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
 
     const uint32_t nsteps = (L + kChunk - 1) / kChunk;
@@ -338,8 +347,10 @@ decode_kernel(DecodeArgs a) {
             l_run *= alpha;
 #pragma unroll
             for (uint32_t mt = 0; mt < NM; ++mt) O[mt] *= alpha;
+            if constexpr (kVBias) {
 #pragma unroll
-            for (uint32_t blk = 0; blk < NB; ++blk) vbias[blk] *= alpha;
+                for (uint32_t blk = 0; blk < NB; ++blk) vbias[blk] *= alpha;
+            }
         }
         float psum = 0.0f;
 #pragma unroll
@@ -371,14 +382,10 @@ decode_kernel(DecodeArgs a) {
                 for (uint32_t sub = 0; sub < 2; ++sub) {
                     const uint32_t mt = 2 * blk + sub;
                     const uint32_t word = J == 0 ? st.v[mt].x : st.v[mt].y;
-#ifdef MIIKV_EXP_NO_VBIAS
-                    O[mt] = mfma_16x16x16(codes4_to_half4(word), pb, O[mt]);
+                    if constexpr (kVBias) O[mt] = mfma_16x16x16(codes4_to_half4_biased(word), pb, O[mt]);
+                    else O[mt] = mfma_16x16x16(codes4_to_half4(word), pb, O[mt]);
                 }
-#else
-                    O[mt] = mfma_16x16x16(codes4_to_half4_biased(word), pb, O[mt]);
-                }
-                vbias[blk] = mfma_16x16x16(ones, pb, vbias[blk]);
-#endif
+                if constexpr (kVBias) vbias[blk] = mfma_16x16x16(ones, pb, vbias[blk]);
             }
         }
     };
@@ -393,8 +400,10 @@ decode_kernel(DecodeArgs a) {
             compute_step(c + r, S[r]);
         }
     }
+    if constexpr (kVBias) {
 #pragma unroll
-    for (uint32_t mt = 0; mt < NM; ++mt) O[mt] -= kCodeBias * vbias[mt / 2];
+        for (uint32_t mt = 0; mt < NM; ++mt) O[mt] -= kCodeBias * vbias[mt / 2];
+    }
 
     // ---- wave-level sums, then cross-wave combine in LDS.
     l_run += __shfl_xor(l_run, 16, 64);

@@ -1,0 +1,220 @@
+// Host-side policy of the prefix-reuse path: the page pool with reference counts
+// and copy-on-write fork planning for paged q8_0 caches, and the prefix
+// fingerprint / match logic of ReusableContext.  Pure C++ (no device calls);
+// the device work these plans describe runs through miikv_copy_pages,
+// miikv_copy_segments and miikv_clone_state.
+#include <cstdint>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "miikv.h"
+
+// ---------------------------------------------------------------------------
+// Page pool: free list + per-page reference counts.  No reference counterpart:
+// the reference keeps one contiguous cache per layer (kv_cache.cpp:10-39) and
+// reuses a prefix by leaving it in place (src/prefill_v2/model.cpp:752-846).
+// ---------------------------------------------------------------------------
+struct miikv_pool {
+    std::vector<uint32_t> refs;
+    std::vector<int32_t> free_list;  // LIFO
+};
+
+extern "C" miikv_pool* miikv_pool_create(uint32_t num_pages) {
+    if (num_pages == 0 || num_pages > 0x7fffffffu) return nullptr;
+    miikv_pool* p = new (std::nothrow) miikv_pool;
+    if (p == nullptr) return nullptr;
+    p->refs.assign(num_pages, 0);
+    p->free_list.reserve(num_pages);
+    for (uint32_t i = num_pages; i > 0; --i) p->free_list.push_back(static_cast<int32_t>(i - 1));
+    return p;
+}
+
+extern "C" void miikv_pool_destroy(miikv_pool* p) { delete p; }
+
+extern "C" int32_t miikv_pool_alloc(miikv_pool* p) {
+    if (p == nullptr || p->free_list.empty()) return -1;
+    const int32_t page = p->free_list.back();
+    p->free_list.pop_back();
+    p->refs[static_cast<size_t>(page)] = 1;
+    return page;
+}
+
+static bool valid_page(const miikv_pool* p, int32_t page) {
+    return p != nullptr && page >= 0 && static_cast<size_t>(page) < p->refs.size();
+}
+
+extern "C" miikv_status miikv_pool_ref(miikv_pool* p, int32_t page) {
+    if (!valid_page(p, page) || p->refs[static_cast<size_t>(page)] == 0) return MIIKV_EINVAL;
+    ++p->refs[static_cast<size_t>(page)];
+    return MIIKV_OK;
+}
+
+extern "C" miikv_status miikv_pool_unref(miikv_pool* p, int32_t page) {
+    if (!valid_page(p, page) || p->refs[static_cast<size_t>(page)] == 0) return MIIKV_EINVAL;
+    if (--p->refs[static_cast<size_t>(page)] == 0) p->free_list.push_back(page);
+    return MIIKV_OK;
+}
+
+extern "C" uint32_t miikv_pool_refcount(const miikv_pool* p, int32_t page) {
+    return valid_page(p, page) ? p->refs[static_cast<size_t>(page)] : 0u;
+}
+
+extern "C" uint32_t miikv_pool_free_pages(const miikv_pool* p) {
+    return p == nullptr ? 0u : static_cast<uint32_t>(p->free_list.size());
+}
+
+static uint32_t pages_for(uint32_t tokens, uint32_t page_tokens) {
+    return (tokens + page_tokens - 1) / page_tokens;
+}
+
+extern "C" miikv_status miikv_pool_fork(miikv_pool* p, const int32_t* parent_row, uint32_t length,
+                                        uint32_t page_tokens, int32_t* child_row, int32_t* copy_src,
+                                        int32_t* copy_dst, uint32_t* n_copies) {
+    if (p == nullptr || page_tokens == 0 || (length > 0 && (parent_row == nullptr || child_row == nullptr)) ||
+        n_copies == nullptr)
+        return MIIKV_EINVAL;
+    *n_copies = 0;
+    const uint32_t np = pages_for(length, page_tokens);
+    for (uint32_t i = 0; i < np; ++i)
+        if (!valid_page(p, parent_row[i]) || p->refs[static_cast<size_t>(parent_row[i])] == 0) return MIIKV_EINVAL;
+    const bool partial = (length % page_tokens) != 0;
+    if (partial && (copy_src == nullptr || copy_dst == nullptr)) return MIIKV_EINVAL;
+    int32_t fresh = -1;
+    if (partial) {
+        fresh = miikv_pool_alloc(p);
+        if (fresh < 0) return MIIKV_EINVAL;  // pool exhausted: nothing was changed
+    }
+    for (uint32_t i = 0; i < np; ++i) {
+        if (partial && i + 1 == np) {
+            child_row[i] = fresh;
+            copy_src[0] = parent_row[i];
+            copy_dst[0] = fresh;
+            *n_copies = 1;
+        } else {
+            child_row[i] = parent_row[i];
+            ++p->refs[static_cast<size_t>(parent_row[i])];
+        }
+    }
+    return MIIKV_OK;
+}
+
+extern "C" miikv_status miikv_pool_prepare_append(miikv_pool* p, int32_t* row, uint32_t row_capacity,
+                                                  uint32_t position, uint32_t page_tokens, int32_t* copy_src,
+                                                  int32_t* copy_dst, uint32_t* n_copies) {
+    if (p == nullptr || row == nullptr || page_tokens == 0 || n_copies == nullptr) return MIIKV_EINVAL;
+    *n_copies = 0;
+    const uint32_t i = position / page_tokens;
+    if (i >= row_capacity) return MIIKV_EINVAL;
+    if (position % page_tokens == 0) {
+        // First token of a new page: allocate it (a shared full page is never written).
+        const int32_t fresh = miikv_pool_alloc(p);
+        if (fresh < 0) return MIIKV_EINVAL;
+        row[i] = fresh;
+        return MIIKV_OK;
+    }
+    if (!valid_page(p, row[i]) || p->refs[static_cast<size_t>(row[i])] == 0) return MIIKV_EINVAL;
+    if (p->refs[static_cast<size_t>(row[i])] == 1) return MIIKV_OK;  // exclusively owned
+    if (copy_src == nullptr || copy_dst == nullptr) return MIIKV_EINVAL;
+    const int32_t fresh = miikv_pool_alloc(p);
+    if (fresh < 0) return MIIKV_EINVAL;
+    copy_src[0] = row[i];
+    copy_dst[0] = fresh;
+    *n_copies = 1;
+    --p->refs[static_cast<size_t>(row[i])];
+    row[i] = fresh;
+    return MIIKV_OK;
+}
+
+extern "C" miikv_status miikv_pool_release(miikv_pool* p, const int32_t* row, uint32_t length, uint32_t page_tokens) {
+    if (p == nullptr || page_tokens == 0 || (length > 0 && row == nullptr)) return MIIKV_EINVAL;
+    const uint32_t np = pages_for(length, page_tokens);
+    for (uint32_t i = 0; i < np; ++i)
+        if (!valid_page(p, row[i]) || p->refs[static_cast<size_t>(row[i])] == 0) return MIIKV_EINVAL;
+    for (uint32_t i = 0; i < np; ++i) miikv_pool_unref(p, row[i]);
+    return MIIKV_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Prefix fingerprint and match policy: restates ReusableContext
+// (include/miinfer/prefill_v2/reusable_context.hpp:17-129,
+//  src/prefill_v2/reusable_context.cpp:130-207).
+// ---------------------------------------------------------------------------
+struct miikv_prefix_ctx {
+    std::string model_id;
+    std::string quantization;
+    uint32_t prefix_length = 0;
+    uint64_t token_hash = 0;
+    uint32_t layout_version = MIIKV_STATE_LAYOUT_VERSION;
+    std::vector<uint32_t> tokens;
+    bool state_valid = false;  // a state checkpoint was captured with the prefix
+};
+
+// 64-bit FNV-1a over u32 tokens widened to u64 (reusable_context.hpp:38-45).
+extern "C" uint64_t miikv_token_hash(const uint32_t* tokens, size_t count) {
+    uint64_t hash = 0xcbf29ce484222325ull;
+    for (size_t i = 0; i < count; ++i) {
+        hash ^= static_cast<uint64_t>(tokens[i]);
+        hash *= 0x100000001b3ull;
+    }
+    return hash;
+}
+
+extern "C" miikv_prefix_ctx* miikv_prefix_create(const char* model_id, const char* quantization) {
+    miikv_prefix_ctx* c = new (std::nothrow) miikv_prefix_ctx;
+    if (c == nullptr) return nullptr;
+    c->model_id = model_id ? model_id : "";
+    c->quantization = quantization ? quantization : "";
+    return c;
+}
+
+extern "C" void miikv_prefix_destroy(miikv_prefix_ctx* c) { delete c; }
+
+extern "C" void miikv_prefix_clear(miikv_prefix_ctx* c) {
+    if (c == nullptr) return;
+    c->state_valid = false;
+    c->tokens.clear();
+    c->prefix_length = 0;
+    c->token_hash = 0;
+}
+
+// save (reusable_context.cpp:138-153): an empty prefix clears; otherwise the caller
+// has captured the recurrent state (capture = miikv_copy_segments) and the
+// fingerprint is recorded.
+extern "C" miikv_status miikv_prefix_save(miikv_prefix_ctx* c, const uint32_t* tokens, size_t count) {
+    if (c == nullptr || (count > 0 && tokens == nullptr) || count > 0xffffffffu) return MIIKV_EINVAL;
+    if (count == 0) {
+        miikv_prefix_clear(c);
+        return MIIKV_OK;
+    }
+    c->tokens.assign(tokens, tokens + count);
+    c->prefix_length = static_cast<uint32_t>(count);
+    c->token_hash = miikv_token_hash(tokens, count);
+    c->layout_version = MIIKV_STATE_LAYOUT_VERSION;
+    c->state_valid = true;
+    return MIIKV_OK;
+}
+
+// check_match (reusable_context.cpp:155-185): precedence Empty -> Version -> Model ->
+// Quantization -> PromptShorter -> token compare.
+extern "C" int miikv_prefix_check(const miikv_prefix_ctx* c, const uint32_t* prompt, size_t count,
+                                  const char* model_id, const char* quantization) {
+    if (c == nullptr || !c->state_valid || c->prefix_length == 0) return MIIKV_MATCH_EMPTY_CACHE;
+    if (c->layout_version != MIIKV_STATE_LAYOUT_VERSION) return MIIKV_MATCH_VERSION_MISMATCH;
+    if (c->model_id != (model_id ? model_id : "")) return MIIKV_MATCH_MODEL_MISMATCH;
+    if (c->quantization != (quantization ? quantization : "")) return MIIKV_MATCH_QUANTIZATION_MISMATCH;
+    if (count < c->prefix_length) return MIIKV_MATCH_PROMPT_SHORTER;
+    if (prompt == nullptr) return MIIKV_MATCH_PREFIX_MISMATCH;
+    if (std::memcmp(prompt, c->tokens.data(), sizeof(uint32_t) * c->prefix_length) != 0)
+        return MIIKV_MATCH_PREFIX_MISMATCH;
+    return MIIKV_MATCH_EXACT;
+}
+
+extern "C" uint32_t miikv_prefix_length(const miikv_prefix_ctx* c) { return c ? c->prefix_length : 0u; }
+
+extern "C" uint64_t miikv_prefix_hash(const miikv_prefix_ctx* c) { return c ? c->token_hash : 0u; }
+
+extern "C" void miikv_prefix_set_layout_version(miikv_prefix_ctx* c, uint32_t version) {
+    if (c) c->layout_version = version;
+}

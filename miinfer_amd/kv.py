@@ -85,8 +85,10 @@ class KvCache:
             bt = self.block_table
             if bt.dtype != torch.int32 or bt.dim() != 2 or not bt.is_contiguous():
                 raise TypeError("block_table must be a contiguous int32 [batch, stride] tensor")
-            if bt.numel() and (int(bt.min()) < 0 or int(bt.max()) >= self.num_pages):
-                raise ValueError("block_table entries must lie in [0, num_pages)")
+            # -1 marks an entry not backing any token yet (kernels only read entries
+            # below each sequence's length; speculative reads clamp the index).
+            if bt.numel() and (int(bt.min()) < -1 or int(bt.max()) >= self.num_pages):
+                raise ValueError("block_table entries must lie in [0, num_pages) or be -1")
             v.block_table = bt.data_ptr()
             v.table_stride = bt.shape[1]
         else:

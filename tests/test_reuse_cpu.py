@@ -1,0 +1,134 @@
+"""Prefix-reuse host policy in libmiikv (no GPU): page pool, copy-on-write fork
+planning, and ReusableContext's fingerprint / match precedence."""
+import numpy as np
+import pytest
+
+import oracle
+
+
+def _m():
+    import torch  # noqa: F401
+
+    from miinfer_amd import reuse
+    return reuse
+
+
+def _prompt(count, seed):
+    # the synthetic prompt generator of bench/prefix_state_reuse_bench.cpp:60-68
+    out, val = [], seed
+    for _ in range(count):
+        val = (val * 1664525 + 1013904223) % (2**32) % 151643
+        out.append(val + 1)
+    return np.array(out, np.uint32)
+
+
+def test_reusable_context_six_cases():
+    """The six validation cases of bench/prefix_state_reuse_bench.cpp:71-112."""
+    r = _m()
+    ctx = r.PrefixContext("Qwen3.8-27B", "Q4_K_M")
+    prefix = _prompt(512, 100)
+    ctx.save(prefix)
+    exact = np.append(prefix, 1234).astype(np.uint32)
+    M = r.MatchResult
+    assert ctx.check_match(exact, "Qwen3.8-27B", "Q4_K_M") == M.EXACT_MATCH
+    assert ctx.check_match(exact, "Qwen3.8-32B", "Q4_K_M") == M.MODEL_MISMATCH
+    assert ctx.check_match(exact, "Qwen3.8-27B", "Q8_0") == M.QUANTIZATION_MISMATCH
+    corrupt = exact.copy()
+    corrupt[50] ^= 0x5555
+    assert ctx.check_match(corrupt, "Qwen3.8-27B", "Q4_K_M") == M.PREFIX_MISMATCH
+    assert ctx.check_match(_prompt(256, 100), "Qwen3.8-27B", "Q4_K_M") == M.PROMPT_SHORTER_THAN_PREFIX
+    ctx.clear()
+    assert ctx.check_match(exact, "Qwen3.8-27B", "Q4_K_M") == M.EMPTY_CACHE
+
+
+def test_match_precedence_and_fingerprint():
+    r = _m()
+    M = r.MatchResult
+    ctx = r.PrefixContext("m", "q")
+    assert ctx.check_match([1, 2], "m", "q") == M.EMPTY_CACHE
+    ctx.save([7, 8, 9])
+    assert ctx.prefix_length == 3
+    assert ctx.token_hash == oracle.token_hash([7, 8, 9]) == r.token_hash([7, 8, 9])
+    # Version is checked before model; model before quantization; both before length.
+    ctx._set_layout_version(1)
+    assert ctx.check_match([1], "x", "y") == M.VERSION_MISMATCH
+    ctx._set_layout_version(20260925)
+    assert ctx.check_match([1], "x", "y") == M.MODEL_MISMATCH
+    assert ctx.check_match([1], "m", "y") == M.QUANTIZATION_MISMATCH
+    assert ctx.check_match([1], "m", "q") == M.PROMPT_SHORTER_THAN_PREFIX
+    assert ctx.check_match([7, 8, 9], "m", "q") == M.EXACT_MATCH
+    ctx.save([])  # an empty save clears (reusable_context.cpp:142-145)
+    assert ctx.check_match([7, 8, 9], "m", "q") == M.EMPTY_CACHE
+
+
+def test_token_hash_published_vectors():
+    r = _m()
+    assert r.token_hash([]) == 0xCBF29CE484222325
+    assert r.token_hash([ord("a")]) == 0xAF63DC4C8601EC8C
+    assert r.token_hash([ord(c) for c in "foobar"]) == 0x85944171F73967E8
+    rng = np.random.default_rng(0)
+    t = rng.integers(0, 2**32, 1000, dtype=np.uint64).astype(np.uint32)
+    assert r.token_hash(t) == oracle.token_hash(t)
+
+
+@pytest.mark.parametrize("length", [1000, 1024])  # partial last page, full last page
+def test_pool_fork_and_copy_on_write(length):
+    r = _m()
+    pt = 256
+    pool = r.PagePool(32)
+    pages = (length + pt - 1) // pt
+    parent = np.array([pool.alloc() for _ in range(pages)] + [-1] * 4, np.int32)
+    child, copies = pool.fork(parent, length, pt)
+    full = length // pt
+    for i in range(full):
+        assert child[i] == parent[i] and pool.refcount(parent[i]) == 2
+    if length % pt:
+        assert len(copies) == 1 and copies[0][0] == parent[pages - 1]
+        assert child[pages - 1] == copies[0][1] != parent[pages - 1]
+        assert pool.refcount(parent[pages - 1]) == 1 and pool.refcount(child[pages - 1]) == 1
+    else:
+        assert copies == []
+    # the child appends: a partial page it owns needs no copy; a page boundary allocates
+    before = pool.free_pages
+    c = child.copy()
+    assert pool.prepare_append(c, length, pt) == []
+    assert pool.free_pages == before - (1 if length % pt == 0 else 0)
+    # a second fork of the child shares the child's partial page only via copy
+    grand, copies2 = pool.fork(c, length + 1, pt)
+    assert len(copies2) == 1
+    # releasing everything returns every page to the pool
+    pool.release(grand, length + 1, pt)
+    pool.release(c, length + 1, pt)
+    pool.release(parent, length, pt)
+    assert pool.free_pages == 32
+
+
+def test_pool_shared_partial_page_copies_on_write():
+    r = _m()
+    pt = 256
+    pool = r.PagePool(8)
+    row = np.array([pool.alloc(), -1], np.int32)
+    other = row.copy()
+    assert r.PagePool.__dict__  # keep linters calm
+    # share the partial page explicitly (as an engine that shares without forking would)
+    from miinfer_amd._lib import lib
+    assert lib().miikv_pool_ref(pool._h, int(row[0])) == 0
+    copies = pool.prepare_append(other, 100, pt)
+    assert len(copies) == 1 and copies[0][0] == row[0] and other[0] == copies[0][1]
+    assert pool.refcount(row[0]) == 1 and pool.refcount(other[0]) == 1
+
+
+def test_pool_exhaustion_and_bad_pages():
+    r = _m()
+    pool = r.PagePool(2)
+    a, b = pool.alloc(), pool.alloc()
+    with pytest.raises(MemoryError):
+        pool.alloc()
+    from miinfer_amd import MiikvError
+    with pytest.raises(MiikvError):  # fork of a partial page needs a free page
+        pool.fork(np.array([a], np.int32), 10, 256)
+    assert pool.refcount(a) == 1  # a failed fork changes nothing
+    with pytest.raises(MiikvError):
+        pool.release(np.array([7], np.int32), 10, 256)
+    pool.release(np.array([a, b], np.int32), 300, 256)
+    assert pool.free_pages == 2
