@@ -222,6 +222,97 @@ def bench_c4(dev, args) -> int:
     return 0
 
 
+def bench_c5(dev, args) -> int:
+    """Config 5: 64 sessions forked from a shared 32768-token prefix of a hybrid model:
+    16 attention layers (4 kv heads x D256 q8_0, 256-token pages) and 48 GDN layers
+    (fp32 state 16x128x128 + conv 8192x3).  Each fork shares the prefix pages (block
+    table + reference counts), copies the last partial page (copy-on-write), and clones
+    the full recurrent state.  Timed: the device work of all 64 forks."""
+    import numpy as np
+    import torch
+
+    import miinfer_amd as m
+    from miinfer_amd import reuse
+    hkv, d, pt, layers_attn, forks = 4, 256, 256, 16, 64
+    state, conv, layers_gdn = 16 * 128 * 128, 8192 * 3, 48
+    results = {}
+    for prefix in (32768, 32768 - 100):
+        pages = (prefix + pt - 1) // pt
+        npool = pages + forks + 1
+        caches, pools, tables = [], [], []
+        for _ in range(layers_attn):
+            pool = reuse.PagePool(npool)
+            row = np.array([pool.alloc() for _ in range(pages)], np.int32)
+            cache = m.KvCache.paged_cache(hkv, d, npool, torch.from_numpy(row[None]).to(dev),
+                                          page_tokens=pt, device=dev)
+            for t in (cache.k_codes, cache.v_codes):
+                t.copy_(torch.randint(-128, 128, t.shape, dtype=torch.int8, device=dev))
+            for t in (cache.k_scales, cache.v_scales):
+                t.copy_(torch.randint(0, 2**15, t.shape, dtype=torch.int16, device=dev))
+            caches.append(cache)
+            pools.append(pool)
+            tables.append(row)
+        parent = reuse.RecurrentStates(layers_gdn, state, conv, device=dev)
+        parent.buf.copy_(torch.randn(parent.buf.numel(), device=dev))
+        kids = [reuse.RecurrentStates(layers_gdn, state, conv, device=dev) for _ in range(forks)]
+        # host planning: 64 forks per attention layer
+        t0 = time.perf_counter()
+        copies = []
+        for li in range(layers_attn):
+            cl = []
+            for _ in range(forks):
+                _, cp = pools[li].fork(tables[li], prefix, pt)
+                cl += cp
+            copies.append(cl)
+        host_s = time.perf_counter() - t0
+        src = [torch.tensor([c[0] for c in cl], dtype=torch.int32, device=dev) for cl in copies]
+        dst = [torch.tensor([c[1] for c in cl], dtype=torch.int32, device=dev) for cl in copies]
+        ptrs = torch.tensor([k.buf.data_ptr() for k in kids], dtype=torch.int64, device=dev)
+        import ctypes
+
+        from miinfer_amd import _lib
+        L = _lib.lib()
+
+        def device_work(s):
+            for li in range(layers_attn):
+                if len(copies[li]):
+                    assert L.miikv_copy_pages(caches[li].view, ctypes.c_void_p(src[li].data_ptr()),
+                                              ctypes.c_void_p(dst[li].data_ptr()), len(copies[li]),
+                                              ctypes.c_void_p(s.cuda_stream)) == 0
+            assert L.miikv_clone_state(ctypes.c_void_p(ptrs.data_ptr()),
+                                       ctypes.c_void_p(parent.buf.data_ptr()), parent.nbytes, forks,
+                                       ctypes.c_void_p(s.cuda_stream)) == 0
+        torch.cuda.synchronize()
+        us, n = _time_graph(device_work, max(5, args.steps // 200), 3)
+        # byte-exact spot checks of the timed work
+        assert torch.equal(kids[-1].buf.view(torch.int32), parent.buf.view(torch.int32))
+        if copies[0]:
+            s0, d0 = copies[0][-1]
+            per = caches[0].k_codes.numel() // npool
+            assert torch.equal(caches[0].k_codes.view(npool, per)[d0], caches[0].k_codes.view(npool, per)[s0])
+        page_bytes = 2 * hkv * pt * (d + d // 16)
+        cow = sum(len(c) for c in copies) * page_bytes * 2
+        clone = parent.nbytes * (1 + forks)
+        results[str(prefix)] = {
+            "us": round(us, 1), "GBs": round((cow + clone) / (us * 1e-6) / 1e9, 1),
+            "cow_pages": sum(len(c) for c in copies), "cow_bytes_rw": cow, "clone_bytes_rw": clone,
+            "host_planning_us": round(host_s * 1e6, 1)}
+        del caches, kids, parent
+        torch.cuda.empty_cache()
+    main_r = results[str(32768 - 100)]
+    print(json.dumps({
+        "metric": "fork 64 sessions: CoW pages + recurrent-state clone, GB/s (config 5)",
+        "unit": "GB/s", "value": main_r["GBs"], "n_gpus": 1,
+        "config": {"workload": "config 5: 64 forks, 16 attn layers (4kv x D256 q8_0, 256-token "
+                               "pages) + 48 GDN layers (16x128x128 + 8192x3 fp32)"},
+        "by_prefix_tokens": results,
+        "roofline": {"bound": "hbm", "kernel": "copy_pages_kernel + clone_state_kernel",
+                     "achieved": main_r["GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(main_r["GBs"] / PEAK_HBM_GBS, 4)},
+    }), flush=True)
+    return 0
+
+
 def calibrate_copy(dev) -> int:
     """A plain 256 MiB device-to-device copy through miikv_copy_segments: its
     FETCH_SIZE / WRITE_SIZE under rocprofv3 --pmc give the counter scale factor."""
@@ -296,7 +387,7 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
-    ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4"],
+    ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "c5"],
                     help="c2 (default, the headline metric); c3 paged batched decode; c4 suffix "
                          "attention (these print their own JSON line, not the headline)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -319,6 +410,8 @@ def main() -> int:
         return bench_c3(dev, args)
     if args.workload == "c4":
         return bench_c4(dev, args)
+    if args.workload == "c5":
+        return bench_c5(dev, args)
     ctx, nl = args.context, args.layers
     torch.manual_seed(0)
     caches = []
