@@ -187,6 +187,8 @@ def bench_c4(dev, args) -> int:
     out = torch.empty((t, hq, d), device=dev)
     L = _lib.lib()
     P = ctypes.c_void_p
+    ws_bytes = m.suffix_workspace_bytes(cache, hq, t)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
 
     def append(s):
         assert L.miikv_append_f16(cache.view, P(kn.data_ptr()), P(vn.data_ptr()), t, prefix, 0,
@@ -195,7 +197,8 @@ def bench_c4(dev, args) -> int:
     def attn(s):
         assert L.miikv_suffix_attn(cache.view, P(q.data_ptr()), _lib.DTYPE_F16, hq,
                                    ctypes.c_float(1 / math.sqrt(d)), t, prefix, 0, None,
-                                   P(out.data_ptr()), None, None, None, 0, P(s.cuda_stream)) == 0
+                                   P(out.data_ptr()), None, None, P(ws.data_ptr()), ws_bytes,
+                                   P(s.cuda_stream)) == 0
 
     def step(s):
         append(s)
@@ -216,6 +219,7 @@ def bench_c4(dev, args) -> int:
                      "achieved": round(flops / (us_attn * 1e-6) / 1e12, 2), "peak": 2500.0,
                      "unit": "TFLOP/s", "frac": round(flops / (us_attn * 1e-6) / 1e12 / 2500.0, 4),
                      "algorithmic_flops_per_launch": flops, "avg_launch_us": round(us_attn, 2)},
+        "split_workspace_bytes": ws_bytes,
         "append": {"us": round(us_app, 2), "rows": t * hkv,
                    "GBs": round(t * append_bytes(hkv, d) / (us_app * 1e-6) / 1e9, 1)},
     }), flush=True)

@@ -14,9 +14,10 @@ from .kv import (  # noqa: F401
     make_decode_state,
     make_prefill_state,
     suffix_attention,
+    suffix_workspace_bytes,
 )
 
 __all__ = [
     "MiikvError", "lib", "KvCache", "DecodeWorkspace", "decode_attention", "clone_state",
-    "copy_segments", "make_decode_state", "make_prefill_state", "suffix_attention",
+    "copy_segments", "make_decode_state", "make_prefill_state", "suffix_attention", "suffix_workspace_bytes",
 ]

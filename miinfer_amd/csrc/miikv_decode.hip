@@ -28,6 +28,7 @@
 // L = sum l_s e^{m_s-g}, out = sum acc_s e^{m_s-g} / L, 0 when L == 0,
 // gated = out * sigmoid(gate).
 #include "miikv_common.hpp"
+#include "miikv_split.hpp"
 
 #include <cmath>
 #include <cstdlib>
@@ -40,9 +41,6 @@ uint64_t view_seq_capacity(const miikv_view* v);
 
 namespace {
 
-#ifndef MIIKV_WPW
-#define MIIKV_WPW 4
-#endif
 // Pipeline depth (32-token steps held in registers) and the occupancy it is tuned for.
 #ifndef MIIKV_RING_D128
 #define MIIKV_RING_D128 3
@@ -59,29 +57,11 @@ namespace {
 #ifndef MIIKV_VBIAS_D256
 #define MIIKV_VBIAS_D256 1
 #endif
-constexpr uint32_t kWavesPerWg = MIIKV_WPW;
 constexpr uint32_t kTargetWaves = 256 * 8;  // 256 CUs x 8 resident waves
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kCodeBias = 1152.0f;  // codes enter the MFMA as fp16(code + 1152)
 constexpr float kRescaleSlack = 6.0f;  // log2 units: p <= 64, and 64 * (65504/127) < 65504
 
-struct DecodeArgs {
-    Geo g;
-    const void* q;
-    uint32_t q_heads;
-    uint32_t group;  // query heads per kv head (<= 16)
-    float scale_log2;
-    const uint32_t* len_ptr;
-    uint32_t len_stride;
-    uint32_t len_add;
-    uint32_t max_context;
-    uint32_t cpw;         // chunks per wave
-    uint32_t max_splits;  // == gridDim.x
-    float* part;          // [batch][kv_heads][max_splits][group*(D+2)]
-    float* out;
-    const float* gate;
-    float* gated_out;
-};
 
 // Streaming loads of cache codes: each byte is read once per launch, so they are
 // issued nontemporal (measured ~5% faster than cached loads at 32k context).
@@ -102,7 +82,6 @@ __device__ __forceinline__ float wave_max_xor_16_32(float x) {
     return x;
 }
 
-__device__ __forceinline__ float exp2_safe(float x) { return exp2f(x); }  // exp2(-inf) == 0
 // Raw v_exp_f32: no denormal range fix-up (results below 2^-126 flush to 0, which
 // only drops probabilities that are already negligible); exp2(-inf) == 0.
 #ifdef MIIKV_EXP_EXP2F
@@ -111,14 +90,10 @@ __device__ __forceinline__ float fast_exp2(float x) { return exp2f(x); }
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 #endif
 
-// Floats in one split's partial record: O [G*D], m [G], l [G], padded to 4.
-__host__ __device__ __forceinline__ uint32_t record_floats(uint32_t G, uint32_t D) {
-    return G * D + ((2 * G + 3) / 4) * 4;
-}
 
 template <uint32_t D, bool QF32>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? MIIKV_WPE_D128 : MIIKV_WPE_D256)))
-decode_kernel(DecodeArgs a) {
+decode_kernel(SplitArgs a) {
     constexpr uint32_t NB = D / 32;   // q8_0 blocks per row
     constexpr uint32_t NC = D / 64;   // 16-byte K loads per tile row group
     constexpr uint32_t NM = D / 16;   // V M-tiles (16 dims each)
@@ -189,8 +164,7 @@ decode_kernel(DecodeArgs a) {
     for (uint32_t r = 0; r + 1 < kRing; ++r)
         if (c_begin + r < c_end_max) load_step(S[r]);
 
-    uint32_t L = a.len_ptr[static_cast<size_t>(b) * a.len_stride] + a.len_add;
-    if (L > a.max_context) L = a.max_context;
+    const uint32_t L = split_length(a, b);
     const uint32_t tps = kWavesPerWg * a.cpw * kChunk;
     const uint32_t nsplit = (L + tps - 1) / tps;
     if (split >= nsplit) return;  // includes L == 0 (the combine kernel writes zeros)
@@ -457,112 +431,6 @@ decode_kernel(DecodeArgs a) {
 
 
 
-// Cross-split combine.  Workgroup (sequence * kv_heads + head, element block of 64)
-// reads the partial records of every split of that (sequence, kv head): thread
-// (e4 = tid & 15, sg = tid >> 4) folds splits sg, sg+16, ... for 4 consecutive
-// elements with its own running max, so its loads are independent; the 16 split
-// groups are merged in a fixed order through LDS (deterministic result).
-template <uint32_t D>
-__global__ void __launch_bounds__(256) combine_kernel(DecodeArgs a) {
-    const uint32_t bh = blockIdx.x;
-    const uint32_t b = bh / a.g.kv_heads;
-    const uint32_t h = bh % a.g.kv_heads;
-    const uint32_t G = a.group;
-    const uint32_t GD = G * D;
-    const uint32_t e0 = blockIdx.y * 64;
-    if (e0 >= GD) return;
-    const uint32_t tid = threadIdx.x;
-    const uint32_t e4 = tid & 15;
-    const uint32_t sg = tid >> 4;
-    const uint32_t e = e0 + e4 * 4;
-    const bool active = e < GD;
-    const uint32_t hn = active ? e / D : 0;
-    const size_t out_row0 = (static_cast<size_t>(b) * a.q_heads + static_cast<size_t>(h) * G) * D;
-
-    const uint32_t rec = record_floats(G, D);
-    const float* part = a.part + (static_cast<size_t>(bh) * a.max_splits) * rec;
-
-    // The first kSpec records of this thread are fetched before the context length
-    // (and with it the split count) arrives; records past the count are ignored.
-    constexpr uint32_t kSpec = 4;
-    float ms[kSpec], ls[kSpec];
-    float4 vv[kSpec];
-#pragma unroll
-    for (uint32_t j = 0; j < kSpec; ++j) {
-        const uint32_t sp = sg + 16 * j;
-        ms[j] = -INFINITY;
-        ls[j] = 0.0f;
-        vv[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (sp < a.max_splits) {
-            const float* r = part + static_cast<size_t>(sp) * rec;
-            ms[j] = r[GD + hn];
-            ls[j] = r[GD + G + hn];
-            if (active) vv[j] = *reinterpret_cast<const float4*>(r + e);
-        }
-    }
-    uint32_t L = a.len_ptr[static_cast<size_t>(b) * a.len_stride] + a.len_add;
-    if (L > a.max_context) L = a.max_context;
-    const uint32_t tps = kWavesPerWg * a.cpw * kChunk;
-    const uint32_t nsplit = (L + tps - 1) / tps;
-
-    float mloc = -INFINITY;
-    float lsum = 0.0f;
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    auto merge = [&](float m_s, float l_s, float4 v) {
-        const float mn = fmaxf(mloc, m_s);
-        const float fo = exp2_safe(mloc - mn);  // 0 on the first split
-        const float fs = exp2_safe(m_s - mn);
-        mloc = mn;
-        lsum = lsum * fo + l_s * fs;
-        acc.x = acc.x * fo + v.x * fs;
-        acc.y = acc.y * fo + v.y * fs;
-        acc.z = acc.z * fo + v.z * fs;
-        acc.w = acc.w * fo + v.w * fs;
-    };
-#pragma unroll
-    for (uint32_t j = 0; j < kSpec; ++j)
-        if (sg + 16 * j < nsplit) merge(ms[j], ls[j], vv[j]);
-    for (uint32_t sp = sg + 16 * kSpec; sp < nsplit; sp += 16) {
-        const float* r = part + static_cast<size_t>(sp) * rec;
-        merge(r[GD + hn], r[GD + G + hn],
-              active ? *reinterpret_cast<const float4*>(r + e) : make_float4(0.f, 0.f, 0.f, 0.f));
-    }
-    __shared__ float4 s_acc[16][16];
-    __shared__ float s_gm[16][16];
-    __shared__ float s_gl[16][16];
-    s_acc[sg][e4] = acc;
-    s_gm[sg][e4] = mloc;
-    s_gl[sg][e4] = lsum;
-    __syncthreads();
-    if (sg != 0 || !active) return;
-    float M = -INFINITY;
-#pragma unroll
-    for (uint32_t g = 0; g < 16; ++g) M = fmaxf(M, s_gm[g][e4]);
-    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    float Ls = 0.0f;
-#pragma unroll
-    for (uint32_t g = 0; g < 16; ++g) {
-        const float mg = s_gm[g][e4];
-        if (mg == -INFINITY) continue;  // split group without splits
-        const float f = exp2_safe(mg - M);
-        const float4 v = s_acc[g][e4];
-        o.x += f * v.x;
-        o.y += f * v.y;
-        o.z += f * v.z;
-        o.w += f * v.w;
-        Ls += f * s_gl[g][e4];
-    }
-    // out = acc / L, 0 when L == 0 (qwen3_primitives.hip:2349); gated = out * sigmoid(gate).
-    const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
-    const float vals[4] = {o.x * inv, o.y * inv, o.z * inv, o.w * inv};
-#pragma unroll
-    for (uint32_t k = 0; k < 4; ++k) {
-        const size_t oi = out_row0 + e + k;
-        if (a.out) a.out[oi] = vals[k];
-        if (a.gate && a.gated_out) a.gated_out[oi] = vals[k] * (1.0f / (1.0f + expf(-a.gate[oi])));
-    }
-}
-
 struct Plan {
     uint32_t cpw;
     uint32_t splits;
@@ -650,7 +518,7 @@ extern "C" miikv_status miikv_decode_attn(const miikv_view* view, const void* q,
     if (p.splits > 65535u || batch > 65535u || static_cast<uint64_t>(batch) * view->kv_heads > 0x7fffffffu)
         return MIIKV_EINVAL;
 
-    DecodeArgs a;
+    SplitArgs a;
     a.g = make_geo(*view);
     a.q = q;
     a.q_heads = q_heads;
@@ -665,6 +533,8 @@ extern "C" miikv_status miikv_decode_attn(const miikv_view* view, const void* q,
         a.len_stride = 0;
         a.len_add = 1;
     }
+    a.len_bstep = 0;
+    a.count_ptr = nullptr;
     a.max_context = max_context;
     a.cpw = p.cpw;
     a.max_splits = p.splits;

@@ -1,0 +1,155 @@
+// Split-K partial records and their combine, shared by decode and suffix attention.
+#pragma once
+
+#include "miikv_common.hpp"
+
+namespace miikv {
+namespace {
+
+#ifndef MIIKV_WPW
+#define MIIKV_WPW 4
+#endif
+constexpr uint32_t kWavesPerWg = MIIKV_WPW;
+
+struct SplitArgs {
+    Geo g;
+    const void* q;
+    uint32_t q_heads;
+    uint32_t group;  // query heads per kv head (<= 16)
+    float scale_log2;
+    // Context length of row-set b: (len_ptr ? len_ptr[b * len_stride] : 0) + len_add
+    // + b * len_bstep (decode: per-sequence lengths; suffix: base + t + 1).
+    const uint32_t* len_ptr;
+    uint32_t len_stride;
+    uint32_t len_add;
+    uint32_t len_bstep;
+    const uint32_t* count_ptr;  // if set, row-sets b >= *count_ptr are skipped
+    uint32_t max_context;
+    uint32_t cpw;         // chunks per wave
+    uint32_t max_splits;  // == gridDim.x
+    float* part;          // [batch][kv_heads][max_splits][group*(D+2)]
+    float* out;
+    const float* gate;
+    float* gated_out;
+};
+
+__device__ __forceinline__ float exp2_safe(float x) { return exp2f(x); }  // exp2(-inf) == 0
+
+// Floats in one split's partial record: O [G*D], m [G], l [G], padded to 4.
+__host__ __device__ __forceinline__ uint32_t record_floats(uint32_t G, uint32_t D) {
+    return G * D + ((2 * G + 3) / 4) * 4;
+}
+
+__device__ __forceinline__ uint32_t split_length(const SplitArgs& a, uint32_t b) {
+    uint32_t L = (a.len_ptr ? a.len_ptr[static_cast<size_t>(b) * a.len_stride] : 0u) + a.len_add + b * a.len_bstep;
+    return L > a.max_context ? a.max_context : L;
+}
+
+// Cross-split combine.  Workgroup (sequence * kv_heads + head, element block of 64)
+// reads the partial records of every split of that (sequence, kv head): thread
+// (e4 = tid & 15, sg = tid >> 4) folds splits sg, sg+16, ... for 4 consecutive
+// elements with its own running max, so its loads are independent; the 16 split
+// groups are merged in a fixed order through LDS (deterministic result).
+template <uint32_t D>
+__global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
+    const uint32_t bh = blockIdx.x;
+    const uint32_t b = bh / a.g.kv_heads;
+    const uint32_t h = bh % a.g.kv_heads;
+    const uint32_t G = a.group;
+    const uint32_t GD = G * D;
+    const uint32_t e0 = blockIdx.y * 64;
+    if (e0 >= GD) return;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t e4 = tid & 15;
+    const uint32_t sg = tid >> 4;
+    const uint32_t e = e0 + e4 * 4;
+    const bool active = e < GD;
+    const uint32_t hn = active ? e / D : 0;
+    const size_t out_row0 = (static_cast<size_t>(b) * a.q_heads + static_cast<size_t>(h) * G) * D;
+
+    const uint32_t rec = record_floats(G, D);
+    const float* part = a.part + (static_cast<size_t>(bh) * a.max_splits) * rec;
+
+    // The first kSpec records of this thread are fetched before the context length
+    // (and with it the split count) arrives; records past the count are ignored.
+    constexpr uint32_t kSpec = 4;
+    float ms[kSpec], ls[kSpec];
+    float4 vv[kSpec];
+#pragma unroll
+    for (uint32_t j = 0; j < kSpec; ++j) {
+        const uint32_t sp = sg + 16 * j;
+        ms[j] = -INFINITY;
+        ls[j] = 0.0f;
+        vv[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (sp < a.max_splits) {
+            const float* r = part + static_cast<size_t>(sp) * rec;
+            ms[j] = r[GD + hn];
+            ls[j] = r[GD + G + hn];
+            if (active) vv[j] = *reinterpret_cast<const float4*>(r + e);
+        }
+    }
+    if (a.count_ptr != nullptr && b >= *a.count_ptr) return;
+    uint32_t L = split_length(a, b);
+    const uint32_t tps = kWavesPerWg * a.cpw * kChunk;
+    const uint32_t nsplit = (L + tps - 1) / tps;
+
+    float mloc = -INFINITY;
+    float lsum = 0.0f;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    auto merge = [&](float m_s, float l_s, float4 v) {
+        const float mn = fmaxf(mloc, m_s);
+        const float fo = exp2_safe(mloc - mn);  // 0 on the first split
+        const float fs = exp2_safe(m_s - mn);
+        mloc = mn;
+        lsum = lsum * fo + l_s * fs;
+        acc.x = acc.x * fo + v.x * fs;
+        acc.y = acc.y * fo + v.y * fs;
+        acc.z = acc.z * fo + v.z * fs;
+        acc.w = acc.w * fo + v.w * fs;
+    };
+#pragma unroll
+    for (uint32_t j = 0; j < kSpec; ++j)
+        if (sg + 16 * j < nsplit) merge(ms[j], ls[j], vv[j]);
+    for (uint32_t sp = sg + 16 * kSpec; sp < nsplit; sp += 16) {
+        const float* r = part + static_cast<size_t>(sp) * rec;
+        merge(r[GD + hn], r[GD + G + hn],
+              active ? *reinterpret_cast<const float4*>(r + e) : make_float4(0.f, 0.f, 0.f, 0.f));
+    }
+    __shared__ float4 s_acc[16][16];
+    __shared__ float s_gm[16][16];
+    __shared__ float s_gl[16][16];
+    s_acc[sg][e4] = acc;
+    s_gm[sg][e4] = mloc;
+    s_gl[sg][e4] = lsum;
+    __syncthreads();
+    if (sg != 0 || !active) return;
+    float M = -INFINITY;
+#pragma unroll
+    for (uint32_t g = 0; g < 16; ++g) M = fmaxf(M, s_gm[g][e4]);
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float Ls = 0.0f;
+#pragma unroll
+    for (uint32_t g = 0; g < 16; ++g) {
+        const float mg = s_gm[g][e4];
+        if (mg == -INFINITY) continue;  // split group without splits
+        const float f = exp2_safe(mg - M);
+        const float4 v = s_acc[g][e4];
+        o.x += f * v.x;
+        o.y += f * v.y;
+        o.z += f * v.z;
+        o.w += f * v.w;
+        Ls += f * s_gl[g][e4];
+    }
+    // out = acc / L, 0 when L == 0 (qwen3_primitives.hip:2349); gated = out * sigmoid(gate).
+    const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
+    const float vals[4] = {o.x * inv, o.y * inv, o.z * inv, o.w * inv};
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) {
+        const size_t oi = out_row0 + e + k;
+        if (a.out) a.out[oi] = vals[k];
+        if (a.gate && a.gated_out) a.gated_out[oi] = vals[k] * (1.0f / (1.0f + expf(-a.gate[oi])));
+    }
+}
+
+}  // namespace
+}  // namespace miikv

@@ -12,11 +12,19 @@
 //   S^T[key][row] = K^_tile (16 keys x D) * Q^T (D x 16 rows)   v_mfma_f32_16x16x32_f16
 //   O^T[dim][row] += V^T (16 dims x 16 keys) * P^T              v_mfma_f32_16x16x16_f16
 // the S^T fragment being the P^T operand layout, as in the decode kernel.
-// Online softmax in the log2 domain with a lazy running max; each row
-// normalises at the end, so no cross-workgroup combine is needed.
+// Online softmax in the log2 domain with a lazy running max.
+//
+// Split-K: grid.z cuts the key range into splits of a fixed number of keys so
+// that a short suffix still fills the chip.  With one split the workgroup
+// normalises and stores its rows; otherwise each (token, kv head, split) writes
+// a partial record (unnormalised O, running max, sum) and the decode path's
+// combine kernel merges them with token t's context length P + t + 1.
 #include "miikv_common.hpp"
+#include "miikv_split.hpp"
 
+#include <algorithm>
 #include <cmath>
+#include <cstdlib>
 
 namespace miikv {
 
@@ -29,6 +37,8 @@ constexpr uint32_t kSufRows = 64;      // query rows per workgroup
 constexpr uint32_t kSufStep = 32;      // keys per step
 constexpr float kLog2eS = 1.4426950408889634f;
 constexpr float kSlackS = 6.0f;        // lazy-rescale threshold (log2 units): p <= 64
+constexpr uint32_t kSufTargetWgs = 1024; // ~4 resident workgroups per CU over 256 CUs
+constexpr uint32_t kSufMaxSplits = 64;
 
 struct SuffixArgs {
     Geo g;
@@ -41,6 +51,9 @@ struct SuffixArgs {
     uint32_t base_position;
     uint32_t seq;
     const miikv_prefill_state* ps;
+    uint32_t split_keys;   // keys per split (multiple of kSufStep)
+    uint32_t splits;       // == gridDim.z
+    float* part;           // partial records when splits > 1
     float* out;
     const float* gate;
     float* gated_out;
@@ -48,8 +61,12 @@ struct SuffixArgs {
 
 __device__ __forceinline__ float sfx_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-__device__ __forceinline__ _Float16 to_half_sat(float x) {
-    return static_cast<_Float16>(fminf(fmaxf(x, -65504.0f), 65504.0f));
+// code * scale rounded once to fp16 (the code is exact in fp16), saturated to the
+// finite range: 127 * fp16(amax / 127) can exceed 65504 for amax near the fp16 max.
+template <typename V>
+__device__ __forceinline__ V scale_sat(V codes, V scales) {
+    const V lim = (V)(_Float16)65504.0f;
+    return __builtin_elementwise_min(__builtin_elementwise_max(codes * scales, -lim), lim);
 }
 
 template <uint32_t D>
@@ -93,7 +110,12 @@ __global__ void __launch_bounds__(256) suffix_kernel(SuffixArgs a) {
     // Keys the whole workgroup needs: up to the last row's limit.
     const uint32_t last_row = min(r0 + kSufRows, rows) - 1;
     const uint32_t nkeys = P + last_row / G + 1;
-    const uint32_t nsteps = (nkeys + kSufStep - 1) / kSufStep;
+    const uint32_t split = blockIdx.z;
+    const uint32_t key_lo = split * a.split_keys;
+    if (key_lo >= nkeys) return;  // no row of this workgroup has keys in this split
+    const uint32_t key_hi = min(nkeys, key_lo + a.split_keys);
+    const uint32_t s_begin = key_lo / kSufStep;
+    const uint32_t s_end = (key_hi + kSufStep - 1) / kSufStep;
 
     // ---- Q fragments (B operand): head qh of token t_row, dims 32*blk + 8*g4 .. +7.
     half8 qf[NB];
@@ -168,13 +190,8 @@ __global__ void __launch_bounds__(256) suffix_kernel(SuffixArgs a) {
 #pragma unroll
             for (uint32_t e = 0; e < 2; ++e) {
                 const uint32_t blk = 2 * c + e;
-                const float sc = f16_bits_to_f32(s_ks[key * NB + blk]);
-                half8 hv;
-#pragma unroll
-                for (uint32_t j = 0; j < 8; ++j) {
-                    const int code = static_cast<int8_t>((w[2 * e + j / 4] >> (8 * (j % 4))) & 0xffu);
-                    hv[j] = to_half_sat(static_cast<float>(code) * sc);
-                }
+                const half8 scv = (half8)__builtin_bit_cast(_Float16, s_ks[key * NB + blk]);
+                const half8 hv = scale_sat(codes8_to_half8(w[2 * e], w[2 * e + 1]), scv);
                 *reinterpret_cast<half8*>(&s_k[buf][key * KPAD + 64 * c + 32 * e + 8 * gq]) = hv;
             }
         }
@@ -186,13 +203,8 @@ __global__ void __launch_bounds__(256) suffix_kernel(SuffixArgs a) {
             const uint32_t w[2] = {st.v[u].x, st.v[u].y};
 #pragma unroll
             for (uint32_t J = 0; J < 2; ++J) {
-                half4 hv;
-#pragma unroll
-                for (uint32_t I = 0; I < 4; ++I) {
-                    const uint32_t key = 16 * J + 4 * Gq + I;
-                    const int code = static_cast<int8_t>((w[J] >> (8 * I)) & 0xffu);
-                    hv[I] = to_half_sat(static_cast<float>(code) * f16_bits_to_f32(s_vs[blk * kSufStep + key]));
-                }
+                const half4 scv = *reinterpret_cast<const half4*>(&s_vs[blk * kSufStep + 16 * J + 4 * Gq]);
+                const half4 hv = scale_sat(codes4_to_half4(w[J]), scv);
                 *reinterpret_cast<half4*>(&s_v[buf][d * VPAD + 16 * J + 4 * Gq]) = hv;
             }
         }
@@ -205,15 +217,15 @@ __global__ void __launch_bounds__(256) suffix_kernel(SuffixArgs a) {
     for (uint32_t mt = 0; mt < NM; ++mt) O[mt] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 
     Stage st;
-    load_stage(0, st);
-    stage_scales(0, st);
+    load_stage(s_begin, st);
+    stage_scales(s_begin, st);
     __syncthreads();
-    stage_tiles(0, st);
+    stage_tiles(s_begin & 1, st);
     __syncthreads();
 
-    for (uint32_t s = 0; s < nsteps; ++s) {
+    for (uint32_t s = s_begin; s < s_end; ++s) {
         const uint32_t buf = s & 1;
-        const bool more = s + 1 < nsteps;
+        const bool more = s + 1 < s_end;
         if (more) load_stage(s + 1, st);  // in flight during this step's MFMAs
 
         const uint32_t key0 = s * kSufStep;
@@ -231,7 +243,7 @@ __global__ void __launch_bounds__(256) suffix_kernel(SuffixArgs a) {
 #pragma unroll
             for (uint32_t i = 0; i < 4; ++i) {
                 const uint32_t key = key0 + 16 * J + 4 * g4 + i;
-                sc[J][i] = (key <= lim && row_ok) ? acc[i] * a.scale_log2 : -INFINITY;
+                sc[J][i] = (key <= lim && key < key_hi && row_ok) ? acc[i] * a.scale_log2 : -INFINITY;
             }
         }
         // ---- online softmax (per row n; lanes of the 4 groups share it)
@@ -251,12 +263,14 @@ __global__ void __launch_bounds__(256) suffix_kernel(SuffixArgs a) {
 #pragma unroll
             for (uint32_t mt = 0; mt < NM; ++mt) O[mt] *= alpha;
         }
+        // A row with no visible key yet keeps m_run = -inf; subtracting 0 keeps p = 0.
+        const float m_use = m_run == -INFINITY ? 0.0f : m_run;
         half4 pb[2];
 #pragma unroll
         for (uint32_t J = 0; J < 2; ++J)
 #pragma unroll
             for (uint32_t i = 0; i < 4; ++i) {
-                const float p = sfx_exp2(sc[J][i] - m_run);  // 0 for masked keys
+                const float p = sfx_exp2(sc[J][i] - m_use);  // 0 for masked keys
                 l_run += p;
                 pb[J][i] = static_cast<_Float16>(p);
             }
@@ -281,6 +295,22 @@ __global__ void __launch_bounds__(256) suffix_kernel(SuffixArgs a) {
     l_run += __shfl_xor(l_run, 16, 64);
     l_run += __shfl_xor(l_run, 32, 64);
     if (!row_ok) return;
+    if (a.splits > 1) {
+        // Partial record of (token t_row, kv head h, split): O [G][D], m [G], l [G].
+        const uint32_t G_ = a.group;
+        float* rec = a.part + ((static_cast<size_t>(t_row) * geo.kv_heads + h) * a.splits + split) *
+                                  record_floats(G_, D);
+        const uint32_t gi = qh - h * G_;
+#pragma unroll
+        for (uint32_t mt = 0; mt < NM; ++mt)
+            *reinterpret_cast<float4*>(rec + gi * D + 16 * mt + 4 * g4) =
+                make_float4(O[mt][0], O[mt][1], O[mt][2], O[mt][3]);
+        if (g4 == 0) {
+            rec[G_ * D + gi] = m_run;
+            rec[G_ * D + G_ + gi] = l_run;
+        }
+        return;
+    }
     const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
     const size_t orow = (static_cast<size_t>(t_row) * a.q_heads + qh) * D;
 #pragma unroll
@@ -309,11 +339,44 @@ __global__ void __launch_bounds__(256) suffix_kernel(SuffixArgs a) {
 
 using namespace miikv;
 
+namespace {
+
+struct SuffixPlan {
+    uint32_t splits;
+    uint32_t split_keys;
+    uint64_t part_bytes;
+};
+
+// Split count for a suffix of `tokens` tokens whose keys end at or before
+// `key_bound`: enough workgroups to fill the chip, at least 256 keys per split.
+// Monotone in key_bound, so a plan made with the cache capacity covers any
+// smaller context.
+SuffixPlan make_suffix_plan(const miikv_view* v, uint32_t q_heads, uint32_t tokens, uint64_t key_bound) {
+    SuffixPlan p{1, 0, 0};
+    const uint32_t G = q_heads / v->kv_heads;
+    const uint64_t wgs = (static_cast<uint64_t>(tokens) * G + kSufRows - 1) / kSufRows * v->kv_heads;
+    uint64_t want = (kSufTargetWgs + wgs - 1) / wgs;
+    if (const char* e = std::getenv("MIIKV_SUFFIX_SPLITS")) want = std::strtoul(e, nullptr, 10);
+    const uint64_t by_keys = (key_bound + 255) / 256;
+    want = std::min<uint64_t>({want, by_keys, kSufMaxSplits});
+    if (want <= 1) return p;
+    const uint64_t unit = kWavesPerWg * kChunk;  // the combine's split granularity (128 keys)
+    const uint64_t cpw = (key_bound + want * unit - 1) / (want * unit);
+    p.split_keys = static_cast<uint32_t>(cpw * unit);
+    p.splits = static_cast<uint32_t>((key_bound + p.split_keys - 1) / p.split_keys);
+    if (p.splits <= 1) return SuffixPlan{1, 0, 0};
+    p.part_bytes = static_cast<uint64_t>(tokens) * v->kv_heads * p.splits * record_floats(G, v->head_dim) * 4;
+    return p;
+}
+
+}  // namespace
+
+// Workspace for the split-K path: partial records of every (token, kv head, split),
+// planned for the cache capacity (any base position fits).  0 when one split suffices.
 extern "C" uint64_t miikv_suffix_workspace_bytes(const miikv_view* view, uint32_t q_heads, uint32_t token_count) {
-    (void)view;
-    (void)q_heads;
-    (void)token_count;
-    return 0;  // each workgroup covers all keys of its rows: no partials
+    if (validate_view(view) != MIIKV_OK || q_heads == 0 || q_heads % view->kv_heads != 0 || token_count == 0)
+        return 0;
+    return make_suffix_plan(view, q_heads, token_count, view_seq_capacity(view)).part_bytes;
 }
 
 extern "C" miikv_status miikv_suffix_attn(const miikv_view* view, const void* q, uint32_t q_dtype, uint32_t q_heads,
@@ -321,8 +384,6 @@ extern "C" miikv_status miikv_suffix_attn(const miikv_view* view, const void* q,
                                           const miikv_prefill_state* prefill_state, float* out, const float* gate,
                                           float* gated_out, void* workspace, uint64_t workspace_bytes,
                                           void* stream) {
-    (void)workspace;
-    (void)workspace_bytes;
     const int st = validate_view(view);
     if (st != MIIKV_OK) return st;
     if (q == nullptr || q_heads == 0 || q_heads % view->kv_heads != 0 || !std::isfinite(scale)) return MIIKV_EINVAL;
@@ -332,11 +393,20 @@ extern "C" miikv_status miikv_suffix_attn(const miikv_view* view, const void* q,
     if ((gate == nullptr) != (gated_out == nullptr)) return MIIKV_EINVAL;
     if (view->layout == MIIKV_LAYOUT_CONTIGUOUS && seq != 0) return MIIKV_EINVAL;
     if (token_count == 0) return MIIKV_OK;
-    if (prefill_state == nullptr && static_cast<uint64_t>(base_position) + token_count > view_seq_capacity(view))
-        return MIIKV_EINVAL;
+    const uint64_t cap = view_seq_capacity(view);
+    if (prefill_state == nullptr && static_cast<uint64_t>(base_position) + token_count > cap) return MIIKV_EINVAL;
     const uint64_t rows = static_cast<uint64_t>(token_count) * G;
     const uint64_t blocks = (rows + kSufRows - 1) / kSufRows;
-    if (blocks > 0x7fffffffu) return MIIKV_EINVAL;
+    if (blocks > 0x7fffffffu || static_cast<uint64_t>(token_count) * view->kv_heads > 0x7fffffffu)
+        return MIIKV_EINVAL;
+    // Without a workspace the kernel runs one split; with one, the plan for the
+    // known context (host base position) or for the capacity (device state).
+    SuffixPlan plan{1, 0, 0};
+    if (workspace != nullptr) {
+        const uint64_t bound = prefill_state ? cap : static_cast<uint64_t>(base_position) + token_count;
+        plan = make_suffix_plan(view, q_heads, token_count, bound);
+        if (workspace_bytes < plan.part_bytes) return MIIKV_EWORKSPACE;
+    }
     SuffixArgs a;
     a.g = make_geo(*view);
     a.q = q;
@@ -348,12 +418,37 @@ extern "C" miikv_status miikv_suffix_attn(const miikv_view* view, const void* q,
     a.base_position = base_position;
     a.seq = seq;
     a.ps = prefill_state;
+    a.split_keys = plan.splits > 1 ? plan.split_keys : 0xffffffffu;
+    a.splits = plan.splits;
+    a.part = static_cast<float*>(workspace);
     a.out = out;
     a.gate = gate;
     a.gated_out = gated_out;
-    const dim3 grid(static_cast<uint32_t>(blocks), view->kv_heads);
+    const dim3 grid(static_cast<uint32_t>(blocks), view->kv_heads, plan.splits);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (view->head_dim == 128) hipLaunchKernelGGL(suffix_kernel<128>, grid, dim3(256), 0, s, a);
     else hipLaunchKernelGGL(suffix_kernel<256>, grid, dim3(256), 0, s, a);
+    if (plan.splits > 1) {
+        // Token t of the suffix sees P + t + 1 keys; rows past the device token count are skipped.
+        SplitArgs c{};
+        c.g = a.g;
+        c.q_heads = q_heads;
+        c.group = G;
+        c.len_ptr = prefill_state ? &prefill_state->base_position : nullptr;
+        c.len_stride = 0;
+        c.len_add = (prefill_state ? 0u : base_position) + 1u;
+        c.len_bstep = 1;
+        c.count_ptr = prefill_state ? &prefill_state->token_count : nullptr;
+        c.max_context = static_cast<uint32_t>(std::min<uint64_t>(cap, 0xffffffffu));
+        c.cpw = plan.split_keys / (kWavesPerWg * kChunk);
+        c.max_splits = plan.splits;
+        c.part = a.part;
+        c.out = out;
+        c.gate = gate;
+        c.gated_out = gated_out;
+        const dim3 cgrid(token_count * view->kv_heads, (G * view->head_dim + 63) / 64);
+        if (view->head_dim == 128) hipLaunchKernelGGL(combine_kernel<128>, cgrid, dim3(256), 0, s, c);
+        else hipLaunchKernelGGL(combine_kernel<256>, cgrid, dim3(256), 0, s, c);
+    }
     return hip_status(hipGetLastError());
 }

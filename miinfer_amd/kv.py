@@ -296,9 +296,14 @@ def decode_attention(cache: KvCache, q: torch.Tensor, scale: float | None = None
 def suffix_attention(cache: KvCache, q: torch.Tensor, base_position: int, scale: float | None = None,
                      *, seq: int = 0, prefill_state: torch.Tensor | None = None,
                      gate: torch.Tensor | None = None, out: torch.Tensor | None = None,
-                     gated_out: torch.Tensor | None = None, stream=None):
+                     gated_out: torch.Tensor | None = None, split: bool = True,
+                     workspace: torch.Tensor | None = None, stream=None):
     """Causal attention of a T-token suffix (rows already appended at base_position..)
-    over the cache.  q: [T, q_heads, head_dim] fp16/fp32.  Returns (out, gated_out)."""
+    over the cache.  q: [T, q_heads, head_dim] fp16/fp32.  Returns (out, gated_out).
+
+    split=True runs split-K over the key range with a workspace of
+    suffix_workspace_bytes() (allocated here unless given); split=False runs one
+    workgroup per row block over all its keys."""
     t, q_heads, d = q.shape
     if d != cache.head_dim or not q.is_contiguous() or q.dtype not in (torch.float16,
                                                                         torch.float32):
@@ -317,10 +322,20 @@ def suffix_attention(cache: KvCache, q: torch.Tensor, base_position: int, scale:
     if gate is not None and gated_out is None:
         gated_out = torch.empty((t, q_heads, d), dtype=torch.float32, device=q.device)
     qd = _lib.DTYPE_F16 if q.dtype == torch.float16 else _lib.DTYPE_F32
+    ws_bytes = 0
+    if split:
+        if workspace is None:
+            need = suffix_workspace_bytes(cache, q_heads, t)
+            workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+        ws_bytes = workspace.numel() * workspace.element_size()
     call("miikv_suffix_attn", cache.view, _ptr(q), qd, q_heads, float(scale), t, base_position,
-         seq, _ptr(prefill_state), _ptr(out), _ptr(gate), _ptr(gated_out), None, 0,
-         _stream(stream))
+         seq, _ptr(prefill_state), _ptr(out), _ptr(gate), _ptr(gated_out),
+         _ptr(workspace) if split else None, ws_bytes, _stream(stream))
     return out, gated_out
+
+
+def suffix_workspace_bytes(cache: KvCache, q_heads: int, tokens: int) -> int:
+    return int(lib().miikv_suffix_workspace_bytes(cache.view, q_heads, tokens))
 
 
 def make_decode_state(position: int, device="cuda") -> torch.Tensor:

@@ -32,8 +32,10 @@ def _setup(gpu, rng, hq, hk, d, prefix, t, cap):
 
 @pytest.mark.parametrize("hq,hk,d,prefix,t", [(24, 4, 256, 300, 40), (32, 8, 128, 1000, 64),
                                               (24, 4, 256, 0, 17), (6, 1, 128, 64, 1),
-                                              (24, 4, 256, 257, 33)])
-def test_suffix_small(gpu, hq, hk, d, prefix, t):
+                                              (24, 4, 256, 257, 33), (24, 4, 256, 5000, 3),
+                                              (8, 8, 128, 3000, 130)])
+@pytest.mark.parametrize("split", [True, False])
+def test_suffix_small(gpu, hq, hk, d, prefix, t, split):
     import miinfer_amd as m
     rng = np.random.default_rng(prefix + t + d)
     cap = ((prefix + t + 63) // 64) * 64
@@ -41,14 +43,15 @@ def test_suffix_small(gpu, hq, hk, d, prefix, t):
     q = randn_f16(rng, (t, hq, d))
     gate = rng.standard_normal((t, hq, d)).astype(np.float32)
     out, gated = m.suffix_attention(cache, _dev(q, gpu), prefix, gate=_dev(gate, gpu),
-                                    out=torch.empty((t, hq, d), device=gpu))
+                                    out=torch.empty((t, hq, d), device=gpu), split=split)
     torch.cuda.synchronize()
     expect = oracle.suffix_attention_q8(q.astype(np.float32), *ref, prefix, hq, 1 / math.sqrt(d))
     assert_attention_close(out.cpu().numpy(), expect, "suffix")
     assert_attention_close(gated.cpu().numpy(), expect / (1 + np.exp(-gate)), "suffix gated")
 
 
-def test_suffix_config4_full_size_sampled_tokens(gpu):
+@pytest.mark.parametrize("split", [True, False])
+def test_suffix_config4_full_size_sampled_tokens(gpu, split):
     """Config 4: 512 suffix tokens over an 8192-token prefix (24q/4kv/D256); the oracle
     checks a sample of tokens (each is an independent causal row set)."""
     import miinfer_amd as m
@@ -56,7 +59,9 @@ def test_suffix_config4_full_size_sampled_tokens(gpu):
     rng = np.random.default_rng(4)
     cache, ref = _setup(gpu, rng, hq, hk, d, prefix, t, prefix + t)
     q = randn_f16(rng, (t, hq, d))
-    out, _ = m.suffix_attention(cache, _dev(q, gpu), prefix)
+    if split:
+        assert m.suffix_workspace_bytes(cache, hq, t) > 0
+    out, _ = m.suffix_attention(cache, _dev(q, gpu), prefix, split=split)
     torch.cuda.synchronize()
     out = out.cpu().numpy()
     for tok in (0, 1, 63, 64, 255, 511):
@@ -65,7 +70,8 @@ def test_suffix_config4_full_size_sampled_tokens(gpu):
         assert_attention_close(out[tok], expect, f"token {tok}")
 
 
-def test_suffix_prefill_state_and_paged(gpu):
+@pytest.mark.parametrize("split", [True, False])
+def test_suffix_prefill_state_and_paged(gpu, split):
     import miinfer_amd as m
     rng = np.random.default_rng(8)
     hq, hk, d, pt = 24, 4, 256, 256
@@ -81,10 +87,37 @@ def test_suffix_prefill_state_and_paged(gpu):
     q = randn_f16(rng, (t + 20, hq, d))  # host bound 120 rows, device says 100
     ps = m.make_prefill_state(prefix, t, device=gpu)
     out = torch.full((t + 20, hq, d), 5.0, device=gpu)
-    m.suffix_attention(cache, _dev(q, gpu), 0, prefill_state=ps, out=out)
+    m.suffix_attention(cache, _dev(q, gpu), 0, prefill_state=ps, out=out, split=split)
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     expect = oracle.suffix_attention_q8(q[:t].astype(np.float32), kc, ks, vc, vs, prefix, hq,
                                         1 / math.sqrt(d))
     assert_attention_close(got[:t], expect, "paged suffix")
     assert np.all(got[t:] == 5.0)  # rows past the device token count untouched
+
+
+def test_suffix_split_matches_unsplit(gpu):
+    """Split-K and single-split results agree closely: same fp16 tiles and MFMAs; only the
+    running max (and so the fp16 rounding of each probability) and the summation order
+    differ.  Probabilities carry 2^-11 relative rounding, so 2e-4 absolute bounds it."""
+    import miinfer_amd as m
+    rng = np.random.default_rng(11)
+    hq, hk, d, prefix, t = 32, 8, 128, 4000, 96
+    cache, _ = _setup(gpu, rng, hq, hk, d, prefix, t, prefix + t + 64)
+    q = _dev(randn_f16(rng, (t, hq, d)), gpu)
+    a, _ = m.suffix_attention(cache, q, prefix, split=True)
+    b, _ = m.suffix_attention(cache, q, prefix, split=False)
+    torch.cuda.synchronize()
+    assert torch.allclose(a, b, atol=2e-4, rtol=1e-3), (a - b).abs().max().item()
+
+
+def test_suffix_workspace_too_small_is_rejected(gpu):
+    import miinfer_amd as m
+    rng = np.random.default_rng(12)
+    cache, _ = _setup(gpu, rng, 24, 4, 256, 2048, 16, 2048 + 64)
+    q = _dev(randn_f16(rng, (16, 24, 256)), gpu)
+    need = m.suffix_workspace_bytes(cache, 24, 16)
+    assert need > 0
+    with pytest.raises(m.MiikvError):
+        m.suffix_attention(cache, q, 2048, workspace=torch.empty(need // 2, dtype=torch.uint8,
+                                                                  device=gpu))
