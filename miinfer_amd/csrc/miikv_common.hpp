@@ -15,6 +15,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float float16v __attribute__((ext_vector_type(16)));
 
 constexpr uint32_t kWave = 64;
 constexpr uint32_t kChunk = 32;   // tokens per wave step (one V group, two K tiles)
