@@ -3,22 +3,32 @@
 // Token t of a T-token suffix sits at absolute position P + t and attends to
 // cache positions [0, P + t]; the cache already holds the suffix's own rows
 // (qwen3_primitives.hip:6826-6836).  For one kv head the query rows are the
-// (token, head) pairs r = t*G + g; a workgroup owns 128 rows (four waves of
-// 32) and streams every key its rows can see.
+// (token, head) pairs r = t*G + g.
 //
-// Each 32-key step is dequantised once per workgroup into fp16 tiles in LDS
-// (double-buffered): K^[key][dim] = code * k_scale and V^T[dim][key] =
-// code * v_scale, so every K/V byte read from HBM feeds 128 query rows and each
-// LDS operand byte feeds 32.  The MFMAs are v_mfma_f32_32x32x16_f16.
-// Online softmax in the log2 domain with a lazy running max.
+// Two kernels (plus the split combine):
+//  1. expand_kernel dequantises every 32-key step of the context once into
+//     fp16 tiles in the workspace, laid out as the MFMA operand fragments the
+//     attention waves read: K^ = code * k_scale as the A operand of S^T = K^ Q^T,
+//     V^T = code * v_scale as the A operand of O^T += V^T P^T.  Each K/V byte is
+//     dequantised once instead of once per row block.
+//  2. suffix_kernel: a workgroup owns 32 query rows per wave and streams the
+//     fp16 tiles of its key range through LDS (direct global->LDS loads,
+//     double-buffered, one barrier per step).  Per 32-key step and wave
+//     (v_mfma_f32_32x32x16_f16):
+//        S^T[key][row] (32x32) = sum over D/16 dim chunks of K^[32 keys][16] Q^T
+//        O^T[dim][row]        += V^T[32 dims][16 keys] P^T, two key halves per tile
+//     The S^T accumulator of lane (n = lane % 32, hh = lane / 32) holds row n
+//     and keys 8j + 4hh + i (register 4j + i); registers 8kc..8kc+7 form the B
+//     operand of the PV MFMA for key half kc, given that V^T's key order within
+//     a half is permuted alike: fragment position 4*b3 + i of lane hh holds key
+//     8*b3 + 4*hh + i.  Online softmax in the log2 domain with a lazy max.
 //
-// Split-K: grid.z cuts the key range into splits of a fixed number of keys so
-// that a short suffix still fills the chip.  With one split the workgroup
-// normalises and stores its rows; otherwise each (token, kv head, split) writes
-// a partial record (unnormalised O, running max, sum) and the decode path's
-// combine kernel merges them with token t's context length P + t + 1.
+// Split-K: the key range is cut into splits of a fixed number of keys so that
+// a short suffix still fills the chip.  With one split the workgroup normalises
+// and stores its rows; otherwise each (token, kv head, split) writes a partial
+// record (unnormalised O, running max, sum) and suffix_combine_kernel merges
+// them with token t's context length P + t + 1.
 #include "miikv_common.hpp"
-#include "miikv_split.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -31,12 +41,31 @@ uint64_t view_seq_capacity(const miikv_view* v);
 
 namespace {
 
-constexpr uint32_t kSufRows = 128;     // query rows per workgroup (4 waves x 32)
-constexpr uint32_t kSufStep = 32;      // keys per step
+#ifndef MIIKV_SUFFIX_WAVES
+#define MIIKV_SUFFIX_WAVES 8
+#endif
+constexpr uint32_t kSufWaves = MIIKV_SUFFIX_WAVES;
+constexpr uint32_t kSufRows = 32 * kSufWaves;  // query rows per workgroup
+constexpr uint32_t kSufStep = 32;              // keys per step
 constexpr float kLog2eS = 1.4426950408889634f;
 constexpr float kSlackS = 6.0f;        // lazy-rescale threshold (log2 units): p <= 64
-constexpr uint32_t kSufTargetWgs = 1024; // ~4 workgroups per CU over 256 CUs
+// Resident workgroups of suffix_kernel on the chip: 256 CUs, each holding 8 waves
+// (two per SIMD at <= 256 VGPRs) and two 64 KiB LDS tile buffers per workgroup.
+constexpr uint32_t kSufSlots = 256 * (8 / kSufWaves);
 constexpr uint32_t kSufMaxSplits = 64;
+
+// fp16 halves of one expanded step: K fragments [D/16][64 lanes][8], then
+// V fragments [D/32][2 key halves][64 lanes][8].
+__host__ __device__ constexpr uint32_t tile_halves(uint32_t D) { return 2 * D * kSufStep; }
+
+struct ExpandArgs {
+    Geo g;
+    uint32_t seq;
+    uint32_t key_count;  // host: P + T; with a device state: the capacity bound
+    const miikv_prefill_state* ps;
+    uint32_t steps;      // steps per kv head in the tile area
+    _Float16* tiles;
+};
 
 struct SuffixArgs {
     Geo g;
@@ -47,73 +76,136 @@ struct SuffixArgs {
     float scale_log2;
     uint32_t token_count;  // host upper bound
     uint32_t base_position;
-    uint32_t seq;
     const miikv_prefill_state* ps;
     uint32_t split_keys;   // keys per split (multiple of kSufStep)
     uint32_t splits;
     uint32_t row_blocks;   // workgroups per (kv head, split) group
+    uint32_t steps;        // steps per kv head in the tile area
+    const _Float16* tiles;
     float* part;           // partial records when splits > 1
     float* out;
     const float* gate;
     float* gated_out;
 };
 
+// Partial records of split-K, laid out so that a wave's 32 rows write one
+// contiguous block: O [split][kv head][row][D] (row = t*G + g, rows counted up
+// to the host token bound), then (m, l) pairs [split][kv head][row].
+struct SuffixCombineArgs {
+    uint32_t kv_heads;
+    uint32_t q_heads;
+    uint32_t group;
+    uint32_t token_count;  // host bound
+    uint32_t base_position;
+    const miikv_prefill_state* ps;
+    uint32_t split_keys;
+    uint32_t splits;
+    const float* part;
+    float* out;
+    const float* gate;
+    float* gated_out;
+};
+
+__host__ __device__ inline size_t part_o_floats(uint32_t splits, uint32_t kv_heads, uint32_t rows, uint32_t D) {
+    return static_cast<size_t>(splits) * kv_heads * rows * D;
+}
+
 __device__ __forceinline__ float sfx_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Largest fp16 scale whose product with any code (|code| <= 128) stays finite:
 // 128 * 511.75 = 65504.  Scales above it only arise for blocks whose absmax is
-// within 0.8% of the fp16 maximum; clamping them bounds the tile to finite values.
+// within 0.8% of the fp16 maximum; clamping them keeps the tiles finite.
 constexpr float kMaxTileScale = 511.75f;
 
-__device__ __forceinline__ half2v clamp_scales(uint32_t bits) {
-    const half2v lim = {(_Float16)kMaxTileScale, (_Float16)kMaxTileScale};
-    return __builtin_elementwise_min(__builtin_bit_cast(half2v, bits), lim);
+__device__ __forceinline__ _Float16 clamp_scale(uint16_t bits) {
+    return __builtin_elementwise_min(__builtin_bit_cast(_Float16, bits), (_Float16)kMaxTileScale);
 }
 
-// The two MFMAs of the step loop, written out so that register classes are fixed:
-// the loop-invariant query fragments (QK B operand) live in accumulation
-// registers, which leaves the 256 architectural VGPRs to the O^T accumulators
-// (128 registers at D = 256), the staging, LDS fragments and softmax.  The
-// compiler does not see these as MFMAs, so each carries its own wait states: a
-// VALU write read by an MFMA needs 2 (the leading s_nop; when the MFMA unit is
-// busy with the previous MFMA it costs nothing), MFMAs accumulating into the same
-// registers back to back need none, and an MFMA result read by VALU needs 18
-// (mfma_result_wait).
-__device__ __forceinline__ void mfma_qk(half8 k, half8 q_agpr, float16v& s) {
-    asm("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(s) : "v"(k), "a"(q_agpr));
-}
-__device__ __forceinline__ void mfma_pv(half8 v, half8 p, float16v& o) {
-    asm("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(o) : "v"(v), "v"(p));
-}
-__device__ __forceinline__ void mfma_result_wait(float16v& c) {
-    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(c));
+// Keys of the context: [0, P + T).
+__device__ __forceinline__ uint32_t context_keys(uint32_t host_count, const miikv_prefill_state* ps) {
+    return ps ? min(host_count, ps->base_position + ps->token_count) : host_count;
 }
 
-// Workgroup: 4 waves x 32 query rows.  Per 32-key step and wave (32x32x16 MFMAs):
-//   S^T[key][row] (32x32) = sum over D/16 dim chunks of K^[key][16 dims] * Q^T
-//   O^T[dim][row] += V^T[32 dims][16 keys] * P^T, two key halves per 32-dim tile
-// The S^T accumulator of lane (n = lane % 32, hh = lane / 32) holds row n and keys
-// 8j + 4hh + i (register 4j + i); the B operand of the PV MFMA for key half kc
-// is registers 8kc .. 8kc+7, provided V^T's key order within a half is permuted
-// the same way: LDS position 8*b2 + 4*b3 + i holds key 8*b3 + 4*b2 + i.
-//
-// One barrier per step: during step s the waves run the MFMAs of step s from LDS
-// buffer s&1 while dequantising step s+1 (codes fetched during step s-1) into
-// buffer (s+1)&1 and fetching step s+2.  V scales are staged transposed in LDS
-// one step ahead; K scales are read per chunk straight from global memory.
+// One 32-key step of kv head blockIdx.y: 256 threads; keys at or past the context
+// end become 0 (their codes may never have been written).
 template <uint32_t D>
-__global__ void __launch_bounds__(256) suffix_kernel(SuffixArgs a) {
-    constexpr uint32_t NB = D / 32;         // q8_0 blocks per row = PV M-tiles
-    constexpr uint32_t NC = D / 16;         // QK k-chunks
-    constexpr uint32_t KPAD = D + 8;        // K^ row stride (halves)
-    constexpr uint32_t VPAD = kSufStep + 8; // V^T row stride (halves)
-    constexpr uint32_t KCH = D / 128;       // 16-byte K chunks per thread per step
-    constexpr uint32_t VCH = D / 128;       // 16-byte V chunks per thread per step
-    __shared__ __align__(16) _Float16 s_k[2][kSufStep * KPAD];
-    __shared__ __align__(16) _Float16 s_v[2][D * VPAD];
-    __shared__ __align__(16) _Float16 s_vs[2][NB * kSufStep];  // [block][key]
-
+__global__ void __launch_bounds__(256) expand_kernel(ExpandArgs a) {
+    constexpr uint32_t NB = D / 32;
+    constexpr uint32_t NKF = D / 16;       // K fragments per step
+    constexpr uint32_t PER = D / 64;       // fragment lanes per thread, per operand
+    __shared__ __align__(16) _Float16 s_vs[NB * kSufStep];  // [block][key]
     const Geo& geo = a.g;
+    const uint32_t step = blockIdx.x;
+    const uint32_t h = blockIdx.y;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t nkeys = context_keys(a.key_count, a.ps);
+    const uint32_t tok0 = step * kSufStep;
+    if (tok0 >= nkeys) return;
+    const size_t slab = slab_of(geo, a.seq, tok0, h);
+    const uint32_t tp0 = tok0 % geo.page_tokens;
+    const size_t sc0 = (slab * geo.page_tokens + tp0) * NB;
+    const size_t cb = slab * static_cast<size_t>(geo.page_tokens) * D + static_cast<size_t>(tp0) * D;
+    const int8_t* kb = geo.k_codes + cb;
+    const int8_t* vb = geo.v_codes + cb;
+    if (tid < kSufStep * NB) {
+        const uint32_t key = tid / NB, blk = tid % NB;
+        s_vs[blk * kSufStep + key] = tok0 + key < nkeys ? clamp_scale(geo.v_scales[sc0 + tid]) : (_Float16)0.0f;
+    }
+    __syncthreads();
+    _Float16* out = a.tiles + (static_cast<size_t>(h) * a.steps + step) * tile_halves(D);
+    // K fragment c, lane (n, hh): key n, dims 16c + 8hh .. +7.  In the cache tile
+    // those 8 codes sit at (key/16)*16D + (c/4)*1024 + g*256 + (key%16)*16 + e*8
+    // with e = (c%4)/2, g = 2*(c%2) + hh.
+#pragma unroll
+    for (uint32_t u = 0; u < PER; ++u) {
+        const uint32_t fl = tid + 256 * u;
+        const uint32_t c = fl / 64, l = fl % 64, n = l % 32, hh = l / 32;
+        const uint32_t off = (n / 16) * 16 * D + (c / 4) * 1024 + (2 * (c % 2) + hh) * 256 + (n % 16) * 16 +
+                             ((c % 4) / 2) * 8;
+        const uint2 w = *reinterpret_cast<const uint2*>(kb + off);
+        const _Float16 sc = tok0 + n < nkeys ? clamp_scale(geo.k_scales[sc0 + n * NB + c / 2]) : (_Float16)0.0f;
+        *reinterpret_cast<half8*>(out + 8 * fl) = codes8_to_half8(w.x, w.y) * (half8)sc;
+    }
+    // V fragment f = 2mt + kc, lane (n, hh): dim 32mt + n, positions 4*b3 + i hold
+    // keys 16kc + 8*b3 + 4hh + i.  A 32-token group stores dim d's code of key
+    // 16J + 4G + I at d*32 + 8G + 4J + I, so b3 = 0 is the dword at G = hh and
+    // b3 = 1 the dword at G = 2 + hh, both at J = kc.
+#pragma unroll
+    for (uint32_t u = 0; u < PER; ++u) {
+        const uint32_t fl = tid + 256 * u;
+        const uint32_t f = fl / 64, l = fl % 64, n = l % 32, hh = l / 32;
+        const uint32_t mt = f / 2, kc = f % 2;
+        const int8_t* vd = vb + (32 * mt + n) * 32;
+        const uint32_t w0 = *reinterpret_cast<const uint32_t*>(vd + 8 * hh + 4 * kc);
+        const uint32_t w1 = *reinterpret_cast<const uint32_t*>(vd + 8 * (2 + hh) + 4 * kc);
+        const _Float16* sv = &s_vs[mt * kSufStep + 16 * kc + 4 * hh];
+        const half4 a0 = codes4_to_half4(w0) * *reinterpret_cast<const half4*>(sv);
+        const half4 a1 = codes4_to_half4(w1) * *reinterpret_cast<const half4*>(sv + 8);
+        half8 r;
+        r.lo = a0;
+        r.hi = a1;
+        *reinterpret_cast<half8*>(out + 64 * 8 * NKF + 8 * fl) = r;
+    }
+}
+
+// This file is compiled with MFMA results in architectural VGPRs
+// (-amdgpu-mfma-vgpr-form): at D = 256 a wave holds O^T (128 registers), the
+// query fragments (64), S^T (16) and the softmax working set, and within the 256
+// registers of two waves per SIMD the lazy rescale multiplies O^T in place.
+__device__ __forceinline__ float16v mfma_32x32x16(half8 a, half8 b, float16v c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+template <uint32_t D>
+__global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
+    constexpr uint32_t NB = D / 32;         // PV M-tiles
+    constexpr uint32_t NC = D / 16;         // QK k-chunks (K fragments)
+    constexpr uint32_t TILE = tile_halves(D);
+    constexpr uint32_t CHUNKS = TILE * 2 / 1024;  // 1 KiB copy chunks per step
+    static_assert(CHUNKS % kSufWaves == 0, "copy chunks must split evenly over waves");
+    __shared__ __align__(16) _Float16 s_t[2][TILE];
+
     uint32_t T = a.token_count;
     uint32_t P = a.base_position;
     if (a.ps != nullptr) {
@@ -122,16 +214,16 @@ __global__ void __launch_bounds__(256) suffix_kernel(SuffixArgs a) {
     }
     const uint32_t G = a.group;
     // XCD-aware order: workgroup L runs on XCD L % 8, so the row blocks of one
-    // (kv head, split) group, which read the same K/V tiles, are given to one XCD
-    // and share its L2.  Groups g = xcd, xcd + 8, ...; the grid is padded to a
+    // (kv head, split) group, which read the same tiles, are given to one XCD and
+    // share its L2.  Groups g = xcd, xcd + 8, ...; the grid is padded to a
     // multiple of 8 groups.
     const uint32_t L = blockIdx.x;
-    const uint32_t j = L / 8;
-    const uint32_t grp = (L % 8) + 8 * (j / a.row_blocks);
+    const uint32_t jx = L / 8;
+    const uint32_t grp = (L % 8) + 8 * (jx / a.row_blocks);
     if (grp >= a.g.kv_heads * a.splits) return;
     const uint32_t h = grp % a.g.kv_heads;
     const uint32_t split = grp / a.g.kv_heads;
-    const uint32_t rb = j % a.row_blocks;
+    const uint32_t rb = jx % a.row_blocks;
     const uint32_t tid = threadIdx.x;
     const uint32_t wave = tid >> 6;
     const uint32_t lane = tid & 63;
@@ -155,7 +247,11 @@ __global__ void __launch_bounds__(256) suffix_kernel(SuffixArgs a) {
     if (key_lo >= nkeys) return;  // no row of this workgroup has keys in this split
     const uint32_t key_hi = min(nkeys, key_lo + a.split_keys);
     const uint32_t s_begin = key_lo / kSufStep;
+#ifdef MIIKV_SFX_EXP_NOLOOP
+    const uint32_t s_end = s_begin + 1;
+#else
     const uint32_t s_end = (key_hi + kSufStep - 1) / kSufStep;
+#endif
 
     // ---- Q^T fragments (B operand): row n, dims 16c + 8hh .. +7.
     half8 qf[NC];
@@ -180,90 +276,16 @@ __global__ void __launch_bounds__(256) suffix_kernel(SuffixArgs a) {
         }
     }
 
-    // ---- producer: codes and scales of one step into registers.
-    const size_t slab_bytes = static_cast<size_t>(geo.page_tokens) * D;
-    struct Stage {
-        uint32_t ks[KCH];   // K scales of the chunk's two blocks
-        uint4 k[KCH];
-        uint4 v[VCH];
-    };
-    auto slab_at = [&](uint32_t s) { return slab_of(geo, a.seq, s * kSufStep, h); };
-    auto scale_base = [&](uint32_t s, size_t slab) {
-        return (slab * geo.page_tokens + (s * kSufStep) % geo.page_tokens) * NB;
-    };
-    auto code_base = [&](uint32_t s, size_t slab) {
-        return slab * slab_bytes + static_cast<size_t>((s * kSufStep) % geo.page_tokens) * D;
-    };
-    // Two V scales per thread (key = 2*tid / NB, blocks 2*tid % NB and +1).
-    auto load_vs = [&](uint32_t s, size_t slab) -> uint32_t {
-        if (tid >= kSufStep * NB / 2) return 0u;
-        return *reinterpret_cast<const uint32_t*>(geo.v_scales + scale_base(s, slab) + 2 * tid);
-    };
-    auto load_k = [&](uint32_t s, size_t slab, Stage& st) {
-        const size_t sc0 = scale_base(s, slab);
-        const int8_t* kb = geo.k_codes + code_base(s, slab);
+    // Step s's tile into LDS buffer b: CHUNKS KiB, each wave copying every
+    // kSufWaves-th KiB with one 16-byte direct-to-LDS load per lane.
+    const char* tiles_h = reinterpret_cast<const char*>(a.tiles + static_cast<size_t>(h) * a.steps * TILE);
+    auto fetch = [&](uint32_t s, uint32_t b) {
+        const char* src = tiles_h + static_cast<size_t>(s) * TILE * 2 + lane * 16;
+        char* dst = reinterpret_cast<char*>(s_t[b]);
 #pragma unroll
-        for (uint32_t u = 0; u < KCH; ++u) {
-            const uint32_t q = tid + 256 * u;
-            const uint32_t key = 16 * (q / D) + q % 16;
-            const uint32_t c = (q % D) / 64;
-            st.ks[u] = *reinterpret_cast<const uint32_t*>(geo.k_scales + sc0 + key * NB + 2 * c);
-            st.k[u] = *reinterpret_cast<const uint4*>(kb + 16 * q);
-        }
-    };
-    auto load_v = [&](uint32_t s, size_t slab, Stage& st) {
-        const int8_t* vb = geo.v_codes + code_base(s, slab);
-#pragma unroll
-        for (uint32_t u = 0; u < VCH; ++u) st.v[u] = *reinterpret_cast<const uint4*>(vb + 16 * (tid + 256 * u));
-    };
-    // V scales of step s into s_vs[buf] ([block][key]); keys at or past key_hi get 0
-    // so their codes (possibly never written) contribute nothing.
-    auto write_vs = [&](uint32_t s, uint32_t vs, uint32_t buf) {
-        if (tid < kSufStep * NB / 2) {
-            const uint32_t e0 = 2 * tid;
-            const uint32_t key = e0 / NB;
-            const uint32_t b0 = e0 % NB;
-            const half2v sc = s * kSufStep + key < key_hi ? clamp_scales(vs) : half2v{};
-            s_vs[buf][b0 * kSufStep + key] = sc[0];
-            s_vs[buf][(b0 + 1) * kSufStep + key] = sc[1];
-        }
-    };
-    // K^ tile: chunk q = key 16*(q/D) + q%16, dims 64c + 8g + j (block 2c) and
-    // 64c + 32 + 8g + j (block 2c+1).
-    auto dequant_k = [&](const Stage& st, uint32_t buf) {
-#pragma unroll
-        for (uint32_t u = 0; u < KCH; ++u) {
-            const uint32_t q = tid + 256 * u;
-            const uint32_t qin = q % D;
-            const uint32_t c = qin / 64, g = (qin % 64) / 16;
-            const uint32_t key = 16 * (q / D) + q % 16;
-            const half2v sc = clamp_scales(st.ks[u]);
-            const half8 lo = codes8_to_half8(st.k[u].x, st.k[u].y) * (half8)sc[0];
-            const half8 hi = codes8_to_half8(st.k[u].z, st.k[u].w) * (half8)sc[1];
-            _Float16* dst = &s_k[buf][key * KPAD + 64 * c + 8 * g];
-            *reinterpret_cast<half8*>(dst) = lo;
-            *reinterpret_cast<half8*>(dst + 32) = hi;
-        }
-    };
-    // V^T tile: chunk q = dim q/2, 16 bytes at 16*(q%2) of the dim's 32 codes:
-    // dwords hold keys 8u+0..3, 16+8u+0..3, 8u+4..7, 16+8u+4..7 (u = q%2).
-    auto dequant_v = [&](const Stage& st, uint32_t buf) {
-#pragma unroll
-        for (uint32_t u = 0; u < VCH; ++u) {
-            const uint32_t q = tid + 256 * u;
-            const uint32_t d = q / 2, up = q % 2;
-            const _Float16* sv = &s_vs[buf][(d / 32) * kSufStep];
-            const half8 slo = *reinterpret_cast<const half8*>(sv + 8 * up);
-            const half8 shi = *reinterpret_cast<const half8*>(sv + 16 + 8 * up);
-            const half4 a0 = codes4_to_half4(st.v[u].x) * slo.lo;
-            const half4 a1 = codes4_to_half4(st.v[u].y) * shi.lo;
-            const half4 a2 = codes4_to_half4(st.v[u].z) * slo.hi;
-            const half4 a3 = codes4_to_half4(st.v[u].w) * shi.hi;
-            _Float16* dst = &s_v[buf][d * VPAD + 4 * up];
-            *reinterpret_cast<half4*>(dst) = a0;
-            *reinterpret_cast<half4*>(dst + 16) = a1;
-            *reinterpret_cast<half4*>(dst + 8) = a2;
-            *reinterpret_cast<half4*>(dst + 24) = a3;
+        for (uint32_t u = 0; u < CHUNKS / kSufWaves; ++u) {
+            const uint32_t chunk = wave + kSufWaves * u;
+            __builtin_amdgcn_global_load_lds(src + chunk * 1024, dst + chunk * 1024, 16, 0, 0);
         }
     };
 
@@ -273,49 +295,36 @@ __global__ void __launch_bounds__(256) suffix_kernel(SuffixArgs a) {
 #pragma unroll
     for (uint32_t mt = 0; mt < NB; ++mt) O[mt] = float16v{};
 
-    // Prologue: step s_begin dequantised, step s_begin+1 codes in registers and its
-    // V scales in LDS, step s_begin+2's V scales in a register.
-    Stage st;
-    size_t slab = slab_at(s_begin);
-    load_k(s_begin, slab, st);
-    load_v(s_begin, slab, st);
-    write_vs(s_begin, load_vs(s_begin, slab), s_begin & 1);
-    __syncthreads();
-    dequant_k(st, s_begin & 1);
-    dequant_v(st, s_begin & 1);
-    if (s_begin + 1 < s_end) {
-        slab = slab_at(s_begin + 1);
-        load_k(s_begin + 1, slab, st);
-        load_v(s_begin + 1, slab, st);
-        write_vs(s_begin + 1, load_vs(s_begin + 1, slab), (s_begin + 1) & 1);
-    }
-    size_t slab2 = 0;   // slab of step s+2
-    uint32_t vs2 = 0;   // V scales of step s+2
-    if (s_begin + 2 < s_end) {
-        slab2 = slab_at(s_begin + 2);
-        vs2 = load_vs(s_begin + 2, slab2);
-    }
+    fetch(s_begin, s_begin & 1);
+    wait_vmem();
     __syncthreads();
 
     for (uint32_t s = s_begin; s < s_end; ++s) {
         const uint32_t buf = s & 1;
-        const bool next = s + 1 < s_end;
-        const bool next2 = s + 2 < s_end;
-        const bool next3 = s + 3 < s_end;
+#ifndef MIIKV_SFX_EXP_NOFETCH
+        if (s + 1 < s_end) fetch(s + 1, buf ^ 1);  // buffer buf^1 was released by the last barrier
+#endif
+#ifdef MIIKV_SFX_EXP_NOLDS
+        // registers stand in for the LDS fragments
+        const _Float16* tk = reinterpret_cast<const _Float16*>(&qf[0]) - 0 * lane;
+        const _Float16* tv = tk;
+#define MIIKV_FRAG_K(c) qf[(c) % NC]
+#define MIIKV_FRAG_V(f) qf[(f) % NC]
+#else
+        const _Float16* tk = s_t[buf] + lane * 8;
+        const _Float16* tv = s_t[buf] + 64 * 8 * NC + lane * 8;
+#define MIIKV_FRAG_K(c) (*reinterpret_cast<const half8*>(tk + 512 * (c)))
+#define MIIKV_FRAG_V(f) (*reinterpret_cast<const half8*>(tv + 512 * (f)))
+#endif
         // ---- S^T = K^ Q^T
         float16v acc = {};
-        const _Float16* kt = &s_k[buf][n * KPAD + 8 * hh];
-        mfma_qk(*reinterpret_cast<const half8*>(kt), qf[0], acc);
 #pragma unroll
-        for (uint32_t c = 1; c < NC; ++c) mfma_qk(*reinterpret_cast<const half8*>(kt + 16 * c), qf[c], acc);
-        mfma_result_wait(acc);
-        if (next) dequant_k(st, buf ^ 1);
-        if (next2) load_k(s + 2, slab2, st);
-        size_t slab3 = 0;
-        uint32_t vs3 = 0;
-        if (next3) {
-            slab3 = slab_at(s + 3);
-            vs3 = load_vs(s + 3, slab3);
+        for (uint32_t c = 0; c < NC; ++c) {
+#ifdef MIIKV_SFX_EXP_NOMFMA
+            acc[c % 16] += (float)MIIKV_FRAG_K(c)[0];
+#else
+            acc = mfma_32x32x16(MIIKV_FRAG_K(c), qf[c], acc);
+#endif
         }
 
         // ---- online softmax over this lane's 16 keys of row n
@@ -327,9 +336,9 @@ __global__ void __launch_bounds__(256) suffix_kernel(SuffixArgs a) {
                 if (!(key <= lim && key < key_hi)) acc[r] = -INFINITY;
             }
         }
-        float cmax = acc[0];
+        float cmax = fmaxf(acc[0], acc[1]);
 #pragma unroll
-        for (uint32_t r = 1; r < 16; ++r) cmax = fmaxf(cmax, acc[r]);
+        for (uint32_t r = 2; r < 16; r += 2) cmax = fmaxf(cmax, fmaxf(acc[r], acc[r + 1]));
         cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
         const float cm = cmax * a.scale_log2;
         const bool grow = cm > m_run + kSlackS;
@@ -344,54 +353,46 @@ __global__ void __launch_bounds__(256) suffix_kernel(SuffixArgs a) {
         // A row with no visible key yet keeps m_run = -inf; subtracting 0 keeps p = 0.
         const float m_use = m_run == -INFINITY ? 0.0f : m_run;
         half8 pb[2];
+        float lsum = 0.0f;
 #pragma unroll
         for (uint32_t kc = 0; kc < 2; ++kc)
 #pragma unroll
-            for (uint32_t e = 0; e < 8; e += 2) {
-                const float p0 = sfx_exp2(fmaf(acc[8 * kc + e], a.scale_log2, -m_use));
-                const float p1 = sfx_exp2(fmaf(acc[8 * kc + e + 1], a.scale_log2, -m_use));
-                l_run += p0 + p1;
-                pb[kc][e] = static_cast<_Float16>(p0);  // round to nearest: no bias against l_run
-                pb[kc][e + 1] = static_cast<_Float16>(p1);
+            for (uint32_t e = 0; e < 8; ++e) {
+                const float p = sfx_exp2(fmaf(acc[8 * kc + e], a.scale_log2, -m_use));
+                lsum += p;
+                pb[kc][e] = static_cast<_Float16>(p);  // round to nearest: no bias against l_run
             }
+        l_run += lsum;
         // ---- O^T += V^T P^T
-        const _Float16* vt = &s_v[buf][n * VPAD + 8 * hh];
-        mfma_pv(*reinterpret_cast<const half8*>(vt), pb[0], O[0]);
-        mfma_pv(*reinterpret_cast<const half8*>(vt + 16), pb[1], O[0]);
 #pragma unroll
-        for (uint32_t mt = 1; mt < NB; ++mt)
+        for (uint32_t mt = 0; mt < NB; ++mt)
 #pragma unroll
             for (uint32_t kc = 0; kc < 2; ++kc)
-                mfma_pv(*reinterpret_cast<const half8*>(vt + 32 * mt * VPAD + 16 * kc), pb[kc], O[mt]);
-        if (next) dequant_v(st, buf ^ 1);
-        if (next2) {
-            load_v(s + 2, slab2, st);
-            write_vs(s + 2, vs2, buf);
-        }
-        slab2 = slab3;
-        vs2 = vs3;
+#ifdef MIIKV_SFX_EXP_NOMFMA
+                O[mt][kc] += (float)(MIIKV_FRAG_V(2 * mt + kc)[0] * pb[kc][0]);
+#else
+                O[mt] = mfma_32x32x16(MIIKV_FRAG_V(2 * mt + kc), pb[kc], O[mt]);
+#endif
+        wait_vmem();
         __syncthreads();
     }
 
-#pragma unroll
-    for (uint32_t mt = 0; mt < NB; ++mt) mfma_result_wait(O[mt]);
     // ---- store: lane (n, hh) holds dims 32mt + 8j + 4hh + i of row n (register 4j + i).
     l_run += __shfl_xor(l_run, 32, 64);
     if (!row_ok) return;
     if (a.splits > 1) {
-        // Partial record of (token t_row, kv head h, split): O [G][D], m [G], l [G].
-        float* rec = a.part + ((static_cast<size_t>(t_row) * geo.kv_heads + h) * a.splits + split) *
-                                  record_floats(G, D);
-        const uint32_t gi = qh - h * G;
+        const uint32_t rows_cap = a.token_count * G;
+        const size_t pr = (static_cast<size_t>(split) * a.g.kv_heads + h) * rows_cap + row;
+        float* po = a.part + pr * D;
 #pragma unroll
         for (uint32_t mt = 0; mt < NB; ++mt)
 #pragma unroll
             for (uint32_t j = 0; j < 4; ++j)
-                *reinterpret_cast<float4*>(rec + gi * D + 32 * mt + 8 * j + 4 * hh) =
+                *reinterpret_cast<float4*>(po + 32 * mt + 8 * j + 4 * hh) =
                     make_float4(O[mt][4 * j], O[mt][4 * j + 1], O[mt][4 * j + 2], O[mt][4 * j + 3]);
         if (hh == 0) {
-            rec[G * D + gi] = m_run;
-            rec[G * D + G + gi] = l_run;
+            float2* ml = reinterpret_cast<float2*>(a.part + part_o_floats(a.splits, a.g.kv_heads, rows_cap, D));
+            ml[pr] = make_float2(m_run, l_run);
         }
         return;
     }
@@ -420,6 +421,60 @@ __global__ void __launch_bounds__(256) suffix_kernel(SuffixArgs a) {
         }
 }
 
+// Merge the splits of each (row, kv head): thread = 4 consecutive dims of one
+// row.  Token t sees P + t + 1 keys, so splits at or past ceil((P + t + 1) /
+// split_keys) hold no key of its row and are skipped; the rest are merged in
+// split order (out = sum e^{m_s-M} O_s / sum e^{m_s-M} l_s, 0 when the sum is 0).
+template <uint32_t D>
+__global__ void __launch_bounds__(256) suffix_combine_kernel(SuffixCombineArgs a) {
+    uint32_t T = a.token_count;
+    uint32_t P = a.base_position;
+    if (a.ps != nullptr) {
+        P = a.ps->base_position;
+        T = min(T, a.ps->token_count);
+    }
+    const uint32_t G = a.group;
+    const uint32_t h = blockIdx.y;
+    const uint32_t idx = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t row = idx / (D / 4);
+    const uint32_t d4 = idx % (D / 4);
+    if (row >= T * G) return;
+    const uint32_t rows_cap = a.token_count * G;
+    const uint32_t t = row / G, g = row % G;
+    const uint32_t nsplit = min(a.splits, (P + t + 1 + a.split_keys - 1) / a.split_keys);
+    const float2* ml = reinterpret_cast<const float2*>(a.part + part_o_floats(a.splits, a.kv_heads, rows_cap, D));
+    float M = -INFINITY, Ls = 0.0f;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t sp = 0; sp < nsplit; ++sp) {
+        const size_t pr = (static_cast<size_t>(sp) * a.kv_heads + h) * rows_cap + row;
+        const float2 e = ml[pr];
+        const float4 v = *reinterpret_cast<const float4*>(a.part + pr * D + 4 * d4);
+        const float mn = fmaxf(M, e.x);
+        if (mn == -INFINITY) continue;  // no key of this row so far
+        const float fo = exp2f(M - mn);
+        const float fs = exp2f(e.x - mn);
+        M = mn;
+        Ls = Ls * fo + e.y * fs;
+        acc.x = acc.x * fo + v.x * fs;
+        acc.y = acc.y * fo + v.y * fs;
+        acc.z = acc.z * fo + v.z * fs;
+        acc.w = acc.w * fo + v.w * fs;
+    }
+    const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
+    const float4 o = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+    const size_t oi = (static_cast<size_t>(t) * a.q_heads + h * G + g) * D + 4 * d4;
+    if (a.out) *reinterpret_cast<float4*>(a.out + oi) = o;
+    if (a.gate && a.gated_out) {
+        const float4 gv = *reinterpret_cast<const float4*>(a.gate + oi);
+        float4 r;
+        r.x = o.x * (1.0f / (1.0f + expf(-gv.x)));
+        r.y = o.y * (1.0f / (1.0f + expf(-gv.y)));
+        r.z = o.z * (1.0f / (1.0f + expf(-gv.z)));
+        r.w = o.w * (1.0f / (1.0f + expf(-gv.w)));
+        *reinterpret_cast<float4*>(a.gated_out + oi) = r;
+    }
+}
+
 }  // namespace
 }  // namespace miikv
 
@@ -430,39 +485,55 @@ namespace {
 struct SuffixPlan {
     uint32_t splits;
     uint32_t split_keys;
-    uint64_t part_bytes;
+    uint32_t steps;        // expanded steps per kv head
+    uint64_t tile_bytes;   // expanded fp16 tiles, all kv heads
+    uint64_t part_bytes;   // partial records (splits > 1)
+    uint64_t total() const { return tile_bytes + part_bytes; }
 };
 
-// Split count for a suffix of `tokens` tokens whose keys end at or before
-// `key_bound`: enough workgroups to fill the chip, at least 256 keys per split.
-// Monotone in key_bound, so a plan made with the cache capacity covers any
-// smaller context.
-SuffixPlan make_suffix_plan(const miikv_view* v, uint32_t q_heads, uint32_t tokens, uint64_t key_bound) {
-    SuffixPlan p{1, 0, 0};
+// Plan for a suffix of `tokens` tokens whose keys end at or before `key_bound`:
+// the expanded tiles of every step, and enough splits to fill the chip (at least
+// 256 keys per split).  Monotone in key_bound, so a plan made with the cache
+// capacity covers any smaller context.
+SuffixPlan make_suffix_plan(const miikv_view* v, uint32_t q_heads, uint32_t tokens, uint64_t key_bound,
+                            bool allow_split) {
+    SuffixPlan p{1, 0, 0, 0, 0};
     const uint32_t G = q_heads / v->kv_heads;
+    p.steps = static_cast<uint32_t>((key_bound + kSufStep - 1) / kSufStep);
+    p.tile_bytes = static_cast<uint64_t>(v->kv_heads) * p.steps * tile_halves(v->head_dim) * 2;
+    p.split_keys = static_cast<uint32_t>(std::min<uint64_t>(static_cast<uint64_t>(p.steps) * kSufStep, 0xffffff00u));
+    if (!allow_split) return p;
     const uint64_t wgs = (static_cast<uint64_t>(tokens) * G + kSufRows - 1) / kSufRows * v->kv_heads;
-    uint64_t want = (kSufTargetWgs + wgs - 1) / wgs;
+    // Splits: enough workgroups for about three quarters of the resident slots.
+    // More splits fill the chip better but cost record traffic and, measured at
+    // config 4, more concurrent tile streams through L2: 4 splits (192 workgroups)
+    // ran faster than 5 (240) or 8 (384).
+    const uint64_t by_keys = std::min<uint64_t>((key_bound + 255) / 256, kSufMaxSplits);
+    uint64_t want = (kSufSlots * 3 / 4 + wgs - 1) / wgs;
     if (const char* e = std::getenv("MIIKV_SUFFIX_SPLITS")) want = std::strtoul(e, nullptr, 10);
-    const uint64_t by_keys = (key_bound + 255) / 256;
-    want = std::min<uint64_t>({want, by_keys, kSufMaxSplits});
+    want = std::max<uint64_t>(1, std::min<uint64_t>({want, by_keys, kSufMaxSplits}));
     if (want <= 1) return p;
-    const uint64_t unit = kWavesPerWg * kChunk;  // the combine's split granularity (128 keys)
+    const uint64_t unit = kSufStep;
     const uint64_t cpw = (key_bound + want * unit - 1) / (want * unit);
-    p.split_keys = static_cast<uint32_t>(cpw * unit);
-    p.splits = static_cast<uint32_t>((key_bound + p.split_keys - 1) / p.split_keys);
-    if (p.splits <= 1) return SuffixPlan{1, 0, 0};
-    p.part_bytes = static_cast<uint64_t>(tokens) * v->kv_heads * p.splits * record_floats(G, v->head_dim) * 4;
+    const uint32_t split_keys = static_cast<uint32_t>(cpw * unit);
+    const uint32_t splits = static_cast<uint32_t>((key_bound + split_keys - 1) / split_keys);
+    if (splits <= 1) return p;
+    p.splits = splits;
+    p.split_keys = split_keys;
+    // Records sized for `want` (>= splits): a plan for a shorter context never needs more.
+    p.part_bytes = want * v->kv_heads * tokens * G * (v->head_dim + 2) * 4;
     return p;
 }
 
 }  // namespace
 
-// Workspace for the split-K path: partial records of every (token, kv head, split),
-// planned for the cache capacity (any base position fits).  0 when one split suffices.
+// Workspace of miikv_suffix_attn: the expanded fp16 tiles of the context and,
+// for split-K, the partial records; planned for the cache capacity, so it serves
+// any base position (and a device prefill state).
 extern "C" uint64_t miikv_suffix_workspace_bytes(const miikv_view* view, uint32_t q_heads, uint32_t token_count) {
     if (validate_view(view) != MIIKV_OK || q_heads == 0 || q_heads % view->kv_heads != 0 || token_count == 0)
         return 0;
-    return make_suffix_plan(view, q_heads, token_count, view_seq_capacity(view)).part_bytes;
+    return make_suffix_plan(view, q_heads, token_count, view_seq_capacity(view), true).total();
 }
 
 extern "C" miikv_status miikv_suffix_attn(const miikv_view* view, const void* q, uint32_t q_dtype, uint32_t q_heads,
@@ -485,16 +556,33 @@ extern "C" miikv_status miikv_suffix_attn(const miikv_view* view, const void* q,
     const uint64_t blocks = (rows + kSufRows - 1) / kSufRows;
     if (blocks > 0x7fffffffu || static_cast<uint64_t>(token_count) * view->kv_heads > 0x7fffffffu)
         return MIIKV_EINVAL;
-    // Without a workspace the kernel runs one split; with one, the plan for the
-    // known context (host base position) or for the capacity (device state).
-    SuffixPlan plan{1, 0, 0};
-    if (workspace != nullptr) {
-        const uint64_t bound = prefill_state ? cap : static_cast<uint64_t>(base_position) + token_count;
-        plan = make_suffix_plan(view, q_heads, token_count, bound);
-        if (workspace_bytes < plan.part_bytes) return MIIKV_EWORKSPACE;
+    // The key bound: the known context (host base position) or the capacity (device
+    // state).  A workspace of miikv_suffix_workspace_bytes() bytes always suffices;
+    // one holding just the tiles runs a single split.
+    const uint64_t bound = prefill_state ? cap : static_cast<uint64_t>(base_position) + token_count;
+    if (workspace == nullptr) return MIIKV_EWORKSPACE;
+    SuffixPlan plan = make_suffix_plan(view, q_heads, token_count, bound, true);
+    if (workspace_bytes < plan.total()) {
+        plan = make_suffix_plan(view, q_heads, token_count, bound, false);
+        if (workspace_bytes < plan.total()) return MIIKV_EWORKSPACE;
     }
+    if (plan.steps > 65535u * 64u) return MIIKV_EINVAL;
+    _Float16* tiles = static_cast<_Float16*>(workspace);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+
+    ExpandArgs e;
+    e.g = make_geo(*view);
+    e.seq = seq;
+    e.key_count = static_cast<uint32_t>(std::min<uint64_t>(bound, 0xffffffffu));
+    e.ps = prefill_state;
+    e.steps = plan.steps;
+    e.tiles = tiles;
+    const dim3 egrid(plan.steps, view->kv_heads);
+    if (view->head_dim == 128) hipLaunchKernelGGL(expand_kernel<128>, egrid, dim3(256), 0, s, e);
+    else hipLaunchKernelGGL(expand_kernel<256>, egrid, dim3(256), 0, s, e);
+
     SuffixArgs a;
-    a.g = make_geo(*view);
+    a.g = e.g;
     a.q = q;
     a.q_f32 = q_dtype == MIIKV_DTYPE_F32;
     a.q_heads = q_heads;
@@ -502,12 +590,13 @@ extern "C" miikv_status miikv_suffix_attn(const miikv_view* view, const void* q,
     a.scale_log2 = scale * kLog2eS;
     a.token_count = token_count;
     a.base_position = base_position;
-    a.seq = seq;
     a.ps = prefill_state;
-    a.split_keys = plan.splits > 1 ? plan.split_keys : 0xffffffffu;
+    a.split_keys = plan.split_keys;
     a.splits = plan.splits;
     a.row_blocks = static_cast<uint32_t>(blocks);
-    a.part = static_cast<float*>(workspace);
+    a.steps = plan.steps;
+    a.tiles = tiles;
+    a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + plan.tile_bytes);
     a.out = out;
     a.gate = gate;
     a.gated_out = gated_out;
@@ -515,30 +604,26 @@ extern "C" miikv_status miikv_suffix_attn(const miikv_view* view, const void* q,
     const uint64_t wgs = ((groups + 7) / 8) * 8 * blocks;
     if (wgs > 0x7fffffffu) return MIIKV_EINVAL;
     const dim3 grid(static_cast<uint32_t>(wgs));
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    if (view->head_dim == 128) hipLaunchKernelGGL(suffix_kernel<128>, grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL(suffix_kernel<256>, grid, dim3(256), 0, s, a);
+    if (view->head_dim == 128) hipLaunchKernelGGL(suffix_kernel<128>, grid, dim3(64 * kSufWaves), 0, s, a);
+    else hipLaunchKernelGGL(suffix_kernel<256>, grid, dim3(64 * kSufWaves), 0, s, a);
     if (plan.splits > 1) {
-        // Token t of the suffix sees P + t + 1 keys; rows past the device token count are skipped.
-        SplitArgs c{};
-        c.g = a.g;
+        SuffixCombineArgs c;
+        c.kv_heads = view->kv_heads;
         c.q_heads = q_heads;
         c.group = G;
-        c.len_ptr = prefill_state ? &prefill_state->base_position : nullptr;
-        c.len_stride = 0;
-        c.len_add = (prefill_state ? 0u : base_position) + 1u;
-        c.len_bstep = 1;
-        c.count_ptr = prefill_state ? &prefill_state->token_count : nullptr;
-        c.max_context = static_cast<uint32_t>(std::min<uint64_t>(cap, 0xffffffffu));
-        c.cpw = plan.split_keys / (kWavesPerWg * kChunk);
-        c.max_splits = plan.splits;
+        c.token_count = token_count;
+        c.base_position = base_position;
+        c.ps = prefill_state;
+        c.split_keys = plan.split_keys;
+        c.splits = plan.splits;
         c.part = a.part;
         c.out = out;
         c.gate = gate;
         c.gated_out = gated_out;
-        const dim3 cgrid(token_count * view->kv_heads, (G * view->head_dim + 63) / 64);
-        if (view->head_dim == 128) hipLaunchKernelGGL(combine_kernel<128>, cgrid, dim3(256), 0, s, c);
-        else hipLaunchKernelGGL(combine_kernel<256>, cgrid, dim3(256), 0, s, c);
+        const uint64_t threads = static_cast<uint64_t>(token_count) * G * (view->head_dim / 4);
+        const dim3 cgrid(static_cast<uint32_t>((threads + 255) / 256), view->kv_heads);
+        if (view->head_dim == 128) hipLaunchKernelGGL(suffix_combine_kernel<128>, cgrid, dim3(256), 0, s, c);
+        else hipLaunchKernelGGL(suffix_combine_kernel<256>, cgrid, dim3(256), 0, s, c);
     }
     return hip_status(hipGetLastError());
 }

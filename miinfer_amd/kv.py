@@ -301,9 +301,9 @@ def suffix_attention(cache: KvCache, q: torch.Tensor, base_position: int, scale:
     """Causal attention of a T-token suffix (rows already appended at base_position..)
     over the cache.  q: [T, q_heads, head_dim] fp16/fp32.  Returns (out, gated_out).
 
-    split=True runs split-K over the key range with a workspace of
-    suffix_workspace_bytes() (allocated here unless given); split=False runs one
-    workgroup per row block over all its keys."""
+    The workspace holds the context's expanded fp16 tiles plus, for split-K, the
+    partial records: split=True allocates suffix_workspace_bytes() (unless given);
+    split=False allocates the tiles only, which runs one split."""
     t, q_heads, d = q.shape
     if d != cache.head_dim or not q.is_contiguous() or q.dtype not in (torch.float16,
                                                                         torch.float32):
@@ -322,15 +322,17 @@ def suffix_attention(cache: KvCache, q: torch.Tensor, base_position: int, scale:
     if gate is not None and gated_out is None:
         gated_out = torch.empty((t, q_heads, d), dtype=torch.float32, device=q.device)
     qd = _lib.DTYPE_F16 if q.dtype == torch.float16 else _lib.DTYPE_F32
-    ws_bytes = 0
-    if split:
-        if workspace is None:
+    if workspace is None:
+        if split:
             need = suffix_workspace_bytes(cache, q_heads, t)
-            workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
-        ws_bytes = workspace.numel() * workspace.element_size()
+        else:
+            bound = cache.capacity if prefill_state is not None else base_position + t
+            need = cache.kv_heads * ((bound + 31) // 32) * 2 * d * 32 * 2
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    ws_bytes = workspace.numel() * workspace.element_size()
     call("miikv_suffix_attn", cache.view, _ptr(q), qd, q_heads, float(scale), t, base_position,
          seq, _ptr(prefill_state), _ptr(out), _ptr(gate), _ptr(gated_out),
-         _ptr(workspace) if split else None, ws_bytes, _stream(stream))
+         _ptr(workspace), ws_bytes, _stream(stream))
     return out, gated_out
 
 

@@ -135,17 +135,18 @@ def test_workspace_bytes_scales_with_geometry():
 
 
 def test_suffix_workspace_bytes_plan():
-    """Split-K workspace: zero when one workgroup per row block already fills the chip or
-    the context is short; otherwise one record (G*D + pad(2G) floats) per token, kv head
-    and split."""
+    """Suffix workspace: the expanded fp16 tiles of every 32-key step of the capacity
+    (2*D*32 halves per step and kv head) plus, when the key range is split, one record
+    (G*D + pad(2G) floats) per token, kv head and split."""
     L = _lib()
     lib = L.lib()
     v = _view(page_tokens=8704, kv_heads=4, head_dim=256)
+    tiles = 4 * (8704 // 32) * 2 * 256 * 32 * 2
     ws = lib.miikv_suffix_workspace_bytes(ctypes.byref(v), 24, 512)
     rec = (6 * 256 + 12) * 4
-    assert ws > 0 and ws % (512 * 4 * rec) == 0
-    assert 2 <= ws // (512 * 4 * rec) <= 64
+    assert ws > tiles and (ws - tiles) % (512 * 4 * rec) == 0
+    assert 2 <= (ws - tiles) // (512 * 4 * rec) <= 64
     short = _view(page_tokens=256, kv_heads=4, head_dim=256)
-    assert lib.miikv_suffix_workspace_bytes(ctypes.byref(short), 24, 16) == 0  # <= 256 keys
+    assert lib.miikv_suffix_workspace_bytes(ctypes.byref(short), 24, 16) == 4 * 8 * 2 * 256 * 32 * 2
     assert lib.miikv_suffix_workspace_bytes(ctypes.byref(v), 24, 0) == 0
     assert lib.miikv_suffix_workspace_bytes(ctypes.byref(v), 25, 512) == 0  # invalid heads
