@@ -196,6 +196,19 @@ __device__ __forceinline__ float16v mfma_32x32x16(half8 a, half8 b, float16v c) 
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Wait until at most N vector-memory operations of this wave are outstanding.
+template <uint32_t N>
+__device__ __forceinline__ void wait_vmem_le() {
+    if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else if constexpr (N == 2) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else static_assert(N == 0, "unsupported count");
+}
+#ifndef MIIKV_SUFFIX_BUFS
+#define MIIKV_SUFFIX_BUFS 3
+#endif
+constexpr uint32_t kSufBufs = MIIKV_SUFFIX_BUFS;  // LDS tile buffers (prefetch distance kSufBufs - 1)
 
 template <uint32_t D>
 __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
@@ -204,7 +217,7 @@ __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
     constexpr uint32_t TILE = tile_halves(D);
     constexpr uint32_t CHUNKS = TILE * 2 / 1024;  // 1 KiB copy chunks per step
     static_assert(CHUNKS % kSufWaves == 0, "copy chunks must split evenly over waves");
-    __shared__ __align__(16) _Float16 s_t[2][TILE];
+    __shared__ __align__(16) _Float16 s_t[kSufBufs][TILE];
 
     uint32_t T = a.token_count;
     uint32_t P = a.base_position;
@@ -213,17 +226,18 @@ __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
         T = min(T, a.ps->token_count);
     }
     const uint32_t G = a.group;
-    // XCD-aware order: workgroup L runs on XCD L % 8, so the row blocks of one
-    // (kv head, split) group, which read the same tiles, are given to one XCD and
-    // share its L2.  Groups g = xcd, xcd + 8, ...; the grid is padded to a
-    // multiple of 8 groups.
+    // XCD-aware order: workgroup L runs on XCD L % 8.  Each XCD gets an equal,
+    // contiguous range of the (group, row block) sequence, group-major, so the
+    // row blocks of one (kv head, split) group, which read the same tiles, share
+    // an L2.  The grid is padded to a multiple of 8 workgroups.
     const uint32_t L = blockIdx.x;
-    const uint32_t jx = L / 8;
-    const uint32_t grp = (L % 8) + 8 * (jx / a.row_blocks);
+    const uint32_t per_xcd = gridDim.x / 8;
+    const uint32_t idx = (L % 8) * per_xcd + L / 8;
+    const uint32_t grp = idx / a.row_blocks;
     if (grp >= a.g.kv_heads * a.splits) return;
     const uint32_t h = grp % a.g.kv_heads;
     const uint32_t split = grp / a.g.kv_heads;
-    const uint32_t rb = jx % a.row_blocks;
+    const uint32_t rb = idx % a.row_blocks;
     const uint32_t tid = threadIdx.x;
     const uint32_t wave = tid >> 6;
     const uint32_t lane = tid & 63;
@@ -295,14 +309,19 @@ __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
 #pragma unroll
     for (uint32_t mt = 0; mt < NB; ++mt) O[mt] = float16v{};
 
-    fetch(s_begin, s_begin & 1);
+    // Step s lives in buffer s % kSufBufs; the fetch of step s + kSufBufs - 1 is
+    // issued at the top of step s into the buffer released by the last barrier.
+    constexpr uint32_t kPer = CHUNKS / kSufWaves;  // loads per wave per fetch
+    for (uint32_t k = 0; k + 1 < kSufBufs; ++k)
+        if (s_begin + k < s_end) fetch(s_begin + k, (s_begin + k) % kSufBufs);
     wait_vmem();
     __syncthreads();
 
     for (uint32_t s = s_begin; s < s_end; ++s) {
-        const uint32_t buf = s & 1;
+        const uint32_t buf = s % kSufBufs;
+        const bool ahead = s + kSufBufs - 1 < s_end;
 #ifndef MIIKV_SFX_EXP_NOFETCH
-        if (s + 1 < s_end) fetch(s + 1, buf ^ 1);  // buffer buf^1 was released by the last barrier
+        if (ahead) fetch(s + kSufBufs - 1, (s + kSufBufs - 1) % kSufBufs);
 #endif
 #ifdef MIIKV_SFX_EXP_NOLDS
         // registers stand in for the LDS fragments
@@ -373,7 +392,9 @@ __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
 #else
                 O[mt] = mfma_32x32x16(MIIKV_FRAG_V(2 * mt + kc), pb[kc], O[mt]);
 #endif
-        wait_vmem();
+        // Step s+1's tile must have landed; this step's own fetch may stay in flight.
+        if (ahead) wait_vmem_le<(kSufBufs > 2 ? kPer : 0)>();
+        else wait_vmem();
         __syncthreads();
     }
 
@@ -504,12 +525,11 @@ SuffixPlan make_suffix_plan(const miikv_view* v, uint32_t q_heads, uint32_t toke
     p.split_keys = static_cast<uint32_t>(std::min<uint64_t>(static_cast<uint64_t>(p.steps) * kSufStep, 0xffffff00u));
     if (!allow_split) return p;
     const uint64_t wgs = (static_cast<uint64_t>(tokens) * G + kSufRows - 1) / kSufRows * v->kv_heads;
-    // Splits: enough workgroups for about three quarters of the resident slots.
-    // More splits fill the chip better but cost record traffic and, measured at
-    // config 4, more concurrent tile streams through L2: 4 splits (192 workgroups)
-    // ran faster than 5 (240) or 8 (384).
+    // Splits: as many as keep every workgroup resident in one round (the
+    // per-workgroup cost does not shrink with more concurrent workgroups, so a
+    // second partial round costs a full one), at least 256 keys each.
     const uint64_t by_keys = std::min<uint64_t>((key_bound + 255) / 256, kSufMaxSplits);
-    uint64_t want = (kSufSlots * 3 / 4 + wgs - 1) / wgs;
+    uint64_t want = std::max<uint64_t>(1, kSufSlots / wgs);
     if (const char* e = std::getenv("MIIKV_SUFFIX_SPLITS")) want = std::strtoul(e, nullptr, 10);
     want = std::max<uint64_t>(1, std::min<uint64_t>({want, by_keys, kSufMaxSplits}));
     if (want <= 1) return p;
@@ -601,7 +621,7 @@ extern "C" miikv_status miikv_suffix_attn(const miikv_view* view, const void* q,
     a.gate = gate;
     a.gated_out = gated_out;
     const uint64_t groups = static_cast<uint64_t>(view->kv_heads) * plan.splits;
-    const uint64_t wgs = ((groups + 7) / 8) * 8 * blocks;
+    const uint64_t wgs = (groups * blocks + 7) / 8 * 8;
     if (wgs > 0x7fffffffu) return MIIKV_EINVAL;
     const dim3 grid(static_cast<uint32_t>(wgs));
     if (view->head_dim == 128) hipLaunchKernelGGL(suffix_kernel<128>, grid, dim3(64 * kSufWaves), 0, s, a);
