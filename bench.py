@@ -215,7 +215,7 @@ def bench_c4(dev, args) -> int:
         "value": round(flops / (us_step * 1e-6) / 1e12, 2), "us_per_step": round(us_step, 2),
         "n_gpus": 1,
         "config": {"workload": "config 4: 512-token suffix over 8192-token prefix, 24q/4kv/D256"},
-        "roofline": {"bound": "mfma", "kernel": "suffix_kernel<256>",
+        "roofline": {"bound": "mfma", "kernel": "miikv_suffix_attn = expand_kernel<256> + suffix_kernel<256> + suffix_combine_kernel<256>",
                      "achieved": round(flops / (us_attn * 1e-6) / 1e12, 2), "peak": 2500.0,
                      "unit": "TFLOP/s", "frac": round(flops / (us_attn * 1e-6) / 1e12 / 2500.0, 4),
                      "algorithmic_flops_per_launch": flops, "avg_launch_us": round(us_attn, 2)},
