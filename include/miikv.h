@@ -133,6 +133,22 @@ miikv_status miikv_append_f16(const miikv_view* view, const uint16_t* k, const u
                               const miikv_prefill_state* prefill_state,
                               const miikv_decode_state* decode_state, void* stream);
 
+/* fp32 K/V rows (layout [token][kv_head][head_dim]) into the cache, as
+ * miikv_append_f16.  With k_norm_weight != NULL (device fp32 [head_dim],
+ * head_dim >= 64) each K row first gets the reference's prologue: RMSNorm
+ * x * rsqrt(mean(x^2) + epsilon) * w, then RoPE on dims 0..63 (pairs i, i+32,
+ * angle position * theta^(-2i/64)) at its absolute position.  V is stored as
+ * given.  This is the drop-in for
+ * launch_qwen35_decoupled_k_norm_rope_kv_store_batch_quant
+ * (include/miinfer/qwen3_gpu_primitives.hpp:695-717; kernel
+ * gfx906/kernels/qwen3_primitives.hip:7213-7365, prologue :7257-7281 and
+ * :622-659), with one scale per 32-value block and any head_dim multiple of 32. */
+miikv_status miikv_append_f32(const miikv_view* view, const float* k, const float* v,
+                              const float* k_norm_weight, uint32_t token_count, uint32_t base_position,
+                              uint32_t seq, float theta, float epsilon,
+                              const miikv_prefill_state* prefill_state,
+                              const miikv_decode_state* decode_state, void* stream);
+
 /* Batched decode append: one fp16 K/V row per sequence (layout [batch][kv_head]
  * [head_dim]); sequence b's row goes to position d_positions[b] (device array).
  * No reference counterpart for batching: the reference decodes one sequence
@@ -168,6 +184,21 @@ miikv_status miikv_decode_attn(const miikv_view* view, const void* q, uint32_t q
                                uint32_t max_context, float* out, const float* gate,
                                float* gated_out, void* workspace, uint64_t workspace_bytes,
                                void* stream);
+
+/* miikv_decode_attn plus the reference's Q8_1 output epilogue: with gate set,
+ * gated_q8_1 (nullable, device, 36-byte blocks {fp16 d, fp16 s, int8 qs[32]},
+ * [batch][q_heads][head_dim/32]) receives gated_out quantized per 32 values:
+ * d = amax/127, qs = clamp(roundf(x/d), -127, 127), s = sum(qs)*d — the
+ * `gated_output_q8` argument of launch_qwen35_tiled_online_attention_quant_dynamic
+ * (include/miinfer/qwen3_gpu_primitives.hpp:719-741; emit
+ * gfx906/kernels/qwen3_primitives.hip:2354-2384; block
+ * include/miinfer/q4_q8_gemv.hpp:23-27), consumed by the O-projection GEMV.
+ * gated_out may then be NULL. */
+miikv_status miikv_decode_attn_q8_1(const miikv_view* view, const void* q, uint32_t q_dtype, uint32_t q_heads,
+                                    float scale, uint32_t batch, const uint32_t* d_lengths,
+                                    const miikv_decode_state* decode_state, uint32_t max_context, float* out,
+                                    const float* gate, float* gated_out, void* gated_q8_1, void* workspace,
+                                    uint64_t workspace_bytes, void* stream);
 
 /* ---- suffix (multi-token) attention over a cached prefix ----------------- */
 

@@ -66,10 +66,14 @@ SIGNATURES = {
     "miikv_plane_bytes": (ctypes.c_int, [_VP, ctypes.POINTER(_U64), ctypes.POINTER(_U64)]),
     "miikv_append_f16": (ctypes.c_int, [_VP, _P, _P, _U32, _U32, _U32, _P, _P, _P]),
     "miikv_append_batch_f16": (ctypes.c_int, [_VP, _P, _P, _U32, _P, _P]),
+    "miikv_append_f32": (ctypes.c_int, [_VP, _P, _P, _P, _U32, _U32, _U32, ctypes.c_float,
+                                         ctypes.c_float, _P, _P, _P]),
     "miikv_decode_workspace_bytes": (_U64, [_VP, _U32, _U32, _U32]),
     "miikv_workspace_init": (ctypes.c_int, [_P, _U64, _P]),
     "miikv_decode_attn": (ctypes.c_int, [_VP, _P, _U32, _U32, ctypes.c_float, _U32, _P, _P, _U32,
                                           _P, _P, _P, _P, _U64, _P]),
+    "miikv_decode_attn_q8_1": (ctypes.c_int, [_VP, _P, _U32, _U32, ctypes.c_float, _U32, _P, _P, _U32,
+                                               _P, _P, _P, _P, _P, _U64, _P]),
     "miikv_export_canonical": (ctypes.c_int, [_VP, _U32, _U32, _U32, _P, _P, _P, _P, _P]),
     "miikv_import_canonical": (ctypes.c_int, [_VP, _U32, _U32, _U32, _P, _P, _P, _P, _P]),
     "miikv_copy_pages": (ctypes.c_int, [_VP, _P, _P, _U32, _P]),

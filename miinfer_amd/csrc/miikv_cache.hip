@@ -31,12 +31,85 @@ uint64_t view_seq_capacity(const miikv_view* v) {
 
 namespace {
 
+// Row inputs of the append kernel: fp16 rows, or fp32 rows with the optional K
+// prologue of the reference store kernel (RMSNorm * weight, RoPE on dims 0..63).
+struct AppendIn {
+    const void* k;
+    const void* v;
+    const float* k_norm_weight;  // fp32 input only; null: no prologue
+    float theta;
+    float epsilon;
+};
+
+__device__ __forceinline__ void load16_f16(const uint16_t* p, float (&x)[16]) {
+    const uint4 a = *reinterpret_cast<const uint4*>(p);
+    const uint4 b = *reinterpret_cast<const uint4*>(p + 8);
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        x[2 * i] = f16_bits_to_f32(static_cast<uint16_t>(w[i] & 0xffffu));
+        x[2 * i + 1] = f16_bits_to_f32(static_cast<uint16_t>(w[i] >> 16));
+    }
+}
+
+__device__ __forceinline__ void load16_f32(const float* p, float (&x)[16]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 f = *reinterpret_cast<const float4*>(p + 4 * i);
+        x[4 * i] = f.x;
+        x[4 * i + 1] = f.y;
+        x[4 * i + 2] = f.z;
+        x[4 * i + 3] = f.w;
+    }
+}
+
+// K prologue on one lane's 16 dims d0 = 16*q16 ..: the row's sum of squares is
+// reduced over its D/16 lanes; RoPE pairs (i, i+32), i < 32, sit in lanes q16
+// and q16 ^ 2.  Pair i's angle is position * s^i with s = theta^(-2/64),
+// accumulated by repeated fp32 multiplication as in the reference
+// (gfx906/kernels/qwen3_primitives.hip:622-659, 7257-7281).
+__device__ __forceinline__ void k_norm_rope16(float (&x)[16], const float* w, uint32_t q16, uint32_t groups,
+                                              uint32_t D, uint32_t position, float theta, float eps) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ss += x[i] * x[i];
+    for (uint32_t o = 1; o < groups; o <<= 1) ss += __shfl_xor(ss, o, 64);
+    const float r = rsqrtf(ss / static_cast<float>(D) + eps);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 wv = *reinterpret_cast<const float4*>(w + 16 * q16 + 4 * i);
+        x[4 * i] = x[4 * i] * r * wv.x;
+        x[4 * i + 1] = x[4 * i + 1] * r * wv.y;
+        x[4 * i + 2] = x[4 * i + 2] * r * wv.z;
+        x[4 * i + 3] = x[4 * i + 3] * r * wv.w;
+    }
+    float partner[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) partner[i] = __shfl_xor(x[i], 2, 64);
+    if (q16 >= 4) return;
+    const float step = powf(theta, -2.0f / 64.0f);
+    float angle = static_cast<float>(position);
+    const uint32_t i0 = 16 * (q16 & 1);  // first pair index of this lane
+    for (uint32_t i = 0; i < i0; ++i) angle *= step;
+    const bool low = q16 < 2;           // dims i (low) or i + 32 (high) of the pairs
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        float sn, cs;
+        sincosf(angle, &sn, &cs);
+        if (low) x[j] = x[j] * cs - partner[j] * sn;
+        else x[j] = partner[j] * sn + x[j] * cs;
+        angle *= step;
+    }
+}
+
 // One thread per (row, 16-dim group); a row is (token, kv_head).  Adjacent
-// lanes (2i, 2i+1) hold the two halves of one 32-value block.
+// lanes (2i, 2i+1) hold the two halves of one 32-value block, and the D/16
+// lanes of a row are consecutive.
+template <bool F32>
 __global__ void __launch_bounds__(256) append_kernel(
-    Geo g, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, uint32_t token_count,
-    uint32_t base_position, uint32_t seq, const miikv_prefill_state* __restrict__ ps,
-    const miikv_decode_state* __restrict__ ds, const uint32_t* __restrict__ positions) {
+    Geo g, AppendIn in, uint32_t token_count, uint32_t base_position, uint32_t seq,
+    const miikv_prefill_state* __restrict__ ps, const miikv_decode_state* __restrict__ ds,
+    const uint32_t* __restrict__ positions) {
     if (ps != nullptr) {
         base_position = ps->base_position;
         token_count = min(token_count, ps->token_count);
@@ -51,7 +124,7 @@ __global__ void __launch_bounds__(256) append_kernel(
     const uint32_t q16 = static_cast<uint32_t>(gid % groups);
     const uint32_t token = static_cast<uint32_t>(row / g.kv_heads);
     const uint32_t head = static_cast<uint32_t>(row % g.kv_heads);
-    if (token >= token_count) return;  // whole (even, odd) pairs exit together
+    if (token >= token_count) return;  // whole rows exit together
 
     uint32_t pos;
     if (positions != nullptr) {  // batched decode: row `token` is sequence `token`
@@ -67,25 +140,14 @@ __global__ void __launch_bounds__(256) append_kernel(
 
     const size_t src = static_cast<size_t>(row) * D + q16 * 16;
     float xk[16], xv[16];
-    {
-        const uint4 a = *reinterpret_cast<const uint4*>(k + src);
-        const uint4 b = *reinterpret_cast<const uint4*>(k + src + 8);
-        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            xk[2 * i] = f16_bits_to_f32(static_cast<uint16_t>(w[i] & 0xffffu));
-            xk[2 * i + 1] = f16_bits_to_f32(static_cast<uint16_t>(w[i] >> 16));
-        }
-    }
-    {
-        const uint4 a = *reinterpret_cast<const uint4*>(v + src);
-        const uint4 b = *reinterpret_cast<const uint4*>(v + src + 8);
-        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            xv[2 * i] = f16_bits_to_f32(static_cast<uint16_t>(w[i] & 0xffffu));
-            xv[2 * i + 1] = f16_bits_to_f32(static_cast<uint16_t>(w[i] >> 16));
-        }
+    if constexpr (F32) {
+        load16_f32(static_cast<const float*>(in.k) + src, xk);
+        load16_f32(static_cast<const float*>(in.v) + src, xv);
+        if (in.k_norm_weight != nullptr)
+            k_norm_rope16(xk, in.k_norm_weight, q16, groups, D, pos, in.theta, in.epsilon);
+    } else {
+        load16_f16(static_cast<const uint16_t*>(in.k) + src, xk);
+        load16_f16(static_cast<const uint16_t*>(in.v) + src, xv);
     }
     int8_t qk[16], qv[16];
     float sk, sv;
@@ -291,17 +353,25 @@ extern "C" miikv_status miikv_plane_bytes(const miikv_view* view, uint64_t* code
     return MIIKV_OK;
 }
 
-static miikv_status launch_append(const miikv_view* view, const uint16_t* k, const uint16_t* v, uint32_t rows_tokens,
-                                  uint32_t base, uint32_t seq, const miikv_prefill_state* ps,
-                                  const miikv_decode_state* ds, const uint32_t* positions, void* stream) {
+template <bool F32>
+static miikv_status launch_append(const miikv_view* view, const AppendIn& in, uint32_t rows_tokens, uint32_t base,
+                                  uint32_t seq, const miikv_prefill_state* ps, const miikv_decode_state* ds,
+                                  const uint32_t* positions, void* stream) {
     const uint64_t threads = static_cast<uint64_t>(rows_tokens) * view->kv_heads * (view->head_dim / 16);
     if (threads == 0) return MIIKV_OK;
     const uint64_t blocks = (threads + 255) / 256;
     if (blocks > 0x7fffffffu) return MIIKV_EINVAL;
-    hipLaunchKernelGGL(append_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), make_geo(*view), k, v, rows_tokens, base, seq, ps, ds,
+    hipLaunchKernelGGL(append_kernel<F32>, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), make_geo(*view), in, rows_tokens, base, seq, ps, ds,
                        positions);
     return launch_status();
+}
+
+static AppendIn f16_rows(const uint16_t* k, const uint16_t* v) {
+    AppendIn in{};
+    in.k = k;
+    in.v = v;
+    return in;
 }
 
 extern "C" miikv_status miikv_append_f16(const miikv_view* view, const uint16_t* k, const uint16_t* v,
@@ -316,7 +386,33 @@ extern "C" miikv_status miikv_append_f16(const miikv_view* view, const uint16_t*
         static_cast<uint64_t>(base_position) + token_count > view_seq_capacity(view))
         return MIIKV_EINVAL;
     if (view->layout == MIIKV_LAYOUT_CONTIGUOUS && seq != 0) return MIIKV_EINVAL;
-    return launch_append(view, k, v, token_count, base_position, seq, prefill_state, decode_state, nullptr, stream);
+    return launch_append<false>(view, f16_rows(k, v), token_count, base_position, seq, prefill_state, decode_state,
+                                nullptr, stream);
+}
+
+extern "C" miikv_status miikv_append_f32(const miikv_view* view, const float* k, const float* v,
+                                         const float* k_norm_weight, uint32_t token_count, uint32_t base_position,
+                                         uint32_t seq, float theta, float epsilon,
+                                         const miikv_prefill_state* prefill_state,
+                                         const miikv_decode_state* decode_state, void* stream) {
+    const int st = validate_view(view);
+    if (st != MIIKV_OK) return st;
+    if (k == nullptr || v == nullptr) return MIIKV_EINVAL;
+    if (k_norm_weight != nullptr && (view->head_dim < 64 || !std::isfinite(theta) || !std::isfinite(epsilon)))
+        return MIIKV_EINVAL;
+    if (decode_state != nullptr && prefill_state == nullptr) token_count = 1;
+    if (prefill_state == nullptr && decode_state == nullptr &&
+        static_cast<uint64_t>(base_position) + token_count > view_seq_capacity(view))
+        return MIIKV_EINVAL;
+    if (view->layout == MIIKV_LAYOUT_CONTIGUOUS && seq != 0) return MIIKV_EINVAL;
+    AppendIn in{};
+    in.k = k;
+    in.v = v;
+    in.k_norm_weight = k_norm_weight;
+    in.theta = theta;
+    in.epsilon = epsilon;
+    return launch_append<true>(view, in, token_count, base_position, seq, prefill_state, decode_state, nullptr,
+                               stream);
 }
 
 extern "C" miikv_status miikv_append_batch_f16(const miikv_view* view, const uint16_t* k, const uint16_t* v,
@@ -325,7 +421,7 @@ extern "C" miikv_status miikv_append_batch_f16(const miikv_view* view, const uin
     if (st != MIIKV_OK) return st;
     if (k == nullptr || v == nullptr || d_positions == nullptr) return MIIKV_EINVAL;
     if (view->layout == MIIKV_LAYOUT_CONTIGUOUS && batch > 1) return MIIKV_EINVAL;
-    return launch_append(view, k, v, batch, 0, 0, nullptr, nullptr, d_positions, stream);
+    return launch_append<false>(view, f16_rows(k, v), batch, 0, 0, nullptr, nullptr, d_positions, stream);
 }
 
 template <bool EXPORT>

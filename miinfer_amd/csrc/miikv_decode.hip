@@ -496,11 +496,12 @@ extern "C" miikv_status miikv_workspace_init(void* workspace, uint64_t bytes, vo
     return hip_status(hipGetLastError());
 }
 
-extern "C" miikv_status miikv_decode_attn(const miikv_view* view, const void* q, uint32_t q_dtype, uint32_t q_heads,
-                                          float scale, uint32_t batch, const uint32_t* d_lengths,
-                                          const miikv_decode_state* decode_state, uint32_t max_context, float* out,
-                                          const float* gate, float* gated_out, void* workspace,
-                                          uint64_t workspace_bytes, void* stream) {
+extern "C" miikv_status miikv_decode_attn_q8_1(const miikv_view* view, const void* q, uint32_t q_dtype,
+                                               uint32_t q_heads, float scale, uint32_t batch,
+                                               const uint32_t* d_lengths, const miikv_decode_state* decode_state,
+                                               uint32_t max_context, float* out, const float* gate,
+                                               float* gated_out, void* gated_q8_1, void* workspace,
+                                               uint64_t workspace_bytes, void* stream) {
     const int st = validate_view(view);
     if (st != MIIKV_OK) return st;
     if (q == nullptr || batch == 0 || q_heads == 0 || q_heads % view->kv_heads != 0 || !std::isfinite(scale))
@@ -508,8 +509,10 @@ extern "C" miikv_status miikv_decode_attn(const miikv_view* view, const void* q,
     const uint32_t G = q_heads / view->kv_heads;
     if (G > 16) return MIIKV_EUNSUPPORTED;
     if (q_dtype != MIIKV_DTYPE_F16 && q_dtype != MIIKV_DTYPE_F32) return MIIKV_EINVAL;
-    if (out == nullptr && !(gate != nullptr && gated_out != nullptr)) return MIIKV_EINVAL;
-    if ((gate == nullptr) != (gated_out == nullptr)) return MIIKV_EINVAL;
+    if (out == nullptr && !(gate != nullptr && (gated_out != nullptr || gated_q8_1 != nullptr)))
+        return MIIKV_EINVAL;
+    if (gate == nullptr && (gated_out != nullptr || gated_q8_1 != nullptr)) return MIIKV_EINVAL;
+    if (gate != nullptr && gated_out == nullptr && gated_q8_1 == nullptr) return MIIKV_EINVAL;
     if (d_lengths == nullptr && (decode_state == nullptr || batch != 1)) return MIIKV_EINVAL;
     if (max_context == 0 || max_context > view_seq_capacity(view)) return MIIKV_EINVAL;
     if (view->layout == MIIKV_LAYOUT_CONTIGUOUS && batch != 1) return MIIKV_EINVAL;
@@ -542,6 +545,7 @@ extern "C" miikv_status miikv_decode_attn(const miikv_view* view, const void* q,
     a.out = out;
     a.gate = gate;
     a.gated_out = gated_out;
+    a.gated_q8_1 = static_cast<uint8_t*>(gated_q8_1);
 
     const size_t lds = (32 * kWavesPerWg + kWavesPerWg * G * view->head_dim) * sizeof(float) +
                        kWavesPerWg * 2 * kChunk * (view->head_dim / 32) * sizeof(uint16_t);
@@ -560,4 +564,13 @@ extern "C" miikv_status miikv_decode_attn(const miikv_view* view, const void* q,
         hipLaunchKernelGGL((combine_kernel<256>), cgrid, dim3(256), 0, s, a);
     }
     return hip_status(hipGetLastError());
+}
+
+extern "C" miikv_status miikv_decode_attn(const miikv_view* view, const void* q, uint32_t q_dtype, uint32_t q_heads,
+                                          float scale, uint32_t batch, const uint32_t* d_lengths,
+                                          const miikv_decode_state* decode_state, uint32_t max_context, float* out,
+                                          const float* gate, float* gated_out, void* workspace,
+                                          uint64_t workspace_bytes, void* stream) {
+    return miikv_decode_attn_q8_1(view, q, q_dtype, q_heads, scale, batch, d_lengths, decode_state, max_context, out,
+                                  gate, gated_out, nullptr, workspace, workspace_bytes, stream);
 }

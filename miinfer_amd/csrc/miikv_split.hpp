@@ -31,6 +31,7 @@ struct SplitArgs {
     float* out;
     const float* gate;
     float* gated_out;
+    uint8_t* gated_q8_1;  // nullable: Q8_1 blocks [batch][q_heads][D/32] of gated_out
 };
 
 __device__ __forceinline__ float exp2_safe(float x) { return exp2f(x); }  // exp2(-inf) == 0
@@ -143,11 +144,42 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
     // out = acc / L, 0 when L == 0 (qwen3_primitives.hip:2349); gated = out * sigmoid(gate).
     const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
     const float vals[4] = {o.x * inv, o.y * inv, o.z * inv, o.w * inv};
+    float gated[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (uint32_t k = 0; k < 4; ++k) {
         const size_t oi = out_row0 + e + k;
         if (a.out) a.out[oi] = vals[k];
-        if (a.gate && a.gated_out) a.gated_out[oi] = vals[k] * (1.0f / (1.0f + expf(-a.gate[oi])));
+        if (a.gate) {
+            gated[k] = vals[k] * (1.0f / (1.0f + expf(-a.gate[oi])));
+            if (a.gated_out) a.gated_out[oi] = gated[k];
+        }
+    }
+    if (a.gate && a.gated_q8_1) {
+        // Q8_1 block of 32 gated values = 8 consecutive lanes (qwen3_primitives.hip:
+        // 2354-2384): d = amax/127, q = clamp(roundf(x/d), -127, 127), s = sum(q)*d.
+        float amax = fmaxf(fmaxf(fabsf(gated[0]), fabsf(gated[1])), fmaxf(fabsf(gated[2]), fabsf(gated[3])));
+#pragma unroll
+        for (uint32_t off = 1; off < 8; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+        const float d = amax / 127.0f;
+        const float qinv = d != 0.0f ? 1.0f / d : 0.0f;
+        int qs[4];
+        int sum = 0;
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k) {
+            qs[k] = max(-127, min(127, static_cast<int>(roundf(gated[k] * qinv))));
+            sum += qs[k];
+        }
+#pragma unroll
+        for (uint32_t off = 1; off < 8; off <<= 1) sum += __shfl_xor(sum, off, 64);
+        const size_t blk = (out_row0 + e) / 32;
+        uint8_t* bp = a.gated_q8_1 + blk * 36;
+        *reinterpret_cast<uint32_t*>(bp + 4 + 4 * (e4 & 7)) =
+            (static_cast<uint32_t>(qs[0]) & 0xffu) | ((static_cast<uint32_t>(qs[1]) & 0xffu) << 8) |
+            ((static_cast<uint32_t>(qs[2]) & 0xffu) << 16) | ((static_cast<uint32_t>(qs[3]) & 0xffu) << 24);
+        if ((e4 & 7) == 0) {
+            *reinterpret_cast<uint16_t*>(bp) = f32_to_f16_bits(d);
+            *reinterpret_cast<uint16_t*>(bp + 2) = f32_to_f16_bits(static_cast<float>(sum) * d);
+        }
     }
 }
 

@@ -136,6 +136,27 @@ class KvCache:
         call("miikv_append_f16", self.view, _ptr(k), _ptr(v), t, base_position, seq,
              _ptr(prefill_state), _ptr(decode_state), _stream(stream))
 
+    def append_f32(self, k: torch.Tensor, v: torch.Tensor, base_position: int = 0, seq: int = 0, *,
+                   k_norm_weight: torch.Tensor | None = None, theta: float = 1.0e7, epsilon: float = 1.0e-6,
+                   prefill_state: torch.Tensor | None = None, decode_state: torch.Tensor | None = None,
+                   stream=None) -> None:
+        """fp32 rows k, v [T, kv_heads, head_dim]; with k_norm_weight ([head_dim] fp32) K first
+        gets RMSNorm * weight and RoPE on dims 0..63 at its position (the reference's fused
+        store prologue)."""
+        for t in (k, v):
+            if t.dtype != torch.float32 or t.dim() != 3 or \
+                    tuple(t.shape[1:]) != (self.kv_heads, self.head_dim) or not t.is_contiguous():
+                raise ValueError(f"rows must be contiguous fp32 [T, {self.kv_heads}, {self.head_dim}]")
+        if k.shape != v.shape:
+            raise ValueError("k and v shapes differ")
+        if k_norm_weight is not None and (k_norm_weight.dtype != torch.float32 or
+                                          k_norm_weight.numel() != self.head_dim):
+            raise ValueError("k_norm_weight must be fp32 [head_dim]")
+        self._check_seq(seq)
+        call("miikv_append_f32", self.view, _ptr(k), _ptr(v), _ptr(k_norm_weight), k.shape[0],
+             base_position, seq, float(theta), float(epsilon), _ptr(prefill_state),
+             _ptr(decode_state), _stream(stream))
+
     def append_batch(self, k: torch.Tensor, v: torch.Tensor, positions: torch.Tensor,
                      stream=None) -> None:
         """One row per sequence: k, v [B, kv_heads, head_dim]; positions [B] device."""
@@ -252,12 +273,14 @@ def decode_attention(cache: KvCache, q: torch.Tensor, scale: float | None = None
                      lengths: torch.Tensor | None = None, decode_state: torch.Tensor | None = None,
                      max_context: int | None = None, gate: torch.Tensor | None = None,
                      out: torch.Tensor | None = None, gated_out: torch.Tensor | None = None,
+                     gated_q8_1: torch.Tensor | None = None,
                      workspace: DecodeWorkspace | None = None, stream=None):
     """Single-token GQA attention over the q8_0 cache.
 
     q: [batch, q_heads, head_dim] fp16 or fp32.  Context lengths come from
-    `lengths` (device [batch]) or `decode_state` (position + 1).
-    Returns (out, gated_out)."""
+    `lengths` (device [batch]) or `decode_state` (position + 1).  With `gate`,
+    `gated_q8_1` (uint8 [batch * q_heads * head_dim / 32, 36]) receives the gated
+    output as Q8_1 blocks.  Returns (out, gated_out)."""
     batch, q_heads, d = q.shape
     if d != cache.head_dim or not q.is_contiguous() or q.dtype not in (torch.float16,
                                                                         torch.float32):
@@ -286,10 +309,16 @@ def decode_attention(cache: KvCache, q: torch.Tensor, scale: float | None = None
         out = torch.empty((batch, q_heads, d), dtype=torch.float32, device=q.device)
     if gate is not None and gated_out is None:
         gated_out = torch.empty((batch, q_heads, d), dtype=torch.float32, device=q.device)
+    if gated_q8_1 is not None:
+        if gate is None:
+            raise ValueError("gated_q8_1 needs a gate")
+        if gated_q8_1.dtype != torch.uint8 or not gated_q8_1.is_contiguous() or \
+                gated_q8_1.numel() < batch * q_heads * (d // QBLOCK) * 36:
+            raise ValueError("gated_q8_1 must be contiguous uint8 [batch*q_heads*D/32, 36]")
     qd = _lib.DTYPE_F16 if q.dtype == torch.float16 else _lib.DTYPE_F32
-    call("miikv_decode_attn", cache.view, _ptr(q), qd, q_heads, float(scale), batch,
+    call("miikv_decode_attn_q8_1", cache.view, _ptr(q), qd, q_heads, float(scale), batch,
          _ptr(lengths), _ptr(decode_state), max_context, _ptr(out), _ptr(gate), _ptr(gated_out),
-         _ptr(workspace.buf), workspace.bytes, _stream(stream))
+         _ptr(gated_q8_1), _ptr(workspace.buf), workspace.bytes, _stream(stream))
     return out, gated_out
 
 

@@ -46,6 +46,9 @@ def _load() -> ctypes.CDLL:
     lib.miikv_oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
     lib.miikv_oracle_q8_0_block.argtypes = [_f32p, _i8p, _u16p]
     lib.miikv_oracle_quantize_rows_f16.argtypes = [_u16p, ctypes.c_size_t, _u32, _i8p, _u16p]
+    lib.miikv_oracle_quantize_rows_f32.argtypes = [_f32p, ctypes.c_size_t, _u32, _i8p, _u16p]
+    lib.miikv_oracle_k_norm_rope.argtypes = [_f32p, _f32p, _u32, _u32, ctypes.c_float, ctypes.c_float, _f32p]
+    lib.miikv_oracle_q8_1_block.argtypes = [_f32p, ctypes.POINTER(ctypes.c_uint8)]
     lib.miikv_oracle_dequantize_rows.argtypes = [_i8p, _u16p, ctypes.c_size_t, _u32, _f32p]
     lib.miikv_oracle_attention_f32.argtypes = [_f32p, _f32p, _f32p, _u32, _u32, _u32, _u32, _u32,
                                                ctypes.c_float, _f32p, _f32p]
@@ -123,6 +126,34 @@ def quantize_rows(rows_f16: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     lib().miikv_oracle_quantize_rows_f16(_p(rows.view(np.uint16), _u16p), n, d,
                                          _p(codes, _i8p), _p(scales, _u16p))
     return codes, scales
+
+
+def quantize_rows_f32(rows: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """rows [..., head_dim] float32 -> (codes int8, scales uint16 [..., head_dim/32])."""
+    rows = np.ascontiguousarray(rows, dtype=np.float32)
+    d = rows.shape[-1]
+    codes = np.zeros(rows.shape, np.int8)
+    scales = np.zeros(rows.shape[:-1] + (d // QBLOCK,), np.uint16)
+    lib().miikv_oracle_quantize_rows_f32(_p(rows, _f32p), rows.size // d, d, _p(codes, _i8p), _p(scales, _u16p))
+    return codes, scales
+
+
+def k_norm_rope(x: np.ndarray, w: np.ndarray, position: int, theta: float, eps: float) -> np.ndarray:
+    """One K row after the reference's RMSNorm * weight and RoPE on dims 0..63."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.zeros_like(x)
+    lib().miikv_oracle_k_norm_rope(_p(x, _f32p), _p(w, _f32p), x.size, position, theta, eps, _p(out, _f32p))
+    return out
+
+
+def q8_1_blocks(x: np.ndarray) -> np.ndarray:
+    """Rows of fp32 values (size % 32 == 0) -> uint8 [n_blocks, 36] Q8_1 blocks."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, QBLOCK)
+    out = np.zeros((x.shape[0], 36), np.uint8)
+    for i in range(x.shape[0]):
+        lib().miikv_oracle_q8_1_block(_p(x[i], _f32p), out[i].ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)))
+    return out
 
 
 def dequantize_rows(codes: np.ndarray, scales: np.ndarray) -> np.ndarray:

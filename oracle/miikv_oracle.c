@@ -111,6 +111,61 @@ void miikv_oracle_quantize_rows_f16(const uint16_t* rows, size_t n_rows, uint32_
     }
 }
 
+void miikv_oracle_quantize_rows_f32(const float* rows, size_t n_rows, uint32_t head_dim, int8_t* codes,
+                                    uint16_t* scales) {
+    const uint32_t nblk = head_dim / MIIKV_ORACLE_QBLOCK;
+    for (size_t r = 0; r < n_rows; ++r)
+        for (uint32_t b = 0; b < nblk; ++b)
+            miikv_oracle_q8_0_block(rows + r * head_dim + (size_t)b * MIIKV_ORACLE_QBLOCK,
+                                    codes + r * head_dim + (size_t)b * MIIKV_ORACLE_QBLOCK, scales + r * nblk + b);
+}
+
+/* gfx906/kernels/qwen3_primitives.hip:7257-7281 (RMSNorm * weight, RoPE on dims
+ * 0..63) and :622-659 (compute_qwen35_rope_pair: every pair < 32 falls in a
+ * rotated section, and the three section angles are the same position). */
+void miikv_oracle_k_norm_rope(const float* x, const float* w, uint32_t head_dim, uint32_t position, float theta,
+                              float eps, float* out) {
+    float ss = 0.0f;
+    for (uint32_t d = 0; d < head_dim; ++d) ss += x[d] * x[d];
+    const float r = 1.0f / sqrtf(ss / (float)head_dim + eps);
+    for (uint32_t d = 0; d < head_dim; ++d) out[d] = x[d] * r * w[d];
+    const float step = powf(theta, -2.0f / 64.0f);
+    float angle = (float)position;
+    for (uint32_t i = 0; i < 32; ++i) {
+        const float c = cosf(angle), s = sinf(angle);
+        const float x0 = out[i], x1 = out[i + 32];
+        out[i] = x0 * c - x1 * s;
+        out[i + 32] = x0 * s + x1 * c;
+        angle *= step;
+    }
+}
+
+/* gfx906/kernels/qwen3_primitives.hip:2354-2384; block layout
+ * include/miinfer/q4_q8_gemv.hpp:23-27. */
+void miikv_oracle_q8_1_block(const float* x, uint8_t* block36) {
+    float amax = 0.0f;
+    for (int i = 0; i < MIIKV_ORACLE_QBLOCK; ++i) {
+        const float a = fabsf(x[i]);
+        amax = a > amax ? a : amax;
+    }
+    const float d = amax / 127.0f;
+    const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+    int sum = 0;
+    for (int i = 0; i < MIIKV_ORACLE_QBLOCK; ++i) {
+        long q = lroundf(x[i] * inv); /* half away from zero, as roundf */
+        if (q < -127) q = -127;
+        if (q > 127) q = 127;
+        block36[4 + i] = (uint8_t)(int8_t)q;
+        sum += (int)q;
+    }
+    const uint16_t db = miikv_oracle_f32_to_f16(d);
+    const uint16_t sb = miikv_oracle_f32_to_f16((float)sum * d);
+    block36[0] = (uint8_t)(db & 0xff);
+    block36[1] = (uint8_t)(db >> 8);
+    block36[2] = (uint8_t)(sb & 0xff);
+    block36[3] = (uint8_t)(sb >> 8);
+}
+
 /* src/prefill_v2/kv_cache.cpp:161-169 */
 void miikv_oracle_dequantize_rows(const int8_t* codes, const uint16_t* scales, size_t n_rows,
                                   uint32_t head_dim, float* out) {

@@ -41,6 +41,25 @@ float miikv_oracle_f16_to_f32(uint16_t bits);
  *   q = clamp(rint(x * inv), -128, 127); scale_h = fp16_rn(scale). */
 void miikv_oracle_q8_0_block(const float* x, int8_t* codes, uint16_t* scale_bits);
 
+/* Quantize n_rows rows of head_dim fp32 values per 32-value block (same rule). */
+void miikv_oracle_quantize_rows_f32(const float* rows, size_t n_rows, uint32_t head_dim, int8_t* codes,
+                                    uint16_t* scales);
+
+/* K prologue of the reference store kernel for one row of head_dim values
+ * (gfx906/kernels/qwen3_primitives.hip:7257-7281 with the RoPE pair of :622-659):
+ *   y = x * (1 / sqrt(sum(x^2)/head_dim + eps)) * w;
+ *   for i < 32: a = position * s^i with s = powf(theta, -2/64) accumulated by
+ *   repeated fp32 multiplication; (y_i, y_{i+32}) <- (y_i cos a - y_{i+32} sin a,
+ *   y_i sin a + y_{i+32} cos a).  Dims >= 64 are only normalised. */
+void miikv_oracle_k_norm_rope(const float* x, const float* w, uint32_t head_dim, uint32_t position, float theta,
+                              float eps, float* out);
+
+/* One Q8_1 block (36 bytes: fp16 d, fp16 s, int8 qs[32]) from 32 values, as the
+ * reference decode combine emits it (qwen3_primitives.hip:2354-2384):
+ *   d = amax/127; inv = d != 0 ? 1/d : 0; q = clamp(roundf(x*inv), -127, 127)
+ *   (round half away from zero); s = fp16(sum(q) * d). */
+void miikv_oracle_q8_1_block(const float* x, uint8_t* block36);
+
 /* Quantize n_rows rows of head_dim fp16 values (head_dim % 32 == 0). */
 void miikv_oracle_quantize_rows_f16(const uint16_t* rows, size_t n_rows, uint32_t head_dim,
                                     int8_t* codes, uint16_t* scales);

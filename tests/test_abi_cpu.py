@@ -150,3 +150,21 @@ def test_suffix_workspace_bytes_plan():
     assert lib.miikv_suffix_workspace_bytes(ctypes.byref(short), 24, 16) == 4 * 8 * 2 * 256 * 32 * 2
     assert lib.miikv_suffix_workspace_bytes(ctypes.byref(v), 24, 0) == 0
     assert lib.miikv_suffix_workspace_bytes(ctypes.byref(v), 25, 512) == 0  # invalid heads
+
+
+def test_fused_append_and_q8_1_decode_reject_before_launch():
+    L = _lib()
+    lib = L.lib()
+    v = _view(page_tokens=256, kv_heads=4, head_dim=256)
+    p = ctypes.c_void_p(0x3000)
+    nan = float("nan")
+    # theta / epsilon must be finite when the prologue runs
+    assert lib.miikv_append_f32(ctypes.byref(v), p, p, p, 1, 0, 0, nan, 1e-6, None, None, None) == L.MIIKV_EINVAL
+    assert lib.miikv_append_f32(ctypes.byref(v), p, p, p, 1, 0, 0, 1e7, nan, None, None, None) == L.MIIKV_EINVAL
+    small = _view(page_tokens=256, kv_heads=4, head_dim=32)
+    assert lib.miikv_append_f32(ctypes.byref(small), p, p, p, 1, 0, 0, 1e7, 1e-6, None, None, None) != L.MIIKV_OK
+    assert lib.miikv_append_f32(ctypes.byref(v), p, p, None, 300, 0, 0, 1e7, 1e-6, None, None, None) == L.MIIKV_EINVAL
+    lens = ctypes.c_void_p(0x4000)
+    # Q8_1 output without a gate
+    assert lib.miikv_decode_attn_q8_1(ctypes.byref(v), p, L.DTYPE_F16, 24, 0.0625, 1, lens, None, 256, p, None,
+                                      None, p, p, 1 << 20, None) == L.MIIKV_EINVAL

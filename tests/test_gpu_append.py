@@ -129,3 +129,58 @@ def test_append_rejects_out_of_range(gpu):
     k = torch.zeros((2, 8, 128), dtype=torch.float16, device=gpu)
     with pytest.raises(m.MiikvError):
         cache.append(k, k, base_position=127)  # 127 + 2 > capacity
+
+
+@pytest.mark.parametrize("hk,d", [(8, 128), (4, 256)])
+def test_append_f32_plain_bitexact(gpu, hk, d):
+    """fp32 rows without the prologue: the q8_0 rule on the fp32 values, bit-exact."""
+    import miinfer_amd as m
+    rng = np.random.default_rng(200 + d)
+    t = 130
+    cache = m.KvCache.contiguous(hk, d, 192)
+    k = (rng.standard_normal((t, hk, d)) * 3).astype(np.float32)
+    v = rng.standard_normal((t, hk, d)).astype(np.float32)
+    k.reshape(-1, 32)[0] = 0.0
+    cache.append_f32(_dev(k, gpu), _dev(v, gpu), base_position=0)
+    kc, ks, vc, vs = _export_np(cache, 0, 0, t)
+    ek, eks = oracle.quantize_rows_f32(k.transpose(1, 0, 2))
+    ev, evs = oracle.quantize_rows_f32(v.transpose(1, 0, 2))
+    assert np.array_equal(kc, ek) and np.array_equal(ks, eks)
+    assert np.array_equal(vc, ev) and np.array_equal(vs, evs)
+
+
+@pytest.mark.parametrize("hk,d,theta", [(4, 256, 1.0e7), (8, 128, 1.0e4)])
+def test_append_f32_norm_rope_matches_oracle(gpu, hk, d, theta):
+    """K gets RMSNorm * weight and RoPE at its position before quantisation.  The
+    device's rsqrt/sincos and summation order differ from the oracle's in the last
+    bits, so a code may differ by one where the pre-quantisation value sits on a
+    rounding boundary: at most 0.5% of K codes, none by more than 1; scales within
+    one fp16 ulp; the dequantised K within one quantisation step.  V is bit-exact."""
+    import miinfer_amd as m
+    rng = np.random.default_rng(300 + d)
+    t, base = 70, 1000
+    cache = m.KvCache.contiguous(hk, d, 1088)
+    k = rng.standard_normal((t, hk, d)).astype(np.float32) * 4
+    v = rng.standard_normal((t, hk, d)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    eps = 1.0e-6
+    ps = m.make_prefill_state(base, t, device=gpu)
+    # host base position for the first half, device state for the second
+    cache.append_f32(_dev(k[:35], gpu), _dev(v[:35], gpu), base_position=base,
+                     k_norm_weight=_dev(w, gpu), theta=theta, epsilon=eps)
+    ps[0] = base + 35
+    ps[1] = t - 35
+    cache.append_f32(_dev(k[35:], gpu), _dev(v[35:], gpu), k_norm_weight=_dev(w, gpu), theta=theta,
+                     epsilon=eps, prefill_state=ps)
+    kc, ks, vc, vs = _export_np(cache, 0, base, t)
+    kn = np.stack([[oracle.k_norm_rope(k[i, h], w, base + i, theta, eps) for h in range(hk)]
+                   for i in range(t)])
+    ek, eks = oracle.quantize_rows_f32(kn.transpose(1, 0, 2))
+    ev, evs = oracle.quantize_rows_f32(v.transpose(1, 0, 2))
+    assert np.array_equal(vc, ev) and np.array_equal(vs, evs)
+    diff = np.abs(kc.astype(np.int32) - ek.astype(np.int32))
+    assert diff.max() <= 1 and (diff > 0).mean() <= 5e-3, (diff.max(), (diff > 0).mean())
+    assert np.abs(ks.astype(np.int32) - eks.astype(np.int32)).max() <= 1
+    deq = oracle.dequantize_rows(kc, ks)
+    step = oracle.dequantize_rows(np.ones_like(kc), ks)
+    assert np.all(np.abs(deq - kn.transpose(1, 0, 2)) <= step * 1.01)

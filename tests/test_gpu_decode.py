@@ -139,6 +139,26 @@ def test_decode_paged_batched(gpu, hq, hk, d):
         assert_attention_close(out[s], expect, f"seq {s} L={n}")
 
 
+def test_decode_q8_1_epilogue(gpu):
+    """The Q8_1 blocks are exactly the reference rule applied to the kernel's own
+    gated output (bit-exact), and that output matches the oracle."""
+    import miinfer_amd as m
+    rng = np.random.default_rng(77)
+    hq, hk, d, length = 24, 4, 256, 3000
+    cache, ref = _filled_contiguous(gpu, rng, hk, d, 3072, length)
+    q = randn_f16(rng, (1, hq, d))
+    gate = rng.standard_normal((1, hq, d)).astype(np.float32)
+    blocks = torch.zeros((hq * d // 32, 36), dtype=torch.uint8, device=gpu)
+    lengths = torch.tensor([length], dtype=torch.int32, device=gpu)
+    _, gated = m.decode_attention(cache, _dev(q, gpu), lengths=lengths, gate=_dev(gate, gpu),
+                                  gated_q8_1=blocks)
+    torch.cuda.synchronize()
+    g = gated.cpu().numpy()
+    assert np.array_equal(blocks.cpu().numpy(), oracle.q8_1_blocks(g.reshape(-1)))
+    expect = oracle.attention_q8(q[0].astype(np.float32), *ref, length, hq, 1 / math.sqrt(d))
+    assert_attention_close(g[0], expect / (1 + np.exp(-gate[0])), "gated")
+
+
 def test_decode_rejects_bad_arguments(gpu):
     import miinfer_amd as m
     cache, _ = _filled_contiguous(gpu, np.random.default_rng(6), 8, 128, 256, 4)

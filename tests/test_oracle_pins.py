@@ -259,3 +259,73 @@ def test_token_hash_published_vectors():
     assert oracle.token_hash([]) == 0xCBF29CE484222325
     assert oracle.token_hash([ord("a")]) == 0xAF63DC4C8601EC8C
     assert oracle.token_hash([ord(c) for c in "foobar"]) == 0x85944171F73967E8
+
+
+# ---- fused store prologue (RMSNorm * weight, RoPE on dims 0..63) -------------
+
+def test_k_norm_rope_at_position_zero_is_rmsnorm():
+    """Angle 0 leaves the pairs unrotated: the output is the float64 RMSNorm."""
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal(256).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 256).astype(np.float32)
+    got = oracle.k_norm_rope(x, w, 0, 1.0e7, 1.0e-6)
+    x64 = x.astype(np.float64)
+    expect = x64 / np.sqrt((x64 * x64).mean() + 1.0e-6) * w
+    assert np.max(np.abs(got - expect)) < 2e-6
+
+
+@pytest.mark.parametrize("d,pos,theta", [(256, 7, 1.0e7), (128, 1000, 1.0e4), (256, 65535, 1.0e6)])
+def test_k_norm_rope_rotates_pairs_by_position_angles(d, pos, theta):
+    """Pair i is rotated by its angle (cos/sin in float64), with the sign pattern of
+    a rotation; pair norms are kept, and dims >= 64 are only normalised.  The angles
+    follow the reference's convention of accumulating pos * s^i with s =
+    theta^(-2/64) by repeated fp32 multiplication (qwen3_primitives.hip:636-648);
+    they stay within 2^-20 relative of pos * theta^(-2i/64)."""
+    rng = np.random.default_rng(pos)
+    x = rng.standard_normal(d).astype(np.float32)
+    w = np.ones(d, np.float32)
+    got = oracle.k_norm_rope(x, w, pos, theta, 1.0e-6).astype(np.float64)
+    n = oracle.k_norm_rope(x, w, 0, theta, 1.0e-6).astype(np.float64)
+    step = np.float32(theta) ** np.float32(-2.0 / 64.0)
+    ang = np.empty(32)
+    a = np.float32(pos)
+    for i in range(32):
+        ang[i] = float(a)
+        a = np.float32(a * step)
+    ideal = pos * np.power(float(theta), -2.0 * np.arange(32) / 64.0)
+    assert np.all(np.abs(ang - ideal) <= 2.0 ** -17 * np.maximum(ideal, 1.0))
+    c, s = np.cos(ang), np.sin(ang)
+    exp0 = n[:32] * c - n[32:64] * s
+    exp1 = n[:32] * s + n[32:64] * c
+    assert np.max(np.abs(got[:32] - exp0)) < 2e-5
+    assert np.max(np.abs(got[32:64] - exp1)) < 2e-5
+    assert np.allclose(got[:32] ** 2 + got[32:64] ** 2, n[:32] ** 2 + n[32:64] ** 2, rtol=1e-5, atol=1e-6)
+    assert np.array_equal(got[64:], n[64:])
+
+
+# ---- Q8_1 output blocks -------------------------------------------------------
+
+def test_q8_1_block_closed_forms():
+    rng = np.random.default_rng(32)
+    x = rng.standard_normal(32).astype(np.float32)
+    blk = oracle.q8_1_blocks(x)[0]
+    d = blk[0:2].view(np.float16)[0]
+    s = blk[2:4].view(np.float16)[0]
+    q = blk[4:].view(np.int8).astype(np.int64)
+    amax = np.abs(x).max()
+    assert d == np.float16(amax / np.float32(127))
+    assert abs(q[np.argmax(np.abs(x))]) == 127
+    assert s == np.float16(np.float32(q.sum()) * (amax / np.float32(127)))
+    # |x - q d| <= d/2 for every element (d in fp32)
+    assert np.all(np.abs(x - q * (amax / 127.0)) <= amax / 127.0 / 2 + 1e-6)
+
+
+def test_q8_1_rounds_half_away_and_zero_block():
+    # x * (1/d) lands on .5 for these values: roundf goes away from zero (q8_0 goes to even)
+    x = np.zeros(32, np.float32)
+    x[0] = 127.0
+    x[1], x[2], x[3], x[4] = 2.5, -2.5, 0.5, -1.5
+    q = oracle.q8_1_blocks(x)[0][4:].view(np.int8)
+    assert list(q[:5]) == [127, 3, -3, 1, -2]
+    z = oracle.q8_1_blocks(np.zeros(32, np.float32))[0]
+    assert not z.any()  # d = 0, inverse 0, all codes 0, s = 0
