@@ -312,6 +312,76 @@ uint32_t miikv_prefix_length(const miikv_prefix_ctx* ctx);
 uint64_t miikv_prefix_hash(const miikv_prefix_ctx* ctx);
 void miikv_prefix_set_layout_version(miikv_prefix_ctx* ctx, uint32_t version);
 
+/* ---- persistent session file (.miinfer) ----------------------------------- */
+
+/* On-disk session state, the reference's PersistentSessionHeader
+ * (include/miinfer/prefill_v2/persistent_session.hpp:18-34): packed, 157 bytes,
+ * magic "MISS", version 20260928, followed by prefix_length u32 tokens, the
+ * recurrent state bytes (per GDN layer: state then conv history, in segment
+ * order) and the KV bytes (per attention layer the raw compact form of
+ * src/prefill_v2/kv_cache.cpp:227-297: for each kv head K codes [P][D] then K
+ * scales, then the same for V).  kv_quant_mode MIIKV_SESSION_KV_Q8_0_32 marks
+ * scales per 32-value block ([P][D/32] fp16 per head), 2*P*Hkv*(D + D/16)
+ * bytes per layer; the reference's per-row modes 0..3 are not produced here and
+ * are rejected on load. */
+#define MIIKV_SESSION_VERSION 20260928u
+#define MIIKV_SESSION_KV_Q8_0_32 4u
+#pragma pack(push, 1)
+typedef struct miikv_session_header {
+    char magic[4];
+    uint32_t version;
+    char model_id[64];
+    char quantization[32];
+    uint32_t prefix_length;
+    uint64_t token_hash;
+    uint32_t gdn_layers;
+    uint64_t gdn_state_bytes;
+    uint32_t gqa_layers;
+    uint8_t kv_quant_mode;
+    uint64_t kv_bytes;
+    uint64_t tokens_bytes;
+    uint64_t created_timestamp;
+} miikv_session_header;
+#pragma pack(pop)
+
+/* "sess_<16 hex digits of token_hash>_p<prefix_length>.miinfer" into out
+ * (persistent_session.cpp:27-32).  Returns MIIKV_EINVAL if out_cap is short. */
+miikv_status miikv_session_filename(uint64_t token_hash, uint32_t prefix_length, char* out, size_t out_cap);
+
+/* Save a session (persistent_session.cpp:34-136): the first prefix_length
+ * tokens of sequence `seq` of every attention layer view, and the recurrent
+ * state given as gdn_segment_count device segments (state, conv, state, conv,
+ * ...; gdn_layers = count / 2).  Written to "<path>.tmp" and renamed.  Device
+ * reads are ordered on `stream`; the call returns after the file is written.
+ * Allocates a device staging buffer of one layer's KV bytes for the call. */
+miikv_status miikv_session_save(const char* path, const char* model_id, const char* quantization,
+                                const uint32_t* tokens, uint32_t prefix_length, const miikv_view* kv_layers,
+                                uint32_t kv_layer_count, uint32_t seq, void* const* gdn_segments,
+                                const uint64_t* gdn_segment_bytes, uint32_t gdn_segment_count, void* stream);
+
+/* Read and validate the header (magic, version) and, if tokens_out is not NULL,
+ * up to tokens_cap prefix tokens (persistent_session.cpp:138-161).  Returns 1
+ * on success, 0 otherwise. */
+int miikv_session_inspect(const char* path, miikv_session_header* out, uint32_t* tokens_out, uint32_t tokens_cap);
+
+/* Load a session (persistent_session.cpp:163-258): checks magic, version, model
+ * id, quantization, layer counts, kv_quant_mode, sizes and the token hash, then
+ * writes the KV of every layer (positions 0..P-1 of sequence `seq`) and the
+ * recurrent segments.  *prefix_length_out = P; the tokens go to tokens_out
+ * (tokens_cap >= P).  Returns 1 on success, 0 if the file does not match (no
+ * device memory is written then), or a negative HIP status. */
+int miikv_session_load(const char* path, const char* model_id, const char* quantization,
+                       const miikv_view* kv_layers, uint32_t kv_layer_count, uint32_t seq,
+                       void* const* gdn_segments, const uint64_t* gdn_segment_bytes, uint32_t gdn_segment_count,
+                       uint32_t* tokens_out, uint32_t tokens_cap, uint32_t* prefix_length_out, void* stream);
+
+/* The longest saved prefix of `prompt` among the .miinfer files of session_dir
+ * for this model and quantization (persistent_session.cpp:260-320): returns 1
+ * and fills path_out / *prefix_length_out, or 0 if none matches. */
+int miikv_session_find(const char* session_dir, const char* model_id, const char* quantization,
+                       const uint32_t* prompt, size_t prompt_len, char* path_out, size_t path_cap,
+                       uint32_t* prefix_length_out);
+
 /* ---- measurement probe --------------------------------------------------- */
 
 /* Read `bytes` from src once with 16-byte nontemporal loads over `blocks`

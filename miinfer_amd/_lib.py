@@ -100,6 +100,14 @@ SIGNATURES = {
     "miikv_prefix_length": (_U32, [_P]),
     "miikv_prefix_hash": (_U64, [_P]),
     "miikv_prefix_set_layout_version": (None, [_P, _U32]),
+    "miikv_session_filename": (ctypes.c_int, [_U64, _U32, ctypes.c_char_p, ctypes.c_size_t]),
+    "miikv_session_save": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _P, _U32, _P,
+                                           _U32, _U32, _P, _P, _U32, _P]),
+    "miikv_session_inspect": (ctypes.c_int, [ctypes.c_char_p, _P, _P, _U32]),
+    "miikv_session_load": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _P, _U32, _U32,
+                                           _P, _P, _U32, _P, _U32, _P, _P]),
+    "miikv_session_find": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _P,
+                                           ctypes.c_size_t, ctypes.c_char_p, ctypes.c_size_t, _P]),
     "miikv_suffix_attn": (ctypes.c_int, [_VP, _P, _U32, _U32, ctypes.c_float, _U32, _U32, _U32, _P,
                                           _P, _P, _P, _P, _U64, _P]),
 }

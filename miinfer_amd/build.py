@@ -21,6 +21,7 @@ SOURCES = [
     "miikv_decode.hip",
     "miikv_suffix.hip",
     "miikv_host.cpp",
+    "miikv_session.cpp",
 ]
 
 # Per-source code-generation options.  The suffix kernel keeps its MFMA
