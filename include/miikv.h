@@ -101,6 +101,18 @@ typedef struct __attribute__((aligned(64))) miikv_prefill_state {
     uint32_t pad[12];
 } miikv_prefill_state;
 
+/* Advance a device decode state after one step, on the device so that a
+ * captured decode graph replays without host work: token_output[generated] =
+ * current_token (if token_output != NULL and generated < capacity); stop |=
+ * current_token in stop_tokens (host array, at most 8; the reference's
+ * Qwen3.5 stop tokens are 151643 and 151645) or generated + 1 >=
+ * max_generated; position += 1; generated += 1.
+ * Replaces launch_qwen35_decode_state_advance
+ * (include/miinfer/qwen3_gpu_primitives.hpp:1248; kernel
+ * gfx906/kernels/qwen3_primitives.hip:4417-4429). */
+miikv_status miikv_decode_state_advance(miikv_decode_state* state, uint32_t* token_output, uint32_t capacity,
+                                        const uint32_t* stop_tokens, uint32_t stop_count, void* stream);
+
 /* A generic device-to-device copy segment for miikv_copy_segments. */
 typedef struct miikv_segment {
     void* dst;

@@ -7,6 +7,7 @@ gfx950) and fails loudly when that library is missing.
 from ._lib import MiikvError, lib  # noqa: F401
 from .kv import (  # noqa: F401
     DecodeWorkspace,
+    advance_decode_state,
     KvCache,
     clone_state,
     copy_segments,
@@ -18,6 +19,6 @@ from .kv import (  # noqa: F401
 )
 
 __all__ = [
-    "MiikvError", "lib", "KvCache", "DecodeWorkspace", "decode_attention", "clone_state",
+    "MiikvError", "lib", "advance_decode_state", "KvCache", "DecodeWorkspace", "decode_attention", "clone_state",
     "copy_segments", "make_decode_state", "make_prefill_state", "suffix_attention", "suffix_workspace_bytes",
 ]

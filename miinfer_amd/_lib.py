@@ -78,6 +78,7 @@ SIGNATURES = {
     "miikv_import_canonical": (ctypes.c_int, [_VP, _U32, _U32, _U32, _P, _P, _P, _P, _P]),
     "miikv_copy_pages": (ctypes.c_int, [_VP, _P, _P, _U32, _P]),
     "miikv_copy_segments": (ctypes.c_int, [_P, _U32, _P]),
+    "miikv_decode_state_advance": (ctypes.c_int, [_P, _P, _U32, _P, _U32, _P]),
     "miikv_clone_state": (ctypes.c_int, [_P, _P, _U64, _U32, _P]),
     "miikv_stream_read": (ctypes.c_int, [_P, _U64, _P, _U32, _P]),
     "miikv_suffix_workspace_bytes": (_U64, [_VP, _U32, _U32]),

@@ -185,6 +185,28 @@ __global__ void __launch_bounds__(256) append_kernel(
     }
 }
 
+// Stop tokens of one decode-state advance (passed by value).
+struct StopSet {
+    uint32_t count;
+    uint32_t token[8];
+};
+
+// After a decode step: record the step's token, raise `stop` on a stop token or
+// the generation limit, and move to the next position
+// (qwen35_decode_state_advance_kernel, gfx906/kernels/qwen3_primitives.hip:4417-4429).
+__global__ void decode_state_advance_kernel(miikv_decode_state* st, uint32_t* token_output, uint32_t capacity,
+                                            StopSet stops) {
+    if (blockIdx.x != 0 || threadIdx.x != 0) return;
+    const uint32_t generated = st->generated;
+    const uint32_t tok = st->current_token;
+    if (token_output != nullptr && generated < capacity) token_output[generated] = tok;
+    bool stop = st->stop != 0 || generated + 1 >= st->max_generated;
+    for (uint32_t i = 0; i < stops.count; ++i) stop = stop || tok == stops.token[i];
+    st->stop = stop ? 1u : 0u;
+    st->position += 1;
+    st->generated = generated + 1;
+}
+
 // Tiled -> canonical (export) or canonical -> tiled (import), one thread per
 // (token, kv_head, 16-dim group).
 template <bool EXPORT>
@@ -495,5 +517,17 @@ extern "C" miikv_status miikv_stream_read(const void* src, uint64_t bytes, uint3
         return MIIKV_EINVAL;
     hipLaunchKernelGGL(stream_read_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
                        reinterpret_cast<const uint4*>(src), bytes / 16 / blocks, sink);
+    return launch_status();
+}
+
+extern "C" miikv_status miikv_decode_state_advance(miikv_decode_state* state, uint32_t* token_output,
+                                                   uint32_t capacity, const uint32_t* stop_tokens,
+                                                   uint32_t stop_count, void* stream) {
+    if (state == nullptr || stop_count > 8 || (stop_count > 0 && stop_tokens == nullptr)) return MIIKV_EINVAL;
+    StopSet stops{};
+    stops.count = stop_count;
+    for (uint32_t i = 0; i < stop_count; ++i) stops.token[i] = stop_tokens[i];
+    hipLaunchKernelGGL(decode_state_advance_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), state,
+                       token_output, capacity, stops);
     return launch_status();
 }

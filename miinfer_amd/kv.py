@@ -369,11 +369,22 @@ def suffix_workspace_bytes(cache: KvCache, q_heads: int, tokens: int) -> int:
     return int(lib().miikv_suffix_workspace_bytes(cache.view, q_heads, tokens))
 
 
-def make_decode_state(position: int, device="cuda") -> torch.Tensor:
+def make_decode_state(position: int, device="cuda", max_generated: int = 0x7fffffff) -> torch.Tensor:
     """A 64-byte device DeviceDecodeState with `position` set (current_token 0)."""
     st = torch.zeros(16, dtype=torch.int32, device=device)
     st[1] = position
+    st[4] = max_generated
     return st
+
+
+def advance_decode_state(state: torch.Tensor, token_output: torch.Tensor | None = None,
+                         stop_tokens=(), stream=None) -> None:
+    """Device-side step of a decode state (record token, stop flag, position += 1)."""
+    import numpy as np
+    st = np.ascontiguousarray(list(stop_tokens), np.uint32)
+    cap = 0 if token_output is None else token_output.numel()
+    call("miikv_decode_state_advance", _ptr(state), _ptr(token_output), cap,
+         st.ctypes.data_as(ctypes.c_void_p) if st.size else None, st.size, _stream(stream))
 
 
 def make_prefill_state(base_position: int, token_count: int, kv_capacity: int = 0,

@@ -168,3 +168,13 @@ def test_fused_append_and_q8_1_decode_reject_before_launch():
     # Q8_1 output without a gate
     assert lib.miikv_decode_attn_q8_1(ctypes.byref(v), p, L.DTYPE_F16, 24, 0.0625, 1, lens, None, 256, p, None,
                                       None, p, p, 1 << 20, None) == L.MIIKV_EINVAL
+
+
+def test_decode_state_advance_rejects_before_launch():
+    L = _lib()
+    lib = L.lib()
+    p = ctypes.c_void_p(0x3000)
+    stops = (ctypes.c_uint32 * 9)(*range(9))
+    assert lib.miikv_decode_state_advance(None, None, 0, None, 0, None) == L.MIIKV_EINVAL
+    assert lib.miikv_decode_state_advance(p, None, 0, stops, 9, None) == L.MIIKV_EINVAL
+    assert lib.miikv_decode_state_advance(p, None, 0, None, 2, None) == L.MIIKV_EINVAL
