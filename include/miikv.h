@@ -212,6 +212,20 @@ miikv_status miikv_decode_attn_q8_1(const miikv_view* view, const void* q, uint3
                                     const float* gate, float* gated_out, void* gated_q8_1, void* workspace,
                                     uint64_t workspace_bytes, void* stream);
 
+/* Fused append + decode: stores the new fp16 K/V row of each sequence
+ * (k_new, v_new device [batch][kv_heads][head_dim]) at position L-1 of that
+ * sequence, where L is the context length including it (d_lengths[b] or
+ * decode_state->position + 1), with the append rule, and attends over all L
+ * keys — one launch pair instead of the reference's store kernel followed by
+ * attention (attention_layer.cpp:599-632).  Cache bytes and results equal
+ * miikv_append_f16 followed by miikv_decode_attn_q8_1. */
+miikv_status miikv_decode_append_attn(const miikv_view* view, const uint16_t* k_new, const uint16_t* v_new,
+                                      const void* q, uint32_t q_dtype, uint32_t q_heads, float scale,
+                                      uint32_t batch, const uint32_t* d_lengths,
+                                      const miikv_decode_state* decode_state, uint32_t max_context, float* out,
+                                      const float* gate, float* gated_out, void* gated_q8_1, void* workspace,
+                                      uint64_t workspace_bytes, void* stream);
+
 /* ---- suffix (multi-token) attention over a cached prefix ----------------- */
 
 /* Causal attention of a token_count-token suffix whose rows already sit in the

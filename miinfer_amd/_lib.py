@@ -74,6 +74,8 @@ SIGNATURES = {
                                           _P, _P, _P, _P, _U64, _P]),
     "miikv_decode_attn_q8_1": (ctypes.c_int, [_VP, _P, _U32, _U32, ctypes.c_float, _U32, _P, _P, _U32,
                                                _P, _P, _P, _P, _P, _U64, _P]),
+    "miikv_decode_append_attn": (ctypes.c_int, [_VP, _P, _P, _P, _U32, _U32, ctypes.c_float, _U32, _P, _P,
+                                                 _U32, _P, _P, _P, _P, _P, _U64, _P]),
     "miikv_export_canonical": (ctypes.c_int, [_VP, _U32, _U32, _U32, _P, _P, _P, _P, _P]),
     "miikv_import_canonical": (ctypes.c_int, [_VP, _U32, _U32, _U32, _P, _P, _P, _P, _P]),
     "miikv_copy_pages": (ctypes.c_int, [_VP, _P, _P, _U32, _P]),

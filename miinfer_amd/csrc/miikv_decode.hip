@@ -91,7 +91,7 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 #endif
 
 
-template <uint32_t D, bool QF32>
+template <uint32_t D, bool QF32, bool APPEND>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? MIIKV_WPE_D128 : MIIKV_WPE_D256)))
 decode_kernel(SplitArgs a) {
     constexpr uint32_t NB = D / 32;   // q8_0 blocks per row
@@ -221,7 +221,11 @@ decode_kernel(SplitArgs a) {
     for (uint32_t blk = 0; blk < (kVBias ? NB : 1); ++blk) vbias[blk] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
     const half4 ones = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
 
-    const uint32_t nsteps = (L + kChunk - 1) / kChunk;
+    // With the fused append the splits cover the L-1 cached keys; the new token
+    // (position L-1, whose cache slot may still hold older bytes: masked) is stored
+    // and merged by the combine kernel.
+    const uint32_t Lc = APPEND ? L - 1 : L;
+    const uint32_t nsteps = (Lc + kChunk - 1) / kChunk;
 #ifdef MIIKV_EXP_NO_LOOP
     const uint32_t c_end = c_begin;
 #else
@@ -234,7 +238,7 @@ decode_kernel(SplitArgs a) {
     // A step that reaches past L (only the sequence's last) is masked under a
     // wave-uniform branch: its scores go to -inf and its V scales to 0 (the memory
     // past L may hold anything, including non-finite scales).
-    auto compute_step = [&](uint32_t c, const Step& st) {
+    auto compute_step = [&](uint32_t c, const Step& st) __attribute__((always_inline)) {
         const uint32_t tok0 = c * kChunk;
 #ifdef MIIKV_EXP_NO_COMPUTE
         {
@@ -250,10 +254,10 @@ decode_kernel(SplitArgs a) {
             return;
         }
 #endif
-        const bool tail = tok0 + kChunk > L;
+        const bool tail = tok0 + kChunk > Lc;
         *reinterpret_cast<ScaleVec*>(s_sc + lane * (NB / 2)) = st.ks;
         ScaleVec vsv = st.vs;
-        if (tail && tok0 + lane / 2 >= L) vsv = ScaleVec{};
+        if (tail && tok0 + lane / 2 >= Lc) vsv = ScaleVec{};
         *reinterpret_cast<ScaleVec*>(s_sc + kChunk * NB + lane * (NB / 2)) = vsv;
 
         // ---- scores S^T[token][head], one MFMA per q8_0 block, block scale in fp32
@@ -301,7 +305,7 @@ decode_kernel(SplitArgs a) {
             for (uint32_t J = 0; J < 2; ++J)
 #pragma unroll
                 for (uint32_t i = 0; i < 4; ++i)
-                    if (tok0 + 16 * J + 4 * g4 + i >= L) s[J][i] = -INFINITY;
+                    if (tok0 + 16 * J + 4 * g4 + i >= Lc) s[J][i] = -INFINITY;
         }
 
         // ---- online softmax with a lazy running max: the accumulators are rescaled only
@@ -496,12 +500,11 @@ extern "C" miikv_status miikv_workspace_init(void* workspace, uint64_t bytes, vo
     return hip_status(hipGetLastError());
 }
 
-extern "C" miikv_status miikv_decode_attn_q8_1(const miikv_view* view, const void* q, uint32_t q_dtype,
-                                               uint32_t q_heads, float scale, uint32_t batch,
-                                               const uint32_t* d_lengths, const miikv_decode_state* decode_state,
-                                               uint32_t max_context, float* out, const float* gate,
-                                               float* gated_out, void* gated_q8_1, void* workspace,
-                                               uint64_t workspace_bytes, void* stream) {
+static miikv_status decode_impl(const miikv_view* view, const uint16_t* k_new, const uint16_t* v_new,
+                                const void* q, uint32_t q_dtype, uint32_t q_heads, float scale, uint32_t batch,
+                                const uint32_t* d_lengths, const miikv_decode_state* decode_state,
+                                uint32_t max_context, float* out, const float* gate, float* gated_out,
+                                void* gated_q8_1, void* workspace, uint64_t workspace_bytes, void* stream) {
     const int st = validate_view(view);
     if (st != MIIKV_OK) return st;
     if (q == nullptr || batch == 0 || q_heads == 0 || q_heads % view->kv_heads != 0 || !std::isfinite(scale))
@@ -546,6 +549,9 @@ extern "C" miikv_status miikv_decode_attn_q8_1(const miikv_view* view, const voi
     a.gate = gate;
     a.gated_out = gated_out;
     a.gated_q8_1 = static_cast<uint8_t*>(gated_q8_1);
+    a.k_new = k_new;
+    a.v_new = v_new;
+    a.q_f32 = q_dtype == MIIKV_DTYPE_F32;
 
     const size_t lds = (32 * kWavesPerWg + kWavesPerWg * G * view->head_dim) * sizeof(float) +
                        kWavesPerWg * 2 * kChunk * (view->head_dim / 32) * sizeof(uint16_t);
@@ -554,16 +560,35 @@ extern "C" miikv_status miikv_decode_attn_q8_1(const miikv_view* view, const voi
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool f32 = q_dtype == MIIKV_DTYPE_F32;
     const dim3 cgrid(batch * view->kv_heads, (G * view->head_dim + 63) / 64);
+    const bool app = k_new != nullptr;
     if (view->head_dim == 128) {
-        if (f32) hipLaunchKernelGGL((decode_kernel<128, true>), grid, dim3(64 * kWavesPerWg), lds, s, a);
-        else hipLaunchKernelGGL((decode_kernel<128, false>), grid, dim3(64 * kWavesPerWg), lds, s, a);
-        hipLaunchKernelGGL((combine_kernel<128>), cgrid, dim3(256), 0, s, a);
+        if (app) {
+            if (f32) hipLaunchKernelGGL((decode_kernel<128, true, true>), grid, dim3(64 * kWavesPerWg), lds, s, a);
+            else hipLaunchKernelGGL((decode_kernel<128, false, true>), grid, dim3(64 * kWavesPerWg), lds, s, a);
+        } else if (f32) hipLaunchKernelGGL((decode_kernel<128, true, false>), grid, dim3(64 * kWavesPerWg), lds, s, a);
+        else hipLaunchKernelGGL((decode_kernel<128, false, false>), grid, dim3(64 * kWavesPerWg), lds, s, a);
+        if (app) hipLaunchKernelGGL((combine_kernel<128, true>), cgrid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((combine_kernel<128, false>), cgrid, dim3(256), 0, s, a);
     } else {
-        if (f32) hipLaunchKernelGGL((decode_kernel<256, true>), grid, dim3(64 * kWavesPerWg), lds, s, a);
-        else hipLaunchKernelGGL((decode_kernel<256, false>), grid, dim3(64 * kWavesPerWg), lds, s, a);
-        hipLaunchKernelGGL((combine_kernel<256>), cgrid, dim3(256), 0, s, a);
+        if (app) {
+            if (f32) hipLaunchKernelGGL((decode_kernel<256, true, true>), grid, dim3(64 * kWavesPerWg), lds, s, a);
+            else hipLaunchKernelGGL((decode_kernel<256, false, true>), grid, dim3(64 * kWavesPerWg), lds, s, a);
+        } else if (f32) hipLaunchKernelGGL((decode_kernel<256, true, false>), grid, dim3(64 * kWavesPerWg), lds, s, a);
+        else hipLaunchKernelGGL((decode_kernel<256, false, false>), grid, dim3(64 * kWavesPerWg), lds, s, a);
+        if (app) hipLaunchKernelGGL((combine_kernel<256, true>), cgrid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((combine_kernel<256, false>), cgrid, dim3(256), 0, s, a);
     }
     return hip_status(hipGetLastError());
+}
+
+extern "C" miikv_status miikv_decode_attn_q8_1(const miikv_view* view, const void* q, uint32_t q_dtype,
+                                               uint32_t q_heads, float scale, uint32_t batch,
+                                               const uint32_t* d_lengths, const miikv_decode_state* decode_state,
+                                               uint32_t max_context, float* out, const float* gate,
+                                               float* gated_out, void* gated_q8_1, void* workspace,
+                                               uint64_t workspace_bytes, void* stream) {
+    return decode_impl(view, nullptr, nullptr, q, q_dtype, q_heads, scale, batch, d_lengths, decode_state, max_context,
+                       out, gate, gated_out, gated_q8_1, workspace, workspace_bytes, stream);
 }
 
 extern "C" miikv_status miikv_decode_attn(const miikv_view* view, const void* q, uint32_t q_dtype, uint32_t q_heads,
@@ -571,6 +596,18 @@ extern "C" miikv_status miikv_decode_attn(const miikv_view* view, const void* q,
                                           const miikv_decode_state* decode_state, uint32_t max_context, float* out,
                                           const float* gate, float* gated_out, void* workspace,
                                           uint64_t workspace_bytes, void* stream) {
-    return miikv_decode_attn_q8_1(view, q, q_dtype, q_heads, scale, batch, d_lengths, decode_state, max_context, out,
-                                  gate, gated_out, nullptr, workspace, workspace_bytes, stream);
+    return decode_impl(view, nullptr, nullptr, q, q_dtype, q_heads, scale, batch, d_lengths, decode_state, max_context,
+                       out, gate, gated_out, nullptr, workspace, workspace_bytes, stream);
+}
+
+extern "C" miikv_status miikv_decode_append_attn(const miikv_view* view, const uint16_t* k_new,
+                                                 const uint16_t* v_new, const void* q, uint32_t q_dtype,
+                                                 uint32_t q_heads, float scale, uint32_t batch,
+                                                 const uint32_t* d_lengths, const miikv_decode_state* decode_state,
+                                                 uint32_t max_context, float* out, const float* gate,
+                                                 float* gated_out, void* gated_q8_1, void* workspace,
+                                                 uint64_t workspace_bytes, void* stream) {
+    if (k_new == nullptr || v_new == nullptr) return MIIKV_EINVAL;
+    return decode_impl(view, k_new, v_new, q, q_dtype, q_heads, scale, batch, d_lengths, decode_state, max_context,
+                       out, gate, gated_out, gated_q8_1, workspace, workspace_bytes, stream);
 }

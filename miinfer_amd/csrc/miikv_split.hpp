@@ -32,6 +32,9 @@ struct SplitArgs {
     const float* gate;
     float* gated_out;
     uint8_t* gated_q8_1;  // nullable: Q8_1 blocks [batch][q_heads][D/32] of gated_out
+    const uint16_t* k_new;  // fused append: fp16 rows [batch][kv_heads][D] stored at position L-1
+    const uint16_t* v_new;
+    uint32_t q_f32;         // q dtype (the combine scores the appended token)
 };
 
 __device__ __forceinline__ float exp2_safe(float x) { return exp2f(x); }  // exp2(-inf) == 0
@@ -51,7 +54,12 @@ __device__ __forceinline__ uint32_t split_length(const SplitArgs& a, uint32_t b)
 // (e4 = tid & 15, sg = tid >> 4) folds splits sg, sg+16, ... for 4 consecutive
 // elements with its own running max, so its loads are independent; the 16 split
 // groups are merged in a fixed order through LDS (deterministic result).
-template <uint32_t D>
+// Fused append (APPEND): the splits covered the L-1 cached keys; this kernel
+// quantises the new row of (b, h) with the append rule (thread t < D owns dim t;
+// block absmax over 32 lanes), stores it at position L-1 (workgroup y == 0),
+// scores it against the query head of this workgroup's elements, and merges it
+// as one more record (m = score, l = 1, O = dequantised V row).
+template <uint32_t D, bool APPEND>
 __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
     const uint32_t bh = blockIdx.x;
     const uint32_t b = bh / a.g.kv_heads;
@@ -60,6 +68,18 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
     const uint32_t GD = G * D;
     const uint32_t e0 = blockIdx.y * 64;
     if (e0 >= GD) return;
+    // fused append: the new rows (dim tid), issued before the records
+    float kx = 0.0f, vx = 0.0f, qx = 0.0f;
+    const uint32_t hq0 = e0 / D;  // query head (within the group) of this workgroup's elements
+    if constexpr (APPEND) {
+        if (threadIdx.x < D) {
+            const size_t row = (static_cast<size_t>(b) * a.g.kv_heads + h) * D + threadIdx.x;
+            kx = f16_bits_to_f32(a.k_new[row]);
+            vx = f16_bits_to_f32(a.v_new[row]);
+            const size_t qi = (static_cast<size_t>(b) * a.q_heads + static_cast<size_t>(h) * G + hq0) * D + threadIdx.x;
+            qx = a.q_f32 ? static_cast<const float*>(a.q)[qi] : f16_bits_to_f32(static_cast<const uint16_t*>(a.q)[qi]);
+        }
+    }
     const uint32_t tid = threadIdx.x;
     const uint32_t e4 = tid & 15;
     const uint32_t sg = tid >> 4;
@@ -98,6 +118,7 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
     float lsum = 0.0f;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     auto merge = [&](float m_s, float l_s, float4 v) {
+        if (m_s == -INFINITY) return;  // a split with no key (possible with the fused append)
         const float mn = fmaxf(mloc, m_s);
         const float fo = exp2_safe(mloc - mn);  // 0 on the first split
         const float fs = exp2_safe(m_s - mn);
@@ -119,10 +140,50 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
     __shared__ float4 s_acc[16][16];
     __shared__ float s_gm[16][16];
     __shared__ float s_gl[16][16];
+    __shared__ float s_vnew[APPEND ? D : 1];
+    __shared__ float s_dot[4];
     s_acc[sg][e4] = acc;
     s_gm[sg][e4] = mloc;
     s_gl[sg][e4] = lsum;
-    __syncthreads();
+    float m_new = -INFINITY;
+    if constexpr (APPEND) {
+        // Same rule as the append kernel: scale = amax/127 (1 for a zero block),
+        // codes round-to-nearest-even, clamped; the score uses code * fp16(scale).
+        const uint32_t t = threadIdx.x;
+        float ka = fabsf(kx), va = fabsf(vx);
+#pragma unroll
+        for (uint32_t off = 1; off < 32; off <<= 1) {
+            ka = fmaxf(ka, __shfl_xor(ka, off, 64));
+            va = fmaxf(va, __shfl_xor(va, off, 64));
+        }
+        const float ksc = ka > 0.0f ? ka / 127.0f : 1.0f, vsc = va > 0.0f ? va / 127.0f : 1.0f;
+        const int kq = max(-128, min(127, __float2int_rn(kx * (1.0f / ksc))));
+        const int vq = max(-128, min(127, __float2int_rn(vx * (1.0f / vsc))));
+        const uint16_t kbits = f32_to_f16_bits(ksc), vbits = f32_to_f16_bits(vsc);
+        float part = t < D ? qx * (static_cast<float>(kq) * f16_bits_to_f32(kbits)) : 0.0f;
+#pragma unroll
+        for (uint32_t off = 1; off < 64; off <<= 1) part += __shfl_xor(part, off, 64);
+        if ((t & 63) == 0) s_dot[t >> 6] = part;
+        if (t < D) s_vnew[t] = static_cast<float>(vq) * f16_bits_to_f32(vbits);
+        const uint32_t L = split_length(a, b);
+        if (blockIdx.y == 0 && t < D && L > 0) {
+            const uint32_t pos = L - 1;
+            const size_t slab = slab_of(a.g, b, pos, h);
+            const uint32_t tp = pos % a.g.page_tokens;
+            const size_t slab_bytes = static_cast<size_t>(a.g.page_tokens) * D;
+            a.g.k_codes[slab * slab_bytes + k_code_offset(tp, t & ~7u, D) + (t & 7u)] = static_cast<int8_t>(kq);
+            a.g.v_codes[slab * slab_bytes + v_code_offset(tp, t, D)] = static_cast<int8_t>(vq);
+            if ((t & 31) == 0) {
+                const size_t sidx = (slab * a.g.page_tokens + tp) * (D / 32) + t / 32;
+                a.g.k_scales[sidx] = kbits;
+                a.g.v_scales[sidx] = vbits;
+            }
+        }
+        __syncthreads();
+        if (L > 0) m_new = (s_dot[0] + s_dot[1] + s_dot[2] + s_dot[3]) * a.scale_log2;
+    } else {
+        __syncthreads();
+    }
     if (sg != 0 || !active) return;
     float M = -INFINITY;
 #pragma unroll
@@ -140,6 +201,19 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
         o.z += f * v.z;
         o.w += f * v.w;
         Ls += f * s_gl[g][e4];
+    }
+    if constexpr (APPEND) {
+        if (m_new != -INFINITY) {
+            const float Mn = fmaxf(M, m_new);
+            const float fo = M == -INFINITY ? 0.0f : exp2_safe(M - Mn);
+            const float fn = exp2_safe(m_new - Mn);
+            const uint32_t d = e % D;
+            o.x = o.x * fo + s_vnew[d] * fn;
+            o.y = o.y * fo + s_vnew[d + 1] * fn;
+            o.z = o.z * fo + s_vnew[d + 2] * fn;
+            o.w = o.w * fo + s_vnew[d + 3] * fn;
+            Ls = Ls * fo + fn;
+        }
     }
     // out = acc / L, 0 when L == 0 (qwen3_primitives.hip:2349); gated = out * sigmoid(gate).
     const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;

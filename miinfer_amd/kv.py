@@ -273,14 +273,17 @@ def decode_attention(cache: KvCache, q: torch.Tensor, scale: float | None = None
                      lengths: torch.Tensor | None = None, decode_state: torch.Tensor | None = None,
                      max_context: int | None = None, gate: torch.Tensor | None = None,
                      out: torch.Tensor | None = None, gated_out: torch.Tensor | None = None,
-                     gated_q8_1: torch.Tensor | None = None,
+                     gated_q8_1: torch.Tensor | None = None, k_new: torch.Tensor | None = None,
+                     v_new: torch.Tensor | None = None,
                      workspace: DecodeWorkspace | None = None, stream=None):
     """Single-token GQA attention over the q8_0 cache.
 
     q: [batch, q_heads, head_dim] fp16 or fp32.  Context lengths come from
     `lengths` (device [batch]) or `decode_state` (position + 1).  With `gate`,
     `gated_q8_1` (uint8 [batch * q_heads * head_dim / 32, 36]) receives the gated
-    output as Q8_1 blocks.  Returns (out, gated_out)."""
+    output as Q8_1 blocks.  With k_new / v_new (fp16 [batch, kv_heads, head_dim]) the
+    new token's row is stored at position L-1 in the same launch (fused append).
+    Returns (out, gated_out)."""
     batch, q_heads, d = q.shape
     if d != cache.head_dim or not q.is_contiguous() or q.dtype not in (torch.float16,
                                                                         torch.float32):
@@ -316,6 +319,17 @@ def decode_attention(cache: KvCache, q: torch.Tensor, scale: float | None = None
                 gated_q8_1.numel() < batch * q_heads * (d // QBLOCK) * 36:
             raise ValueError("gated_q8_1 must be contiguous uint8 [batch*q_heads*D/32, 36]")
     qd = _lib.DTYPE_F16 if q.dtype == torch.float16 else _lib.DTYPE_F32
+    if (k_new is None) != (v_new is None):
+        raise ValueError("k_new and v_new go together")
+    if k_new is not None:
+        for t in (k_new, v_new):
+            if t.dtype != torch.float16 or tuple(t.shape) != (batch, cache.kv_heads, d) or \
+                    not t.is_contiguous():
+                raise ValueError("k_new/v_new must be contiguous fp16 [batch, kv_heads, head_dim]")
+        call("miikv_decode_append_attn", cache.view, _ptr(k_new), _ptr(v_new), _ptr(q), qd, q_heads,
+             float(scale), batch, _ptr(lengths), _ptr(decode_state), max_context, _ptr(out), _ptr(gate),
+             _ptr(gated_out), _ptr(gated_q8_1), _ptr(workspace.buf), workspace.bytes, _stream(stream))
+        return out, gated_out
     call("miikv_decode_attn_q8_1", cache.view, _ptr(q), qd, q_heads, float(scale), batch,
          _ptr(lengths), _ptr(decode_state), max_context, _ptr(out), _ptr(gate), _ptr(gated_out),
          _ptr(gated_q8_1), _ptr(workspace.buf), workspace.bytes, _stream(stream))

@@ -1,0 +1,118 @@
+"""Fused append + decode (one launch pair): the new row lands in the cache with
+the same bytes as miikv_append_f16, and attention covers it (oracle
+tolerance, tests/helpers.py)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.helpers import assert_attention_close, randn_f16
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a, gpu):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+
+
+def _canon(cache, seq, n):
+    out = cache.export_canonical(seq, 0, n)
+    torch.cuda.synchronize()
+    return [t.cpu().numpy() for t in out]
+
+
+@pytest.mark.parametrize("hq,hk,d", [(32, 8, 128), (24, 4, 256)])
+@pytest.mark.parametrize("length", [1, 2, 32, 33, 64, 65, 127, 128, 129, 1000, 4097])
+def test_fused_append_decode_contiguous(gpu, hq, hk, d, length):
+    import miinfer_amd as m
+    rng = np.random.default_rng(length * 7 + d)
+    cap = ((length + 127) // 128) * 128
+    fused = m.KvCache.contiguous(hk, d, cap)
+    plain = m.KvCache.contiguous(hk, d, cap)
+    k = randn_f16(rng, (length, hk, d))
+    v = randn_f16(rng, (length, hk, d))
+    k.reshape(-1, 32)[-1] = 0.0  # a zero block in the new row
+    # the slot of the new token holds older bytes (a previous sequence) in `fused`
+    junk = randn_f16(rng, (length, hk, d)) * np.float16(50)
+    fused.append(_dev(junk, gpu), _dev(junk, gpu))
+    if length > 1:
+        fused.append(_dev(k[:-1], gpu), _dev(v[:-1], gpu))
+    plain.append(_dev(k, gpu), _dev(v, gpu))
+    q = randn_f16(rng, (1, hq, d))
+    gate = rng.standard_normal((1, hq, d)).astype(np.float32)
+    lengths = torch.tensor([length], dtype=torch.int32, device=gpu)
+    out, gated = m.decode_attention(fused, _dev(q, gpu), lengths=lengths, max_context=cap,
+                                    gate=_dev(gate, gpu), out=torch.empty((1, hq, d), device=gpu),
+                                    k_new=_dev(k[-1:], gpu), v_new=_dev(v[-1:], gpu))
+    torch.cuda.synchronize()
+    for a, b in zip(_canon(fused, 0, length), _canon(plain, 0, length)):
+        assert np.array_equal(a, b)
+    kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+    vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+    expect = oracle.attention_q8(q[0].astype(np.float32), kc, ks, vc, vs, length, hq, 1 / math.sqrt(d))
+    assert_attention_close(out.cpu().numpy()[0], expect, f"L={length}")
+    assert_attention_close(gated.cpu().numpy()[0], expect / (1 + np.exp(-gate[0])), "gated")
+
+
+def test_fused_append_decode_state_and_fp32_query(gpu):
+    import miinfer_amd as m
+    rng = np.random.default_rng(3)
+    hq, hk, d, length = 32, 8, 128, 777
+    cache = m.KvCache.contiguous(hk, d, 1024)
+    k = randn_f16(rng, (length, hk, d))
+    v = randn_f16(rng, (length, hk, d))
+    cache.append(_dev(k[:-1], gpu), _dev(v[:-1], gpu))
+    q = rng.standard_normal((1, hq, d)).astype(np.float32)
+    ds = m.make_decode_state(length - 1, device=gpu)
+    out, _ = m.decode_attention(cache, _dev(q, gpu), decode_state=ds, max_context=1024,
+                                k_new=_dev(k[-1:], gpu), v_new=_dev(v[-1:], gpu))
+    torch.cuda.synchronize()
+    kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+    vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+    expect = oracle.attention_q8(q[0], kc, ks, vc, vs, length, hq, 1 / math.sqrt(d))
+    assert_attention_close(out.cpu().numpy()[0], expect, "fp32 q, decode state")
+
+
+@pytest.mark.parametrize("hq,hk,d", [(24, 4, 256), (32, 8, 128)])
+def test_fused_append_decode_paged_batched(gpu, hq, hk, d):
+    import miinfer_amd as m
+    rng = np.random.default_rng(hq * d)
+    pt = 256
+    lens = [1, 256, 257, 512, 3000, 1100]   # lengths include the new token
+    pages = [(n + pt - 1) // pt for n in lens]
+    stride = max(pages)
+    total = sum(pages)
+    perm = rng.permutation(total).astype(np.int32)
+    table = np.zeros((len(lens), stride), np.int32)
+    o = 0
+    for s, p in enumerate(pages):
+        table[s, :p] = perm[o:o + p]
+        o += p
+    cache = m.KvCache.paged_cache(hk, d, total, _dev(table, gpu), page_tokens=pt)
+    refs, knew, vnew = [], [], []
+    for s, n in enumerate(lens):
+        k = randn_f16(rng, (n, hk, d))
+        v = randn_f16(rng, (n, hk, d))
+        if n > 1:
+            cache.append(_dev(k[:-1], gpu), _dev(v[:-1], gpu), base_position=0, seq=s)
+        knew.append(k[-1])
+        vnew.append(v[-1])
+        kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+        vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+        refs.append((kc, ks, vc, vs))
+    q = randn_f16(rng, (len(lens), hq, d))
+    out, _ = m.decode_attention(cache, _dev(q, gpu), lengths=_dev(np.array(lens, np.int32), gpu),
+                                max_context=stride * pt, k_new=_dev(np.stack(knew), gpu),
+                                v_new=_dev(np.stack(vnew), gpu))
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    for s, n in enumerate(lens):
+        expect = oracle.attention_q8(q[s].astype(np.float32), *refs[s], n, hq, 1 / math.sqrt(d))
+        assert_attention_close(out[s], expect, f"seq {s} L={n}")
+        kc, ks, vc, vs = _canon(cache, s, n)
+        assert np.array_equal(kc[:, n - 1], refs[s][0][:, n - 1])
+        assert np.array_equal(ks[:, n - 1].view(np.uint16), refs[s][1][:, n - 1])
+        assert np.array_equal(vc[:, n - 1], refs[s][2][:, n - 1])
+        assert np.array_equal(vs[:, n - 1].view(np.uint16), refs[s][3][:, n - 1])
