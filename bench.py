@@ -263,10 +263,7 @@ def bench_c5(dev, args) -> int:
         t0 = time.perf_counter()
         copies = []
         for li in range(layers_attn):
-            cl = []
-            for _ in range(forks):
-                _, cp = pools[li].fork(tables[li], prefix, pt)
-                cl += cp
+            _, cl = pools[li].fork_many(tables[li], prefix, pt, forks)
             copies.append(cl)
         host_s = time.perf_counter() - t0
         src = [torch.tensor([c[0] for c in cl], dtype=torch.int32, device=dev) for cl in copies]

@@ -92,6 +92,7 @@ SIGNATURES = {
     "miikv_pool_refcount": (_U32, [_P, ctypes.c_int32]),
     "miikv_pool_free_pages": (_U32, [_P]),
     "miikv_pool_fork": (ctypes.c_int, [_P, _P, _U32, _U32, _P, _P, _P, _P]),
+    "miikv_pool_fork_n": (ctypes.c_int, [_P, _P, _U32, _U32, _U32, _P, _U32, _P, _P, _P, _P]),
     "miikv_pool_prepare_append": (ctypes.c_int, [_P, _P, _U32, _U32, _U32, _P, _P, _P]),
     "miikv_pool_release": (ctypes.c_int, [_P, _P, _U32, _U32]),
     "miikv_token_hash": (_U64, [_P, ctypes.c_size_t]),

@@ -100,6 +100,31 @@ extern "C" miikv_status miikv_pool_fork(miikv_pool* p, const int32_t* parent_row
     return MIIKV_OK;
 }
 
+// n forks of one parent in one call: child i's row goes to child_rows + i*row_stride;
+// copy_src/copy_dst (capacity n) receive the copy-on-write page pairs, *n_copies
+// their count.  On pool exhaustion the forks made so far stay (each is complete)
+// and MIIKV_EINVAL is returned with *n_done set.
+extern "C" miikv_status miikv_pool_fork_n(miikv_pool* p, const int32_t* parent_row, uint32_t length,
+                                          uint32_t page_tokens, uint32_t n, int32_t* child_rows, uint32_t row_stride,
+                                          int32_t* copy_src, int32_t* copy_dst, uint32_t* n_copies,
+                                          uint32_t* n_done) {
+    if (p == nullptr || n_copies == nullptr || n_done == nullptr || page_tokens == 0 ||
+        (n > 0 && child_rows == nullptr) || row_stride < pages_for(length, page_tokens))
+        return MIIKV_EINVAL;
+    *n_copies = 0;
+    *n_done = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        uint32_t c = 0;
+        const miikv_status st =
+            miikv_pool_fork(p, parent_row, length, page_tokens, child_rows + static_cast<size_t>(i) * row_stride,
+                            copy_src ? copy_src + *n_copies : nullptr, copy_dst ? copy_dst + *n_copies : nullptr, &c);
+        if (st != MIIKV_OK) return st;
+        *n_copies += c;
+        *n_done = i + 1;
+    }
+    return MIIKV_OK;
+}
+
 extern "C" miikv_status miikv_pool_prepare_append(miikv_pool* p, int32_t* row, uint32_t row_capacity,
                                                   uint32_t position, uint32_t page_tokens, int32_t* copy_src,
                                                   int32_t* copy_dst, uint32_t* n_copies) {

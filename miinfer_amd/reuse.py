@@ -69,6 +69,22 @@ class PagePool:
              _i32p(src), _i32p(dst), ctypes.byref(n))
         return child, [(int(src[0]), int(dst[0]))] if n.value else []
 
+    def fork_many(self, parent_row: np.ndarray, length: int, page_tokens: int, n: int):
+        """n children of one parent in one call: (child_rows [n, len(parent_row)],
+        [(src, dst)] copy-on-write page pairs)."""
+        parent_row = np.ascontiguousarray(parent_row, np.int32)
+        rows = np.full((n, parent_row.size), -1, np.int32)
+        src = np.zeros(max(n, 1), np.int32)
+        dst = np.zeros(max(n, 1), np.int32)
+        nc = ctypes.c_uint32(0)
+        done = ctypes.c_uint32(0)
+        r = lib().miikv_pool_fork_n(self._h, _i32p(parent_row), length, page_tokens, n, _i32p(rows),
+                                    parent_row.size, _i32p(src), _i32p(dst), ctypes.byref(nc),
+                                    ctypes.byref(done))
+        if r != 0:
+            raise MemoryError(f"page pool exhausted after {done.value} of {n} forks")
+        return rows, list(zip(src[:nc.value].tolist(), dst[:nc.value].tolist()))
+
     def prepare_append(self, row: np.ndarray, position: int, page_tokens: int):
         """Make the page receiving `position` writable (new page or copy-on-write);
         updates `row` in place and returns the [(src, dst)] page copies to run."""

@@ -132,3 +132,19 @@ def test_pool_exhaustion_and_bad_pages():
         pool.release(np.array([7], np.int32), 10, 256)
     pool.release(np.array([a, b], np.int32), 300, 256)
     assert pool.free_pages == 2
+
+
+def test_fork_many_matches_repeated_fork():
+    """One batched call plans the same rows, reference counts and copies as n single forks."""
+    from miinfer_amd.reuse import PagePool
+    pt, length, n = 256, 256 * 3 + 10, 5
+    a, b = PagePool(40), PagePool(40)
+    ra = np.array([a.alloc() for _ in range(4)], np.int32)
+    rb = np.array([b.alloc() for _ in range(4)], np.int32)
+    rows, copies = a.fork_many(ra, length, pt, n)
+    single = [b.fork(rb, length, pt) for _ in range(n)]
+    assert np.array_equal(rows, np.stack([r for r, _ in single]))
+    assert copies == [c for _, cs in single for c in cs]
+    assert [a.refcount(p) for p in range(40)] == [b.refcount(p) for p in range(40)]
+    with pytest.raises(MemoryError):
+        PagePool(5).fork_many(np.array([0, 1, 2, 3], np.int32), length, pt, 3)
