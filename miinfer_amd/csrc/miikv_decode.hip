@@ -43,20 +43,31 @@ namespace {
 
 // Pipeline depth (32-token steps held in registers) and the occupancy it is tuned for.
 #ifndef MIIKV_RING_D128
-#define MIIKV_RING_D128 3
+#define MIIKV_RING_D128 1
 #endif
 #ifndef MIIKV_WPE_D128
-#define MIIKV_WPE_D128 2
+#define MIIKV_WPE_D128 3
 #endif
 #ifndef MIIKV_RING_D256
-#define MIIKV_RING_D256 2
+#define MIIKV_RING_D256 1
 #endif
 #ifndef MIIKV_WPE_D256
-#define MIIKV_WPE_D256 1
+#define MIIKV_WPE_D256 2
 #endif
 #ifndef MIIKV_VBIAS_D256
-#define MIIKV_VBIAS_D256 1
+#define MIIKV_VBIAS_D256 0
 #endif
+#ifndef MIIKV_VBIAS_D128
+#define MIIKV_VBIAS_D128 1
+#endif
+// An fp32 query carries a second (low-half) set of query fragments and a second
+// MFMA per block; those variants keep a deeper ring at lower occupancy.
+template <uint32_t D, bool QF32>
+struct DecodeTuning {
+    static constexpr uint32_t ring = D == 128 ? MIIKV_RING_D128 : (QF32 ? 2 : MIIKV_RING_D256);
+    static constexpr uint32_t waves_per_eu = D == 128 ? (QF32 ? 2 : MIIKV_WPE_D128) : (QF32 ? 1 : MIIKV_WPE_D256);
+    static constexpr bool vbias = D == 128 ? MIIKV_VBIAS_D128 != 0 : (QF32 ? true : MIIKV_VBIAS_D256 != 0);
+};
 constexpr uint32_t kTargetWaves = 256 * 8;  // 256 CUs x 8 resident waves
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kCodeBias = 1152.0f;  // codes enter the MFMA as fp16(code + 1152)
@@ -92,7 +103,7 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 
 template <uint32_t D, bool QF32, bool APPEND>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? MIIKV_WPE_D128 : MIIKV_WPE_D256)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DecodeTuning<D, QF32>::waves_per_eu)))
 decode_kernel(SplitArgs a) {
     constexpr uint32_t NB = D / 32;   // q8_0 blocks per row
     constexpr uint32_t NC = D / 64;   // 16-byte K loads per tile row group
@@ -100,7 +111,7 @@ decode_kernel(SplitArgs a) {
     using ScaleVec = typename std::conditional<NB == 4, uint32_t, uint2>::type;  // NB/2 fp16 scales
     // V codes enter the PV MFMA biased (one v_perm per two codes) and the bias is removed
     // with column sums, or exactly (perm + subtract): the fold costs NB accumulators.
-    constexpr bool kVBias = (D == 128) ? true : (MIIKV_VBIAS_D256 != 0);
+    constexpr bool kVBias = DecodeTuning<D, QF32>::vbias;
     extern __shared__ float smem[];
 
     const uint32_t split = blockIdx.x;
@@ -158,7 +169,7 @@ decode_kernel(SplitArgs a) {
     };
 
     // Ring of kRing step buffers; the first kRing-1 are loaded before L is known.
-    constexpr uint32_t kRing = (D == 128) ? MIIKV_RING_D128 : MIIKV_RING_D256;
+    constexpr uint32_t kRing = DecodeTuning<D, QF32>::ring;
     Step S[kRing];
 #pragma unroll
     for (uint32_t r = 0; r + 1 < kRing; ++r)
