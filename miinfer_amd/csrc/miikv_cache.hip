@@ -85,7 +85,7 @@ __device__ __forceinline__ void k_norm_rope16(float (&x)[16], const float* w, ui
     }
     float partner[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) partner[i] = __shfl_xor(x[i], 2, 64);
+    for (int i = 0; i < 16; ++i) partner[i] = dpp_mov<0x4E>(x[i]);  // lane ^ 2
     if (q16 >= 4) return;
     const float step = powf(theta, -2.0f / 64.0f);
     float angle = static_cast<float>(position);

@@ -86,6 +86,59 @@ __device__ __forceinline__ uint32_t v_code_offset(uint32_t tp, uint32_t d, uint3
     return H * (32 * D) + d * 32 + G * 8 + J * 4 + I;
 }
 
+// Butterfly reductions over aligned lane groups of 2..64 lanes without an LDS
+// round trip: DPP quad permutes for partners 1 and 2, the row half-mirror and
+// mirror for partners in the other quad / half-row (within a group whose lanes
+// already agree these pair the same groups as xor 4 and xor 8), and the gfx950
+// permlane swaps for partners 16 and 32 lanes away. Every lane of a group ends
+// with the same value, combined in the same tree as the xor-shuffle butterfly.
+template <typename T>
+__device__ __forceinline__ T lane_bits_to(int v) { return __builtin_bit_cast(T, v); }
+template <uint32_t kCtrl, typename T>
+__device__ __forceinline__ T dpp_mov(T x) {
+    return lane_bits_to<T>(__builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kCtrl, 0xF, 0xF, false));
+}
+// The swap results are copied out element by element before any bit cast: clang
+// lowers __builtin_bit_cast of an element of the returned vector to element 0.
+template <typename T, typename Op>
+__device__ __forceinline__ T swap16_reduce(T x, Op op) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, x);
+    const auto r = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+    const uint32_t r0 = r[0], r1 = r[1];
+    return op(__builtin_bit_cast(T, r0), __builtin_bit_cast(T, r1));
+}
+template <typename T, typename Op>
+__device__ __forceinline__ T swap32_reduce(T x, Op op) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, x);
+    const auto r = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+    const uint32_t r0 = r[0], r1 = r[1];
+    return op(__builtin_bit_cast(T, r0), __builtin_bit_cast(T, r1));
+}
+// Reduce over the kLanes-lane group (lanes [k*kLanes, (k+1)*kLanes)) holding x.
+template <uint32_t kLanes, typename T, typename Op>
+__device__ __forceinline__ T group_reduce(T x, Op op) {
+    static_assert(kLanes >= 2 && kLanes <= 64 && (kLanes & (kLanes - 1)) == 0, "power of two");
+    x = op(x, dpp_mov<0xB1>(x));                        // quad_perm [1,0,3,2]
+    if constexpr (kLanes >= 4) x = op(x, dpp_mov<0x4E>(x));   // quad_perm [2,3,0,1]
+    if constexpr (kLanes >= 8) x = op(x, dpp_mov<0x141>(x));  // row_half_mirror
+    if constexpr (kLanes >= 16) x = op(x, dpp_mov<0x140>(x)); // row_mirror
+    if constexpr (kLanes >= 32) x = swap16_reduce(x, op);
+    if constexpr (kLanes >= 64) x = swap32_reduce(x, op);
+    return x;
+}
+struct MaxOp {
+    __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+struct AddOp {
+    template <typename T>
+    __device__ T operator()(T a, T b) const { return a + b; }
+};
+// Reduce across the four 16-lane rows (partners 16 and 32 lanes away) only.
+template <typename T, typename Op>
+__device__ __forceinline__ T rows_reduce(T x, Op op) {
+    return swap32_reduce(swap16_reduce(x, op), op);
+}
+
 // q8_0 quantization of 16 values held by this lane; its partner lane (lane ^ 1)
 // holds the other 16 values of the same 32-value block.  Rule of
 // gfx906/kernels/qwen3_primitives.hip:7285-7322 applied per block.
@@ -93,7 +146,7 @@ __device__ __forceinline__ void quantize16(const float (&x)[16], int8_t (&q)[16]
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(x[i]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = group_reduce<2>(amax, MaxOp{});
     const float scale = (amax > 0.0f) ? (amax / 127.0f) : 1.0f;
     const float inv = (scale > 0.0f) ? (1.0f / scale) : 1.0f;
 #pragma unroll

@@ -88,9 +88,7 @@ __device__ __forceinline__ uint2 load8(const int8_t* p) {
 }
 
 __device__ __forceinline__ float wave_max_xor_16_32(float x) {
-    x = fmaxf(x, __shfl_xor(x, 16, 64));
-    x = fmaxf(x, __shfl_xor(x, 32, 64));
-    return x;
+    return rows_reduce(x, MaxOp{});
 }
 
 // Raw v_exp_f32: no denormal range fix-up (results below 2^-126 flush to 0, which
@@ -214,8 +212,7 @@ decode_kernel(SplitArgs a) {
                     for (int i = 0; i < 8; ++i) qs += static_cast<float>(v[i]);
                 }
             }
-            qs += __shfl_xor(qs, 16, 64);
-            qs += __shfl_xor(qs, 32, 64);
+            qs = rows_reduce(qs, AddOp{});
             kbias[blk] = kCodeBias * qs;
             qf[blk] = v;
             if (QF32) ql[QF32 ? blk : 0] = lo;
@@ -395,8 +392,7 @@ decode_kernel(SplitArgs a) {
     }
 
     // ---- wave-level sums, then cross-wave combine in LDS.
-    l_run += __shfl_xor(l_run, 16, 64);
-    l_run += __shfl_xor(l_run, 32, 64);
+    l_run = rows_reduce(l_run, AddOp{});
     float* s_m = smem;                          // [waves][16]
     float* s_l = smem + 16 * kWavesPerWg;       // [waves][16]
     float* s_O = smem + 32 * kWavesPerWg;       // [waves][G][D]

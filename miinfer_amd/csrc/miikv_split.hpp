@@ -151,18 +151,14 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
         // codes round-to-nearest-even, clamped; the score uses code * fp16(scale).
         const uint32_t t = threadIdx.x;
         float ka = fabsf(kx), va = fabsf(vx);
-#pragma unroll
-        for (uint32_t off = 1; off < 32; off <<= 1) {
-            ka = fmaxf(ka, __shfl_xor(ka, off, 64));
-            va = fmaxf(va, __shfl_xor(va, off, 64));
-        }
+        ka = group_reduce<32>(ka, MaxOp{});
+        va = group_reduce<32>(va, MaxOp{});
         const float ksc = ka > 0.0f ? ka / 127.0f : 1.0f, vsc = va > 0.0f ? va / 127.0f : 1.0f;
         const int kq = max(-128, min(127, __float2int_rn(kx * (1.0f / ksc))));
         const int vq = max(-128, min(127, __float2int_rn(vx * (1.0f / vsc))));
         const uint16_t kbits = f32_to_f16_bits(ksc), vbits = f32_to_f16_bits(vsc);
         float part = t < D ? qx * (static_cast<float>(kq) * f16_bits_to_f32(kbits)) : 0.0f;
-#pragma unroll
-        for (uint32_t off = 1; off < 64; off <<= 1) part += __shfl_xor(part, off, 64);
+        part = group_reduce<64>(part, AddOp{});
         if ((t & 63) == 0) s_dot[t >> 6] = part;
         if (t < D) s_vnew[t] = static_cast<float>(vq) * f16_bits_to_f32(vbits);
         const uint32_t L = split_length(a, b);
@@ -232,8 +228,7 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
         // Q8_1 block of 32 gated values = 8 consecutive lanes (qwen3_primitives.hip:
         // 2354-2384): d = amax/127, q = clamp(roundf(x/d), -127, 127), s = sum(q)*d.
         float amax = fmaxf(fmaxf(fabsf(gated[0]), fabsf(gated[1])), fmaxf(fabsf(gated[2]), fabsf(gated[3])));
-#pragma unroll
-        for (uint32_t off = 1; off < 8; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+        amax = group_reduce<8>(amax, MaxOp{});
         const float d = amax / 127.0f;
         const float qinv = d != 0.0f ? 1.0f / d : 0.0f;
         int qs[4];
@@ -243,8 +238,7 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
             qs[k] = max(-127, min(127, static_cast<int>(roundf(gated[k] * qinv))));
             sum += qs[k];
         }
-#pragma unroll
-        for (uint32_t off = 1; off < 8; off <<= 1) sum += __shfl_xor(sum, off, 64);
+        sum = group_reduce<8>(sum, AddOp{});
         const size_t blk = (out_row0 + e) / 32;
         uint8_t* bp = a.gated_q8_1 + blk * 36;
         *reinterpret_cast<uint32_t*>(bp + 4 + 4 * (e4 & 7)) =

@@ -358,7 +358,7 @@ __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
         float cmax = fmaxf(acc[0], acc[1]);
 #pragma unroll
         for (uint32_t r = 2; r < 16; r += 2) cmax = fmaxf(cmax, fmaxf(acc[r], acc[r + 1]));
-        cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+        cmax = swap32_reduce(cmax, MaxOp{});
         const float cm = cmax * a.scale_log2;
         const bool grow = cm > m_run + kSlackS;
         if (__any(grow)) {
@@ -399,7 +399,7 @@ __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
     }
 
     // ---- store: lane (n, hh) holds dims 32mt + 8j + 4hh + i of row n (register 4j + i).
-    l_run += __shfl_xor(l_run, 32, 64);
+    l_run = swap32_reduce(l_run, AddOp{});
     if (!row_ok) return;
     if (a.splits > 1) {
         const uint32_t rows_cap = a.token_count * G;
