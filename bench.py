@@ -134,23 +134,24 @@ def bench_c3(dev, args) -> int:
     P = ctypes.c_void_p
 
     def step(s):
-        st = L.miikv_append_batch_f16(cache.view, P(kn.data_ptr()), P(vn.data_ptr()), batch,
-                                      P(pos.data_ptr()), P(s.cuda_stream))
-        st |= L.miikv_decode_attn(cache.view, P(q.data_ptr()), _lib.DTYPE_F16, hq,
-                                  ctypes.c_float(1 / math.sqrt(d)), batch, P(lengths.data_ptr()),
-                                  None, max_ctx, P(out.data_ptr()), None, None, P(ws.buf.data_ptr()),
-                                  ws.bytes, P(s.cuda_stream))
+        # one launch pair: the new rows are stored and scored by the combine kernel
+        st = L.miikv_decode_append_attn(cache.view, P(kn.data_ptr()), P(vn.data_ptr()), P(q.data_ptr()),
+                                        _lib.DTYPE_F16, hq, ctypes.c_float(1 / math.sqrt(d)), batch,
+                                        P(lengths.data_ptr()), None, max_ctx, P(out.data_ptr()), None,
+                                        None, None, P(ws.buf.data_ptr()), ws.bytes, P(s.cuda_stream))
         assert st == 0, st
 
-    def dec(s):
-        st = L.miikv_decode_attn(cache.view, P(q.data_ptr()), _lib.DTYPE_F16, hq,
+    def dec(s, qq=q, dt=_lib.DTYPE_F16):
+        st = L.miikv_decode_attn(cache.view, P(qq.data_ptr()), dt, hq,
                                  ctypes.c_float(1 / math.sqrt(d)), batch, P(lengths.data_ptr()),
                                  None, max_ctx, P(out.data_ptr()), None, None, P(ws.buf.data_ptr()),
                                  ws.bytes, P(s.cuda_stream))
         assert st == 0, st
+    q32 = q.float()
     torch.cuda.synchronize()
     us, n = _time_graph(step, max(10, args.steps // 10), 10)
     us_dec, _ = _time_graph(dec, max(10, args.steps // 10), 10)
+    us_dec32, _ = _time_graph(lambda s: dec(s, q32, _lib.DTYPE_F32), max(10, args.steps // 10), 10)
     tokens = int(lens.sum())
     dbytes = tokens * kv_bytes_per_token(hkv, d) + batch * hq * d * 6
     print(json.dumps({
@@ -163,6 +164,9 @@ def bench_c3(dev, args) -> int:
                      "achieved": round(dbytes / (us_dec * 1e-6) / 1e9, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(dbytes / (us_dec * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
                      "algorithmic_bytes_per_launch": dbytes, "avg_launch_us": round(us_dec, 2)},
+        "step": "miikv_decode_append_attn (store the 16 new rows + attend)",
+        "decode_fp32_query": {"avg_launch_us": round(us_dec32, 2),
+                              "GBs": round((dbytes + batch * hq * d * 2) / (us_dec32 * 1e-6) / 1e9, 1)},
     }), flush=True)
     return 0
 

@@ -51,6 +51,15 @@ namespace {
 #ifndef MIIKV_RING_D256
 #define MIIKV_RING_D256 1
 #endif
+#ifndef MIIKV_RING_D256_F32
+#define MIIKV_RING_D256_F32 1
+#endif
+#ifndef MIIKV_WPE_D256_F32
+#define MIIKV_WPE_D256_F32 1
+#endif
+#ifndef MIIKV_VBIAS_D256_F32
+#define MIIKV_VBIAS_D256_F32 1
+#endif
 #ifndef MIIKV_WPE_D256
 #define MIIKV_WPE_D256 2
 #endif
@@ -64,9 +73,9 @@ namespace {
 // MFMA per block; those variants keep a deeper ring at lower occupancy.
 template <uint32_t D, bool QF32>
 struct DecodeTuning {
-    static constexpr uint32_t ring = D == 128 ? MIIKV_RING_D128 : (QF32 ? 2 : MIIKV_RING_D256);
-    static constexpr uint32_t waves_per_eu = D == 128 ? (QF32 ? 2 : MIIKV_WPE_D128) : (QF32 ? 1 : MIIKV_WPE_D256);
-    static constexpr bool vbias = D == 128 ? MIIKV_VBIAS_D128 != 0 : (QF32 ? true : MIIKV_VBIAS_D256 != 0);
+    static constexpr uint32_t ring = D == 128 ? MIIKV_RING_D128 : (QF32 ? MIIKV_RING_D256_F32 : MIIKV_RING_D256);
+    static constexpr uint32_t waves_per_eu = D == 128 ? (QF32 ? 2 : MIIKV_WPE_D128) : (QF32 ? MIIKV_WPE_D256_F32 : MIIKV_WPE_D256);
+    static constexpr bool vbias = D == 128 ? MIIKV_VBIAS_D128 != 0 : (QF32 ? MIIKV_VBIAS_D256_F32 != 0 : MIIKV_VBIAS_D256 != 0);
 };
 constexpr uint32_t kTargetWaves = 256 * 8;  // 256 CUs x 8 resident waves
 constexpr float kLog2e = 1.4426950408889634f;
@@ -152,16 +161,18 @@ decode_kernel(SplitArgs a) {
         const int8_t* kb = geo.k_codes + ld_slab * slab_bytes + static_cast<size_t>(ld_tp) * D;
         const int8_t* vb = geo.v_codes + ld_slab * slab_bytes + static_cast<size_t>(ld_tp) * D;
         const size_t sc0 = (ld_slab * geo.page_tokens + ld_tp) * NB;
+        // Scales first, each ahead of its codes: loads complete in issue order, so the
+        // score MFMAs wait only for the K scales and codes while V is still in flight.
+        st.ks = *reinterpret_cast<const ScaleVec*>(geo.k_scales + sc0 + lane * (NB / 2));
 #pragma unroll
         for (uint32_t J = 0; J < 2; ++J)
 #pragma unroll
             for (uint32_t cc = 0; cc < NC; ++cc)
                 st.k[J][cc] = load16(kb + J * 16 * D + cc * 1024 + g4 * 256 + n * 16);
+        st.vs = *reinterpret_cast<const ScaleVec*>(geo.v_scales + sc0 + lane * (NB / 2));
 #pragma unroll
         for (uint32_t mt = 0; mt < NM; ++mt)
             st.v[mt] = load8(vb + (16 * mt + n) * 32 + g4 * 8);
-        st.ks = *reinterpret_cast<const ScaleVec*>(geo.k_scales + sc0 + lane * (NB / 2));
-        st.vs = *reinterpret_cast<const ScaleVec*>(geo.v_scales + sc0 + lane * (NB / 2));
         ld_tok += kChunk;
         ld_tp += kChunk;
     };
