@@ -68,17 +68,19 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
     const uint32_t GD = G * D;
     const uint32_t e0 = blockIdx.y * 64;
     if (e0 >= GD) return;
-    // fused append: the new rows (dim tid), issued before the records
-    float kx = 0.0f, vx = 0.0f, qx = 0.0f;
+    // fused append: the new rows (dim tid), issued before the records as raw bits and
+    // converted after them, so no wait on these loads sits ahead of the record loads.
+    // Threads past D load dim D-1 and discard it.
+    uint32_t kraw = 0, vraw = 0, qraw = 0;
     const uint32_t hq0 = e0 / D;  // query head (within the group) of this workgroup's elements
     if constexpr (APPEND) {
-        if (threadIdx.x < D) {
-            const size_t row = (static_cast<size_t>(b) * a.g.kv_heads + h) * D + threadIdx.x;
-            kx = f16_bits_to_f32(a.k_new[row]);
-            vx = f16_bits_to_f32(a.v_new[row]);
-            const size_t qi = (static_cast<size_t>(b) * a.q_heads + static_cast<size_t>(h) * G + hq0) * D + threadIdx.x;
-            qx = a.q_f32 ? static_cast<const float*>(a.q)[qi] : f16_bits_to_f32(static_cast<const uint16_t*>(a.q)[qi]);
-        }
+        const uint32_t t = min(threadIdx.x, D - 1);
+        const size_t row = (static_cast<size_t>(b) * a.g.kv_heads + h) * D + t;
+        kraw = a.k_new[row];
+        vraw = a.v_new[row];
+        const size_t qi = (static_cast<size_t>(b) * a.q_heads + static_cast<size_t>(h) * G + hq0) * D + t;
+        if (a.q_f32) qraw = static_cast<const uint32_t*>(a.q)[qi];
+        else qraw = static_cast<const uint16_t*>(a.q)[qi];
     }
     const uint32_t tid = threadIdx.x;
     const uint32_t e4 = tid & 15;
@@ -147,6 +149,11 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
     s_gl[sg][e4] = lsum;
     float m_new = -INFINITY;
     if constexpr (APPEND) {
+        const bool row_lane = threadIdx.x < D;
+        const float kx = row_lane ? f16_bits_to_f32(static_cast<uint16_t>(kraw)) : 0.0f;
+        const float vx = row_lane ? f16_bits_to_f32(static_cast<uint16_t>(vraw)) : 0.0f;
+        const float qx = !row_lane ? 0.0f
+                         : a.q_f32 ? __uint_as_float(qraw) : f16_bits_to_f32(static_cast<uint16_t>(qraw));
         // Same rule as the append kernel: scale = amax/127 (1 for a zero block),
         // codes round-to-nearest-even, clamped; the score uses code * fp16(scale).
         const uint32_t t = threadIdx.x;
