@@ -2,6 +2,7 @@
 #include "miikv_common.hpp"
 
 #include <cmath>
+#include <cstdlib>
 
 namespace miikv {
 
@@ -182,6 +183,82 @@ __global__ void __launch_bounds__(256) append_kernel(
         const size_t sidx = (slab * g.page_tokens + tp) * (D / 32) + d0 / 32;
         g.k_scales[sidx] = f32_to_f16_bits(sk);
         g.v_scales[sidx] = f32_to_f16_bits(sv);
+    }
+}
+
+// Bulk append of whole 32-token groups: one workgroup per (group, kv head), one
+// thread per (token, 16-dim group) with the same arithmetic as append_kernel (so the
+// codes are identical), but the codes and scales are assembled in LDS and leave as
+// contiguous 16-byte stores: a 32-token group owns 32*D contiguous bytes of the K
+// slab (two 16-token tiles), 32*D of the V slab (one group) and 32*D/32 scales of
+// each kind.  base_position is a multiple of 32 and every group lies inside the
+// sequence's capacity (checked on the host).
+template <bool F32>
+__global__ void __launch_bounds__(512) append_tile_kernel(Geo g, AppendIn in, uint32_t base_position,
+                                                          uint32_t seq) {
+    extern __shared__ uint4 s_tile[];
+    const uint32_t D = g.head_dim;
+    const uint32_t groups = D / 16;
+    const uint32_t head = blockIdx.y;
+    const uint32_t tl = threadIdx.x / groups;  // token within the 32-token group
+    const uint32_t q16 = threadIdx.x % groups;
+    const uint32_t token = blockIdx.x * 32 + tl;
+    const uint32_t pos = base_position + token;
+    const size_t src = (static_cast<size_t>(token) * g.kv_heads + head) * D + q16 * 16;
+    float xk[16], xv[16];
+    if constexpr (F32) {
+        load16_f32(static_cast<const float*>(in.k) + src, xk);
+        load16_f32(static_cast<const float*>(in.v) + src, xv);
+        if (in.k_norm_weight != nullptr)
+            k_norm_rope16(xk, in.k_norm_weight, q16, groups, D, pos, in.theta, in.epsilon);
+    } else {
+        load16_f16(static_cast<const uint16_t*>(in.k) + src, xk);
+        load16_f16(static_cast<const uint16_t*>(in.v) + src, xv);
+    }
+    int8_t qk[16], qv[16];
+    float sk, sv;
+    quantize16(xk, qk, sk);
+    quantize16(xv, qv, sv);
+
+    uint8_t* s_k = reinterpret_cast<uint8_t*>(s_tile);  // [32*D] K codes, slab order
+    uint8_t* s_v = s_k + 32 * D;                         // [32*D] V codes, slab order
+    uint16_t* s_s = reinterpret_cast<uint16_t*>(s_v + 32 * D);  // [2][32][D/32] scales
+    const uint32_t d0 = q16 * 16;
+    uint32_t packed[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        packed[w] = (static_cast<uint32_t>(static_cast<uint8_t>(qk[4 * w]))) |
+                    (static_cast<uint32_t>(static_cast<uint8_t>(qk[4 * w + 1])) << 8) |
+                    (static_cast<uint32_t>(static_cast<uint8_t>(qk[4 * w + 2])) << 16) |
+                    (static_cast<uint32_t>(static_cast<uint8_t>(qk[4 * w + 3])) << 24);
+    }
+    *reinterpret_cast<uint2*>(s_k + k_code_offset(tl, d0, D)) = make_uint2(packed[0], packed[1]);
+    *reinterpret_cast<uint2*>(s_k + k_code_offset(tl, d0 + 8, D)) = make_uint2(packed[2], packed[3]);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s_v[v_code_offset(tl, d0 + i, D)] = static_cast<uint8_t>(qv[i]);
+    if ((q16 & 1) == 0) {
+        s_s[tl * (D / 32) + d0 / 32] = f32_to_f16_bits(sk);
+        s_s[32 * (D / 32) + tl * (D / 32) + d0 / 32] = f32_to_f16_bits(sv);
+    }
+    __syncthreads();
+
+    const uint32_t pos0 = base_position + blockIdx.x * 32;
+    const size_t slab = slab_of(g, seq, pos0, head);
+    const uint32_t tp0 = pos0 % g.page_tokens;
+    const size_t slab_bytes = static_cast<size_t>(g.page_tokens) * D;
+    uint4* kdst = reinterpret_cast<uint4*>(g.k_codes + slab * slab_bytes + static_cast<size_t>(tp0) * D);
+    uint4* vdst = reinterpret_cast<uint4*>(g.v_codes + slab * slab_bytes + static_cast<size_t>(tp0) * D);
+    const uint32_t chunks = 32 * D / 16;  // 16-byte chunks per code region
+    for (uint32_t c = threadIdx.x; c < chunks; c += blockDim.x) {
+        kdst[c] = s_tile[c];
+        vdst[c] = s_tile[chunks + c];
+    }
+    const uint32_t schunks = 32 * (D / 32) * 2 / 16;  // 16-byte chunks per scale region
+    const size_t sidx = (slab * g.page_tokens + tp0) * (D / 32);
+    if (threadIdx.x < 2 * schunks) {
+        const uint32_t kind = threadIdx.x / schunks, c = threadIdx.x % schunks;
+        uint16_t* sdst = (kind == 0 ? g.k_scales : g.v_scales) + sidx;
+        reinterpret_cast<uint4*>(sdst)[c] = s_tile[2 * chunks + kind * schunks + c];
     }
 }
 
@@ -375,10 +452,23 @@ extern "C" miikv_status miikv_plane_bytes(const miikv_view* view, uint64_t* code
     return MIIKV_OK;
 }
 
+// Token count from which a host-positioned append sends its whole 32-token groups to
+// append_tile_kernel (the partial groups at either end go through append_kernel).
+constexpr uint32_t kTileAppendMin = 64;
+
 template <bool F32>
-static miikv_status launch_append(const miikv_view* view, const AppendIn& in, uint32_t rows_tokens, uint32_t base,
-                                  uint32_t seq, const miikv_prefill_state* ps, const miikv_decode_state* ds,
-                                  const uint32_t* positions, void* stream) {
+static AppendIn advance_rows(AppendIn in, uint64_t tokens, uint32_t kv_heads, uint32_t D) {
+    const uint64_t elems = tokens * kv_heads * D;
+    const size_t esize = F32 ? sizeof(float) : sizeof(uint16_t);
+    in.k = static_cast<const char*>(in.k) + elems * esize;
+    in.v = static_cast<const char*>(in.v) + elems * esize;
+    return in;
+}
+
+template <bool F32>
+static miikv_status launch_rows(const miikv_view* view, const AppendIn& in, uint32_t rows_tokens, uint32_t base,
+                                uint32_t seq, const miikv_prefill_state* ps, const miikv_decode_state* ds,
+                                const uint32_t* positions, void* stream) {
     const uint64_t threads = static_cast<uint64_t>(rows_tokens) * view->kv_heads * (view->head_dim / 16);
     if (threads == 0) return MIIKV_OK;
     const uint64_t blocks = (threads + 255) / 256;
@@ -387,6 +477,33 @@ static miikv_status launch_append(const miikv_view* view, const AppendIn& in, ui
                        static_cast<hipStream_t>(stream), make_geo(*view), in, rows_tokens, base, seq, ps, ds,
                        positions);
     return launch_status();
+}
+
+template <bool F32>
+static miikv_status launch_append(const miikv_view* view, const AppendIn& in, uint32_t rows_tokens, uint32_t base,
+                                  uint32_t seq, const miikv_prefill_state* ps, const miikv_decode_state* ds,
+                                  const uint32_t* positions, void* stream) {
+    // Positions known on the host: [head partial group][whole groups][tail partial group].
+    if (ps == nullptr && ds == nullptr && positions == nullptr && rows_tokens >= kTileAppendMin &&
+        std::getenv("MIIKV_APPEND_ROWS_ONLY") == nullptr) {
+        const uint32_t D = view->head_dim;
+        const uint32_t head = (32 - base % 32) % 32;
+        const uint32_t whole = (rows_tokens - head) / 32;
+        const uint32_t tail = rows_tokens - head - whole * 32;
+        int st = launch_rows<F32>(view, in, head, base, seq, nullptr, nullptr, nullptr, stream);
+        if (st != MIIKV_OK) return st;
+        if (whole > 0) {
+            const size_t lds = 2 * 32 * D + 2 * 32 * (D / 32) * sizeof(uint16_t);
+            hipLaunchKernelGGL(append_tile_kernel<F32>, dim3(whole, view->kv_heads), dim3(32 * (D / 16)), lds,
+                               static_cast<hipStream_t>(stream), make_geo(*view),
+                               advance_rows<F32>(in, head, view->kv_heads, D), base + head, seq);
+            st = launch_status();
+            if (st != MIIKV_OK) return st;
+        }
+        return launch_rows<F32>(view, advance_rows<F32>(in, head + 32ull * whole, view->kv_heads, D), tail,
+                                base + head + whole * 32, seq, nullptr, nullptr, nullptr, stream);
+    }
+    return launch_rows<F32>(view, in, rows_tokens, base, seq, ps, ds, positions, stream);
 }
 
 static AppendIn f16_rows(const uint16_t* k, const uint16_t* v) {

@@ -448,7 +448,6 @@ decode_kernel(SplitArgs a) {
         mine[idx] = o;
     }
 
-    // ---- publish, and let the last workgroup of this (sequence, kv head) finish.
 }
 
 

@@ -184,3 +184,50 @@ def test_append_f32_norm_rope_matches_oracle(gpu, hk, d, theta):
     deq = oracle.dequantize_rows(kc, ks)
     step = oracle.dequantize_rows(np.ones_like(kc), ks)
     assert np.all(np.abs(deq - kn.transpose(1, 0, 2)) <= step * 1.01)
+
+
+@pytest.mark.parametrize("hk,d", [(8, 128), (4, 256)])
+def test_append_tile_path_matches_row_path(gpu, hk, d, monkeypatch):
+    """Bulk appends send whole 32-token groups through the LDS-assembled tile kernel and
+    the partial groups at either end through the per-row kernel: the bytes must equal
+    the per-row kernel's alone (same arithmetic), for fp16 rows against the oracle too,
+    on a contiguous cache and across page boundaries of a paged one, from unaligned
+    starts."""
+    import miinfer_amd as m
+    rng = np.random.default_rng(400 + d)
+    pt = 256
+    table = _dev(np.array([[3, 0, 2]], np.int32), gpu)
+    k16 = _edge_rows(rng, 400, hk, d)
+    v16 = randn_f16(rng, (400, hk, d))
+    k32 = rng.standard_normal((400, hk, d)).astype(np.float32) * 4
+    v32 = rng.standard_normal((400, hk, d)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, d).astype(np.float32)
+
+    def run(rows_only):
+        if rows_only:
+            monkeypatch.setenv("MIIKV_APPEND_ROWS_ONLY", "1")
+        else:
+            monkeypatch.delenv("MIIKV_APPEND_ROWS_ONLY", raising=False)
+        out = []
+        for layout in ("contiguous", "paged"):
+            cache = (m.KvCache.contiguous(hk, d, 768) if layout == "contiguous"
+                     else m.KvCache.paged_cache(hk, d, 4, table, page_tokens=pt))
+            cache.append(_dev(k16[:300], gpu), _dev(v16[:300], gpu), base_position=45)
+            cache.append_f32(_dev(k32[:100], gpu), _dev(v32[:100], gpu), base_position=345,
+                             k_norm_weight=_dev(w, gpu), theta=1.0e6, epsilon=1e-6)
+            cache.append_f32(_dev(k32[100:400], gpu), _dev(v32[100:400], gpu), base_position=445)
+            out.append(_export_np(cache, 0, 0, 745))
+        return out
+
+    tiled = run(False)
+    rows = run(True)
+    for a, b in zip(tiled, rows):
+        for x, y in zip(a, b):
+            assert np.array_equal(x, y)
+    kc, ks, vc, vs = tiled[0]
+    ekc, eks = oracle.quantize_rows(k16[:300].transpose(1, 0, 2))
+    evc, evs = oracle.quantize_rows(v16[:300].transpose(1, 0, 2))
+    assert np.array_equal(kc[:, 45:345], ekc) and np.array_equal(ks[:, 45:345], eks)
+    assert np.array_equal(vc[:, 45:345], evc) and np.array_equal(vs[:, 45:345], evs)
+    ek, eks = oracle.quantize_rows_f32(k32[100:400].transpose(1, 0, 2))
+    assert np.array_equal(kc[:, 445:745], ek) and np.array_equal(ks[:, 445:745], eks)
