@@ -109,6 +109,51 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 #endif
 
 
+// Packed work items of a batch: sequence b owns ceil(L_b / split tokens) * kv_heads
+// items (none past *count_ptr).  Every workgroup scans the per-sequence counts
+// (256 sequences per pass, Hillis-Steele in LDS) and finds the item at index
+// `id`; false if the batch holds fewer items.  Called by all 256 threads.
+__device__ bool locate_item(const SplitArgs& a, uint32_t cpw, uint32_t id, uint32_t& b_out, uint32_t& h_out,
+                            uint32_t& split_out) {
+    __shared__ uint32_t s_scan[256];
+    __shared__ uint32_t s_hit[3];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t tps = kWavesPerWg * cpw * kChunk;
+    const uint32_t H = a.g.kv_heads;
+    const uint32_t count = a.count_ptr ? min(a.batch, *a.count_ptr) : a.batch;
+    if (tid == 0) s_hit[0] = 0xffffffffu;
+    uint32_t base = 0;
+    for (uint32_t b0 = 0; b0 < count; b0 += 256) {
+        const uint32_t bb = b0 + tid;
+        const uint32_t nsplit = bb < count ? (split_length(a, bb) + tps - 1) / tps : 0;
+        const uint32_t n = nsplit * H;
+        s_scan[tid] = n;
+        __syncthreads();
+        for (uint32_t off = 1; off < 256; off <<= 1) {
+            const uint32_t add = tid >= off ? s_scan[tid - off] : 0;
+            __syncthreads();
+            s_scan[tid] += add;
+            __syncthreads();
+        }
+        const uint32_t incl = base + s_scan[tid];
+        const uint32_t excl = incl - n;
+        if (id >= excl && id < incl) {
+            const uint32_t rem = id - excl;
+            s_hit[0] = bb;
+            s_hit[1] = rem / nsplit;
+            s_hit[2] = rem % nsplit;
+        }
+        base += s_scan[255];
+        __syncthreads();
+    }
+    __syncthreads();
+    if (s_hit[0] == 0xffffffffu) return false;
+    b_out = s_hit[0];
+    h_out = s_hit[1];
+    split_out = s_hit[2];
+    return true;
+}
+
 template <uint32_t D, bool QF32, bool APPEND>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DecodeTuning<D, QF32>::waves_per_eu)))
 decode_kernel(SplitArgs a) {
@@ -121,9 +166,21 @@ decode_kernel(SplitArgs a) {
     constexpr bool kVBias = DecodeTuning<D, QF32>::vbias;
     extern __shared__ float smem[];
 
-    const uint32_t split = blockIdx.x;
-    const uint32_t h = blockIdx.y;
-    const uint32_t b = blockIdx.z;
+    // Work item of this workgroup: one (sequence b, kv head h, split) of 4 waves x
+    // cpw steps.  One sequence: workgroup x = h * max_splits + split.  A batch: the
+    // items that hold keys are packed to the front of the grid (sequence-major,
+    // then head, then split), so whatever the lengths, the busy workgroups are the
+    // first ones dispatched and spread evenly over the XCDs and CUs; the grid's
+    // tail (bounded by max_context) exits at once.
+    const uint32_t cpw = launch_cpw(a);
+    uint32_t split, h, b;
+    if (a.batch == 1) {
+        b = 0;
+        h = blockIdx.x / a.max_splits;
+        split = blockIdx.x % a.max_splits;
+    } else if (!locate_item(a, cpw, blockIdx.x, b, h, split)) {
+        return;
+    }
     const uint32_t tid = threadIdx.x;
     const uint32_t wave = tid >> 6;
     const uint32_t lane = tid & 63;
@@ -134,9 +191,9 @@ decode_kernel(SplitArgs a) {
 
     // Steps this wave may own, from the host bound alone: the first loads are issued
     // before the context length arrives from memory.
-    const uint32_t c_begin = (split * kWavesPerWg + wave) * a.cpw;
+    const uint32_t c_begin = (split * kWavesPerWg + wave) * cpw;
     const uint32_t nsteps_max = (a.max_context + kChunk - 1) / kChunk;
-    const uint32_t c_end_max = min(c_begin + a.cpw, nsteps_max);
+    const uint32_t c_end_max = min(c_begin + cpw, nsteps_max);
     const size_t slab_bytes = static_cast<size_t>(geo.page_tokens) * D;
 
     // Registers of one 32-token step: two K tiles, one V group, their scales.
@@ -185,7 +242,7 @@ decode_kernel(SplitArgs a) {
         if (c_begin + r < c_end_max) load_step(S[r]);
 
     const uint32_t L = split_length(a, b);
-    const uint32_t tps = kWavesPerWg * a.cpw * kChunk;
+    const uint32_t tps = kWavesPerWg * cpw * kChunk;
     const uint32_t nsplit = (L + tps - 1) / tps;
     if (split >= nsplit) return;  // includes L == 0 (the combine kernel writes zeros)
 
@@ -452,8 +509,17 @@ decode_kernel(SplitArgs a) {
 
 
 
+// Workgroups of decode_kernel resident on the chip at its occupancy: 256 CUs x 4
+// SIMDs x waves per SIMD, 4 waves per workgroup.
+uint32_t resident_workgroups(uint32_t D, bool f32) {
+    const uint32_t wpe = D == 128 ? (f32 ? DecodeTuning<128, true>::waves_per_eu : DecodeTuning<128, false>::waves_per_eu)
+                                  : (f32 ? DecodeTuning<256, true>::waves_per_eu : DecodeTuning<256, false>::waves_per_eu);
+    return 256 * 4 * wpe / kWavesPerWg;
+}
+
 struct Plan {
     uint32_t cpw;
+    bool adaptive;  // steps per wave chosen on the device (launch_cpw)
     uint32_t splits;
     uint64_t counter_bytes;
     uint64_t part_bytes;
@@ -471,6 +537,11 @@ Plan make_plan(const miikv_view* v, uint32_t q_heads, uint32_t batch, uint32_t m
         const char* e = std::getenv("MIIKV_DECODE_STEPS_PER_WAVE");
         return e ? std::strtoull(e, nullptr, 10) : 0ull;
     }();
+    // A batch: cpw is the floor of the device-side choice (launch_cpw), which
+    // can only raise it; the records and the grid are sized for the floor, a
+    // quarter of the all-sequences-full value.
+    if (batch > 1) cpw = (cpw + 3) / 4;
+    p.adaptive = batch > 1 && fixed_cpw == 0;
     if (fixed_cpw != 0) cpw = fixed_cpw;
     if (cpw < 1) cpw = 1;
     if (cpw > 64) cpw = 64;
@@ -573,7 +644,12 @@ static miikv_status decode_impl(const miikv_view* view, const uint16_t* k_new, c
     const size_t lds = (32 * kWavesPerWg + kWavesPerWg * G * view->head_dim) * sizeof(float) +
                        kWavesPerWg * 2 * kChunk * (view->head_dim / 32) * sizeof(uint16_t);
     if (lds > 64 * 1024) return MIIKV_EUNSUPPORTED;
-    const dim3 grid(p.splits, view->kv_heads, batch);
+    // One workgroup per possible (sequence, kv head, split) work item.
+    const uint64_t wgs = static_cast<uint64_t>(p.splits) * view->kv_heads * batch;
+    if (wgs > 0x7fffffffu) return MIIKV_EINVAL;
+    a.batch = batch;
+    a.slots = p.adaptive ? resident_workgroups(view->head_dim, q_dtype == MIIKV_DTYPE_F32) : 0u;
+    const dim3 grid(static_cast<uint32_t>(wgs));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool f32 = q_dtype == MIIKV_DTYPE_F32;
     const dim3 cgrid(batch * view->kv_heads, (G * view->head_dim + 63) / 64);

@@ -26,7 +26,11 @@ struct SplitArgs {
     const uint32_t* count_ptr;  // if set, row-sets b >= *count_ptr are skipped
     uint32_t max_context;
     uint32_t cpw;         // chunks per wave
-    uint32_t max_splits;  // == gridDim.x
+    uint32_t max_splits;  // splits per (sequence, kv head)
+    uint32_t batch;       // sequences (row-sets)
+    // batch > 1: resident workgroups of the split kernel; the steps per wave are
+    // then chosen on the device from the lengths (at least cpw), 0: always cpw
+    uint32_t slots;
     float* part;          // [batch][kv_heads][max_splits][group*(D+2)]
     float* out;
     const float* gate;
@@ -47,6 +51,34 @@ __host__ __device__ __forceinline__ uint32_t record_floats(uint32_t G, uint32_t 
 __device__ __forceinline__ uint32_t split_length(const SplitArgs& a, uint32_t b) {
     uint32_t L = (a.len_ptr ? a.len_ptr[static_cast<size_t>(b) * a.len_stride] : 0u) + a.len_add + b * a.len_bstep;
     return L > a.max_context ? a.max_context : L;
+}
+
+// Steps per wave of a launch.  One sequence: the host's cpw.  A batch: the lengths
+// are only known on the device, so every workgroup of both kernels derives the
+// same value from them: the smallest cpw (>= the host's, which sized the records)
+// for which the work items, at most sum(L_b) * H / (4 waves * 32 * cpw) + count * H,
+// fit in one round of `slots` resident workgroups.  Called by all threads of a
+// 256-thread block (barriers inside).
+__device__ uint32_t launch_cpw(const SplitArgs& a) {
+    if (a.batch == 1 || a.slots == 0) return a.cpw;
+    __shared__ unsigned long long s_sum[256];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t count = a.count_ptr ? min(a.batch, *a.count_ptr) : a.batch;
+    unsigned long long sum = 0;
+    for (uint32_t bb = tid; bb < count; bb += 256) sum += split_length(a, bb);
+    s_sum[tid] = sum;
+    __syncthreads();
+    for (uint32_t off = 128; off > 0; off >>= 1) {
+        if (tid < off) s_sum[tid] += s_sum[tid + off];
+        __syncthreads();
+    }
+    const unsigned long long total = s_sum[0] * a.g.kv_heads;
+    __syncthreads();  // s_sum is reused by the next call
+    const unsigned long long fixed_items = static_cast<unsigned long long>(count) * a.g.kv_heads;
+    const unsigned long long room = a.slots > fixed_items ? a.slots - fixed_items : a.slots;
+    const unsigned long long per = static_cast<unsigned long long>(kWavesPerWg) * kChunk * room;
+    const unsigned long long cpw = (total + per - 1) / per;
+    return static_cast<uint32_t>(cpw < a.cpw ? a.cpw : (cpw > 64 ? 64 : cpw));
 }
 
 // Cross-split combine.  Workgroup (sequence * kv_heads + head, element block of 64)
@@ -111,9 +143,10 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
             if (active) vv[j] = *reinterpret_cast<const float4*>(r + e);
         }
     }
+    const uint32_t cpw = launch_cpw(a);
     if (a.count_ptr != nullptr && b >= *a.count_ptr) return;
     uint32_t L = split_length(a, b);
-    const uint32_t tps = kWavesPerWg * a.cpw * kChunk;
+    const uint32_t tps = kWavesPerWg * cpw * kChunk;
     const uint32_t nsplit = (L + tps - 1) / tps;
 
     float mloc = -INFINITY;
