@@ -170,3 +170,37 @@ def test_decode_rejects_bad_arguments(gpu):
     with pytest.raises(m.MiikvError):  # max_context beyond capacity
         m.decode_attention(cache, q, lengths=torch.ones(1, dtype=torch.int32, device=gpu),
                            max_context=512)
+
+
+def test_decode_batch_device_chosen_split(gpu):
+    """A batch whose total context is large enough that the device raises the steps
+    per wave above the host's floor (the lengths are only known on the device): the
+    packed work items and the combine must agree on the split size."""
+    import miinfer_amd as m
+    rng = np.random.default_rng(31)
+    hq, hk, d, pt = 32, 8, 128, 256
+    lens = [60000, 1000, 30000, 9000, 1]
+    pages = [(n + pt) // pt for n in lens]
+    stride = max(pages)
+    perm = rng.permutation(sum(pages)).astype(np.int32)
+    table = np.zeros((len(lens), stride), np.int32)
+    o = 0
+    for s, p in enumerate(pages):
+        table[s, :p] = perm[o:o + p]
+        o += p
+    cache = m.KvCache.paged_cache(hk, d, sum(pages), _dev(table, gpu), page_tokens=pt)
+    refs = []
+    for s, n in enumerate(lens):
+        k = randn_f16(rng, (n, hk, d))
+        v = randn_f16(rng, (n, hk, d))
+        cache.append(_dev(k, gpu), _dev(v, gpu), base_position=0, seq=s)
+        refs.append((oracle.quantize_rows(k.transpose(1, 0, 2)), oracle.quantize_rows(v.transpose(1, 0, 2))))
+    q = randn_f16(rng, (len(lens), hq, d))
+    out, _ = m.decode_attention(cache, _dev(q, gpu), lengths=_dev(np.array(lens, np.int32), gpu),
+                                max_context=stride * pt)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    for s, n in enumerate(lens):
+        (kc, ks), (vc, vs) = refs[s]
+        expect = oracle.attention_q8(q[s].astype(np.float32), kc, ks, vc, vs, n, hq, 1 / math.sqrt(d))
+        assert_attention_close(out[s], expect, f"seq {s} L={n}")
