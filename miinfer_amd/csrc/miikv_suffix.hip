@@ -50,7 +50,7 @@ constexpr uint32_t kSufStep = 32;              // keys per step
 constexpr float kLog2eS = 1.4426950408889634f;
 constexpr float kSlackS = 6.0f;        // lazy-rescale threshold (log2 units): p <= 64
 // Resident workgroups of suffix_kernel on the chip: 256 CUs, each holding 8 waves
-// (two per SIMD at <= 256 VGPRs) and two 64 KiB LDS tile buffers per workgroup.
+// (two per SIMD at <= 256 VGPRs) and its LDS tile buffers (4 x 32 KiB at D = 256).
 constexpr uint32_t kSufSlots = 256 * (8 / kSufWaves);
 constexpr uint32_t kSufMaxSplits = 64;
 
@@ -205,10 +205,13 @@ __device__ __forceinline__ void wait_vmem_le() {
     else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
     else static_assert(N == 0, "unsupported count");
 }
-#ifndef MIIKV_SUFFIX_BUFS
-#define MIIKV_SUFFIX_BUFS 3
+#ifndef MIIKV_SUFFIX_STAGGER
+#define MIIKV_SUFFIX_STAGGER 1
 #endif
-constexpr uint32_t kSufBufs = MIIKV_SUFFIX_BUFS;  // LDS tile buffers (prefetch distance kSufBufs - 1)
+constexpr bool kSufStagger = MIIKV_SUFFIX_STAGGER != 0;
+constexpr uint32_t kDist = 2;                                       // prefetch distance (steps)
+constexpr uint32_t kSufBufs = kSufStagger ? kDist + 2 : kDist + 1;  // LDS tile buffers
+
 
 template <uint32_t D>
 __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
@@ -309,44 +312,25 @@ __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
 #pragma unroll
     for (uint32_t mt = 0; mt < NB; ++mt) O[mt] = float16v{};
 
-    // Step s lives in buffer s % kSufBufs; the fetch of step s + kSufBufs - 1 is
-    // issued at the top of step s into the buffer released by the last barrier.
+    // Step s lives in buffer s % kSufBufs; the fetch of step s + kDist is issued at
+    // the top of step s into a buffer that no wave reads any more (the barrier that
+    // ends each step orders it after those reads).
     constexpr uint32_t kPer = CHUNKS / kSufWaves;  // loads per wave per fetch
-    for (uint32_t k = 0; k + 1 < kSufBufs; ++k)
+    for (uint32_t k = 0; k < kDist; ++k)
         if (s_begin + k < s_end) fetch(s_begin + k, (s_begin + k) % kSufBufs);
     wait_vmem();
     __syncthreads();
 
-    for (uint32_t s = s_begin; s < s_end; ++s) {
-        const uint32_t buf = s % kSufBufs;
-        const bool ahead = s + kSufBufs - 1 < s_end;
-#ifndef MIIKV_SFX_EXP_NOFETCH
-        if (ahead) fetch(s + kSufBufs - 1, (s + kSufBufs - 1) % kSufBufs);
-#endif
-#ifdef MIIKV_SFX_EXP_NOLDS
-        // registers stand in for the LDS fragments
-        const _Float16* tk = reinterpret_cast<const _Float16*>(&qf[0]) - 0 * lane;
-        const _Float16* tv = tk;
-#define MIIKV_FRAG_K(c) qf[(c) % NC]
-#define MIIKV_FRAG_V(f) qf[(f) % NC]
-#else
-        const _Float16* tk = s_t[buf] + lane * 8;
-        const _Float16* tv = s_t[buf] + 64 * 8 * NC + lane * 8;
-#define MIIKV_FRAG_K(c) (*reinterpret_cast<const half8*>(tk + 512 * (c)))
-#define MIIKV_FRAG_V(f) (*reinterpret_cast<const half8*>(tv + 512 * (f)))
-#endif
-        // ---- S^T = K^ Q^T
+    // ---- S^T = K^ Q^T of step s
+    auto scores = [&](uint32_t s) __attribute__((always_inline)) {
+        const _Float16* tk = s_t[s % kSufBufs] + lane * 8;
         float16v acc = {};
 #pragma unroll
-        for (uint32_t c = 0; c < NC; ++c) {
-#ifdef MIIKV_SFX_EXP_NOMFMA
-            acc[c % 16] += (float)MIIKV_FRAG_K(c)[0];
-#else
-            acc = mfma_32x32x16(MIIKV_FRAG_K(c), qf[c], acc);
-#endif
-        }
-
-        // ---- online softmax over this lane's 16 keys of row n
+        for (uint32_t c = 0; c < NC; ++c) acc = mfma_32x32x16(*reinterpret_cast<const half8*>(tk + 512 * c), qf[c], acc);
+        return acc;
+    };
+    // ---- online softmax over this lane's 16 keys of row n; P^T fragments out
+    auto softmax = [&](uint32_t s, float16v acc, half8 (&pb)[2]) __attribute__((always_inline)) {
         const uint32_t key0 = s * kSufStep;
         if (key0 + kSufStep - 1 > wave_lim || key0 + kSufStep > key_hi) {
 #pragma unroll
@@ -371,7 +355,6 @@ __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
         }
         // A row with no visible key yet keeps m_run = -inf; subtracting 0 keeps p = 0.
         const float m_use = m_run == -INFINITY ? 0.0f : m_run;
-        half8 pb[2];
         float lsum = 0.0f;
 #pragma unroll
         for (uint32_t kc = 0; kc < 2; ++kc)
@@ -382,20 +365,55 @@ __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
                 pb[kc][e] = static_cast<_Float16>(p);  // round to nearest: no bias against l_run
             }
         l_run += lsum;
-        // ---- O^T += V^T P^T
+    };
+    // ---- O^T += V^T P^T of step s
+    auto values = [&](uint32_t s, const half8 (&pb)[2]) __attribute__((always_inline)) {
+        const _Float16* tv = s_t[s % kSufBufs] + 64 * 8 * NC + lane * 8;
 #pragma unroll
         for (uint32_t mt = 0; mt < NB; ++mt)
 #pragma unroll
             for (uint32_t kc = 0; kc < 2; ++kc)
-#ifdef MIIKV_SFX_EXP_NOMFMA
-                O[mt][kc] += (float)(MIIKV_FRAG_V(2 * mt + kc)[0] * pb[kc][0]);
-#else
-                O[mt] = mfma_32x32x16(MIIKV_FRAG_V(2 * mt + kc), pb[kc], O[mt]);
-#endif
-        // Step s+1's tile must have landed; this step's own fetch may stay in flight.
-        if (ahead) wait_vmem_le<(kSufBufs > 2 ? kPer : 0)>();
+                O[mt] = mfma_32x32x16(*reinterpret_cast<const half8*>(tv + 512 * (2 * mt + kc)), pb[kc], O[mt]);
+    };
+    // Top of step s: the fetch of step s + kDist.  End of step s: step s+1's tile
+    // must have landed (this step's own fetch may stay in flight), then the barrier.
+    auto step_begin = [&](uint32_t s) __attribute__((always_inline)) {
+        if (s + kDist < s_end) fetch(s + kDist, (s + kDist) % kSufBufs);
+    };
+    auto step_end = [&](uint32_t s) __attribute__((always_inline)) {
+        if (s + kDist < s_end) wait_vmem_le<(kDist > 1 ? kPer : 0)>();
         else wait_vmem();
         __syncthreads();
+    };
+
+    // With kSufStagger the two waves of each SIMD (waves w and w + kSufWaves/2)
+    // run half a step apart: the leading half orders a step as scores, softmax,
+    // values; the lagging half adds step s-1's values before step s's scores, so
+    // one wave's softmax can overlap the other's MFMAs (C4: ~2% faster).
+    // Every wave still passes one barrier per step; the lagging half's values of
+    // step s-1 read a buffer that is refilled only at the top of step s+1
+    // (kSufBufs >= kDist + 2).
+    const bool lag = kSufStagger && wave >= kSufWaves / 2;
+    if (!lag) {
+        for (uint32_t s = s_begin; s < s_end; ++s) {
+            step_begin(s);
+            half8 pb[2];
+            softmax(s, scores(s), pb);
+            values(s, pb);
+            step_end(s);
+        }
+    } else {
+        half8 pprev[2];
+        step_begin(s_begin);
+        softmax(s_begin, scores(s_begin), pprev);
+        step_end(s_begin);
+        for (uint32_t s = s_begin + 1; s < s_end; ++s) {
+            step_begin(s);
+            values(s - 1, pprev);
+            softmax(s, scores(s), pprev);
+            step_end(s);
+        }
+        values(s_end - 1, pprev);
     }
 
     // ---- store: lane (n, hh) holds dims 32mt + 8j + 4hh + i of row n (register 4j + i).
