@@ -344,10 +344,11 @@ def calibrate_copy(dev) -> int:
     return 0
 
 
-def stream_read_ceiling(dev, span_bytes: int, spans: int = 8, reps: int = 40) -> dict:
+def stream_read_ceiling(dev, span_bytes: int, spans: int = 8, reps: int = 20) -> dict:
     """Cold single-pass read of `span_bytes` (rotating over `spans` buffers so the
-    256 MB Infinity Cache does not serve it): the practical per-launch ceiling a
-    kernel streaming the same bytes can reach on this device."""
+    256 MB Infinity Cache does not serve it), timed like the decode step: back-to-back
+    launches captured in one graph.  The practical per-launch ceiling of a kernel
+    streaming the same bytes on this device."""
     import ctypes
 
     import torch
@@ -358,27 +359,79 @@ def stream_read_ceiling(dev, span_bytes: int, spans: int = 8, reps: int = 40) ->
     buf = torch.ones(span * spans, dtype=torch.uint8, device=dev)
     sink = torch.empty(blocks, dtype=torch.int32, device=dev)
     lib = _lib.lib()
-    times = []
-    s = torch.cuda.current_stream()
-    for it in range(reps):
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(s)
-        st = lib.miikv_stream_read(ctypes.c_void_p(buf.data_ptr() + (it % spans) * span), span,
-                                   ctypes.c_void_p(sink.data_ptr()), blocks,
-                                   ctypes.c_void_p(s.cuda_stream))
-        e1.record(s)
-        e1.synchronize()
+    counter = [0]
+
+    def read(s):
+        i = counter[0] % spans
+        counter[0] += 1
+        st = lib.miikv_stream_read(ctypes.c_void_p(buf.data_ptr() + i * span), span,
+                                   ctypes.c_void_p(sink.data_ptr()), blocks, ctypes.c_void_p(s.cuda_stream))
         if st:
             raise RuntimeError(f"stream probe failed: {st}")
-        if it >= 8:
-            times.append(e0.elapsed_time(e1) * 1e3)
-    times.sort()
-    us = times[len(times) // 2]
+    us, _ = _time_graph(read, reps, 3, inner=8 * spans)
     del buf
-    return {"bytes": span, "median_us": round(us, 2), "GBs": round(span / (us * 1e-6) / 1e9, 1),
-            "note": "miikv_stream_read, 2048x256 threads, 16 B nontemporal loads, cold "
-                    "(rotating 8 spans), one launch per event pair"}
+    return {"bytes": span, "us_per_launch": round(us, 2), "GBs": round(span / (us * 1e-6) / 1e9, 1),
+            "note": "miikv_stream_read, 2048x256 threads, 16 B nontemporal loads, cold (rotating "
+                    f"{spans} spans), {8 * spans} back-to-back launches per graph replay"}
+
+
+def decode_at(dev, ctx: int, nl: int, replays: int = 30) -> dict:
+    """Fused append + decode (config 2 shape) at context `ctx` over `nl` rotated layer
+    caches: per-replay HIP-event times (one replay = 8 rounds over the layers) give the
+    median and p10/p90 per layer-token."""
+    import ctypes
+
+    import torch
+
+    import miinfer_amd as m
+    from miinfer_amd import _lib
+    torch.manual_seed(ctx)
+    caches = []
+    for _ in range(nl):
+        c = m.KvCache.contiguous(HKV, D, ctx, device=dev)
+        for t0 in range(0, ctx, 8192):
+            n = min(8192, ctx - t0)
+            c.append(torch.randn((n, HKV, D), device=dev).half(), torch.randn((n, HKV, D), device=dev).half(),
+                     base_position=t0)
+        caches.append(c)
+    q = torch.randn((1, HQ, D), device=dev).half()
+    kn = torch.randn((1, HKV, D), device=dev).half()
+    vn = torch.randn((1, HKV, D), device=dev).half()
+    out = torch.empty((1, HQ, D), device=dev)
+    lens = torch.tensor([ctx], dtype=torch.int32, device=dev)
+    ws = m.DecodeWorkspace(caches[0], HQ, 1, ctx)
+    L = _lib.lib()
+    P = ctypes.c_void_p
+    stream = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for i in range(8 * nl):
+            st = L.miikv_decode_append_attn(caches[i % nl].view, P(kn.data_ptr()), P(vn.data_ptr()),
+                                            P(q.data_ptr()), _lib.DTYPE_F16, HQ, ctypes.c_float(1 / math.sqrt(D)),
+                                            1, P(lens.data_ptr()), None, ctx, P(out.data_ptr()), None, None,
+                                            None, P(ws.buf.data_ptr()), ws.bytes,
+                                            P(torch.cuda.current_stream().cuda_stream))
+            assert st == 0, st
+    times = []
+    with torch.cuda.stream(stream):
+        for _ in range(5):
+            g.replay()
+        for _ in range(replays):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            g.replay()
+            e1.record(stream)
+            e1.synchronize()
+            times.append(e0.elapsed_time(e1) * 1e3 / (8 * nl))
+    times.sort()
+    med = times[len(times) // 2]
+    nbytes = decode_bytes(ctx) + append_bytes()
+    del caches
+    return {"context": ctx, "layers_rotated": nl, "working_set_mb": round(nl * ctx * kv_bytes_per_token() / 1e6, 1),
+            "us_median": round(med, 3), "us_p10": round(times[len(times) // 10], 3),
+            "us_p90": round(times[(9 * len(times)) // 10], 3),
+            "GBs_median": round(nbytes / (med * 1e-6) / 1e9, 1)}
 
 
 def traffic_from_profile():
@@ -402,6 +455,8 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-sweep", action="store_true",
+                    help="config 2 at 32k only (skip the 4k/16k and hot-cache lines)")
     ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c4", "c5"],
                     help="c2 (default, the headline metric); c3 paged batched decode; c4 suffix "
                          "attention (these print their own JSON line, not the headline)")
@@ -560,6 +615,15 @@ def main() -> int:
                         "algorithmic_bytes_per_launch": decode_bytes(ctx)},
     }
     line["roofline"]["stream_read_ceiling"] = stream_read_ceiling(dev, decode_bytes(ctx))
+    # The other contexts of config 2, cold (enough rotated layers to exceed the 256 MB
+    # Infinity Cache) and hot (one layer, MALL-resident), with per-replay spread.
+    if not args.no_sweep:
+        del caches, graphs
+        torch.cuda.empty_cache()
+        line["contexts"] = {
+            "cold": [decode_at(dev, c, max(8, -(-300_000_000 // (c * kv_bytes_per_token())))) for c in (4096, 16384, 32768)],
+            "hot": [decode_at(dev, c, 1) for c in (4096, 16384, 32768)],
+        }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)
