@@ -241,6 +241,15 @@ decode_kernel(SplitArgs a) {
     for (uint32_t r = 0; r + 1 < kRing; ++r)
         if (c_begin + r < c_end_max) load_step(S[r]);
 
+    // fp16 query bits, issued before the context length so that the two loads
+    // overlap (lanes past the group read the group's last head and discard it).
+    uint4 qraw[QF32 ? 1 : NB];
+    if constexpr (!QF32) {
+        const size_t qrow = (static_cast<size_t>(b) * a.q_heads + static_cast<size_t>(h) * G + min(n, G - 1)) * D;
+#pragma unroll
+        for (uint32_t blk = 0; blk < NB; ++blk)
+            qraw[blk] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.q) + qrow + blk * 32 + g4 * 8);
+    }
     const uint32_t L = split_length(a, b);
     const uint32_t tps = kWavesPerWg * cpw * kChunk;
     const uint32_t nsplit = (L + tps - 1) / tps;
@@ -274,8 +283,7 @@ decode_kernel(SplitArgs a) {
                         qs += static_cast<float>(hi) + static_cast<float>(lo[i]);
                     }
                 } else {
-                    const uint16_t* qp = static_cast<const uint16_t*>(a.q) + qrow + blk * 32 + g4 * 8;
-                    v = __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(qp));
+                    v = __builtin_bit_cast(half8, qraw[QF32 ? 0 : blk]);
 #pragma unroll
                     for (int i = 0; i < 8; ++i) qs += static_cast<float>(v[i]);
                 }
