@@ -1,0 +1,90 @@
+// Definitions of the suffix-attention kernels (miikv_suffix.hip): launch
+// constants, argument blocks, the split-record layout and small device helpers.
+#pragma once
+#include "miikv_common.hpp"
+
+namespace miikv {
+
+#ifndef MIIKV_SUFFIX_WAVES
+#define MIIKV_SUFFIX_WAVES 8
+#endif
+constexpr uint32_t kSufWaves = MIIKV_SUFFIX_WAVES;
+constexpr uint32_t kSufRows = 32 * kSufWaves;  // query rows per workgroup
+constexpr uint32_t kSufStep = 32;              // keys per step
+constexpr float kLog2eS = 1.4426950408889634f;
+constexpr float kSlackS = 6.0f;        // lazy-rescale threshold (log2 units): p <= 64
+// Resident workgroups of suffix_kernel on the chip: 256 CUs, each holding 8 waves
+// (two per SIMD at <= 256 VGPRs) and its LDS tile buffers (4 x 32 KiB at D = 256).
+constexpr uint32_t kSufSlots = 256 * (8 / kSufWaves);
+constexpr uint32_t kSufMaxSplits = 64;
+
+// fp16 halves of one expanded step: K fragments [D/16][64 lanes][8], then
+// V fragments [D/32][2 key halves][64 lanes][8].
+__host__ __device__ constexpr uint32_t tile_halves(uint32_t D) { return 2 * D * kSufStep; }
+
+struct ExpandArgs {
+    Geo g;
+    uint32_t seq;
+    uint32_t key_count;  // host: P + T; with a device state: the capacity bound
+    const miikv_prefill_state* ps;
+    uint32_t steps;      // steps per kv head in the tile area
+    _Float16* tiles;
+};
+
+struct SuffixArgs {
+    Geo g;
+    const void* q;
+    uint32_t q_f32;
+    uint32_t q_heads;
+    uint32_t group;
+    float scale_log2;
+    uint32_t token_count;  // host upper bound
+    uint32_t base_position;
+    const miikv_prefill_state* ps;
+    uint32_t split_keys;   // keys per split (multiple of kSufStep)
+    uint32_t splits;
+    uint32_t row_blocks;   // workgroups per (kv head, split) group
+    uint32_t steps;        // steps per kv head in the tile area
+    const _Float16* tiles;
+    float* part;           // partial records when splits > 1
+    float* out;
+    const float* gate;
+    float* gated_out;
+};
+
+// Partial records of split-K, laid out so that a wave's 32 rows write one
+// contiguous block: O [split][kv head][row][D] (row = t*G + g, rows counted up
+// to the host token bound), then (m, l) pairs [split][kv head][row].
+struct SuffixCombineArgs {
+    uint32_t kv_heads;
+    uint32_t q_heads;
+    uint32_t group;
+    uint32_t token_count;  // host bound
+    uint32_t base_position;
+    const miikv_prefill_state* ps;
+    uint32_t split_keys;
+    uint32_t splits;
+    const float* part;
+    float* out;
+    const float* gate;
+    float* gated_out;
+};
+
+__host__ __device__ inline size_t part_o_floats(uint32_t splits, uint32_t kv_heads, uint32_t rows, uint32_t D) {
+    return static_cast<size_t>(splits) * kv_heads * rows * D;
+}
+
+__device__ __forceinline__ float sfx_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float16v mfma_32x32x16(half8 a, half8 b, float16v c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Wait until at most N vector-memory operations of this wave are outstanding.
+template <uint32_t N>
+__device__ __forceinline__ void wait_vmem_le() {
+    static_assert(N < 64, "vmcnt holds 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory");
+}
+
+}  // namespace miikv
