@@ -335,23 +335,27 @@ __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
     // ---- store: lane (n, hh) holds dims 32mt + 8j + 4hh + i of row n (register 4j + i).
     l_run = swap32_reduce(l_run, AddOp{});
     if (!row_ok) return;
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
     if (a.splits > 1) {
         const uint32_t rows_cap = a.token_count * G;
         const size_t pr = (static_cast<size_t>(split) * a.g.kv_heads + h) * rows_cap + row;
-        float* po = a.part + pr * D;
+        _Float16* po = static_cast<_Float16*>(a.part) + pr * D;
 #pragma unroll
         for (uint32_t mt = 0; mt < NB; ++mt)
 #pragma unroll
-            for (uint32_t j = 0; j < 4; ++j)
-                *reinterpret_cast<float4*>(po + 32 * mt + 8 * j + 4 * hh) =
-                    make_float4(O[mt][4 * j], O[mt][4 * j + 1], O[mt][4 * j + 2], O[mt][4 * j + 3]);
+            for (uint32_t j = 0; j < 4; ++j) {
+                half4 v;
+#pragma unroll
+                for (uint32_t i = 0; i < 4; ++i) v[i] = static_cast<_Float16>(O[mt][4 * j + i] * inv);
+                *reinterpret_cast<half4*>(po + 32 * mt + 8 * j + 4 * hh) = v;
+            }
         if (hh == 0) {
-            float2* ml = reinterpret_cast<float2*>(a.part + part_o_floats(a.splits, a.g.kv_heads, rows_cap, D));
+            float2* ml = reinterpret_cast<float2*>(static_cast<_Float16*>(a.part) +
+                                                   part_o_halves(a.splits, a.g.kv_heads, rows_cap, D));
             ml[pr] = make_float2(m_run, l_run);
         }
         return;
     }
-    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
     const size_t orow = (static_cast<size_t>(t_row) * a.q_heads + qh) * D;
 #pragma unroll
     for (uint32_t mt = 0; mt < NB; ++mt)
@@ -397,23 +401,25 @@ __global__ void __launch_bounds__(256) suffix_combine_kernel(SuffixCombineArgs a
     const uint32_t rows_cap = a.token_count * G;
     const uint32_t t = row / G, g = row % G;
     const uint32_t nsplit = min(a.splits, (P + t + 1 + a.split_keys - 1) / a.split_keys);
-    const float2* ml = reinterpret_cast<const float2*>(a.part + part_o_floats(a.splits, a.kv_heads, rows_cap, D));
+    const _Float16* po = static_cast<const _Float16*>(a.part);
+    const float2* ml = reinterpret_cast<const float2*>(po + part_o_halves(a.splits, a.kv_heads, rows_cap, D));
+    // Records hold O_s / l_s: each split enters with weight l_s e^{m_s - M}.
     float M = -INFINITY, Ls = 0.0f;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (uint32_t sp = 0; sp < nsplit; ++sp) {
         const size_t pr = (static_cast<size_t>(sp) * a.kv_heads + h) * rows_cap + row;
         const float2 e = ml[pr];
-        const float4 v = *reinterpret_cast<const float4*>(a.part + pr * D + 4 * d4);
+        const half4 v = *reinterpret_cast<const half4*>(po + pr * D + 4 * d4);
         const float mn = fmaxf(M, e.x);
         if (mn == -INFINITY) continue;  // no key of this row so far
         const float fo = exp2f(M - mn);
-        const float fs = exp2f(e.x - mn);
+        const float ws = e.y * exp2f(e.x - mn);
         M = mn;
-        Ls = Ls * fo + e.y * fs;
-        acc.x = acc.x * fo + v.x * fs;
-        acc.y = acc.y * fo + v.y * fs;
-        acc.z = acc.z * fo + v.z * fs;
-        acc.w = acc.w * fo + v.w * fs;
+        Ls = Ls * fo + ws;
+        acc.x = acc.x * fo + static_cast<float>(v[0]) * ws;
+        acc.y = acc.y * fo + static_cast<float>(v[1]) * ws;
+        acc.z = acc.z * fo + static_cast<float>(v[2]) * ws;
+        acc.w = acc.w * fo + static_cast<float>(v[3]) * ws;
     }
     const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
     const float4 o = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
@@ -475,7 +481,7 @@ SuffixPlan make_suffix_plan(const miikv_view* v, uint32_t q_heads, uint32_t toke
     p.splits = splits;
     p.split_keys = split_keys;
     // Records sized for `want` (>= splits): a plan for a shorter context never needs more.
-    p.part_bytes = want * v->kv_heads * tokens * G * (v->head_dim + 2) * 4;
+    p.part_bytes = want * v->kv_heads * tokens * G * part_row_bytes(v->head_dim);
     return p;
 }
 
@@ -550,7 +556,7 @@ extern "C" miikv_status miikv_suffix_attn(const miikv_view* view, const void* q,
     a.row_blocks = static_cast<uint32_t>(blocks);
     a.steps = plan.steps;
     a.tiles = tiles;
-    a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + plan.tile_bytes);
+    a.part = static_cast<uint8_t*>(workspace) + plan.tile_bytes;
     a.out = out;
     a.gate = gate;
     a.gated_out = gated_out;

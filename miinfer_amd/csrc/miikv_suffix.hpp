@@ -46,15 +46,18 @@ struct SuffixArgs {
     uint32_t row_blocks;   // workgroups per (kv head, split) group
     uint32_t steps;        // steps per kv head in the tile area
     const _Float16* tiles;
-    float* part;           // partial records when splits > 1
+    void* part;            // partial records when splits > 1
     float* out;
     const float* gate;
     float* gated_out;
 };
 
 // Partial records of split-K, laid out so that a wave's 32 rows write one
-// contiguous block: O [split][kv head][row][D] (row = t*G + g, rows counted up
-// to the host token bound), then (m, l) pairs [split][kv head][row].
+// contiguous block: O / l in fp16 [split][kv head][row][D] (row = t*G + g, rows
+// counted up to the host token bound), then (m, l) fp32 pairs [split][kv head][row].
+// The split's output is stored normalised (a convex combination of V rows, so
+// fp16 holds it to the same relative precision as the fp16 V tiles it came from),
+// which halves the record traffic of the split kernel and the combine.
 struct SuffixCombineArgs {
     uint32_t kv_heads;
     uint32_t q_heads;
@@ -64,15 +67,17 @@ struct SuffixCombineArgs {
     const miikv_prefill_state* ps;
     uint32_t split_keys;
     uint32_t splits;
-    const float* part;
+    const void* part;
     float* out;
     const float* gate;
     float* gated_out;
 };
 
-__host__ __device__ inline size_t part_o_floats(uint32_t splits, uint32_t kv_heads, uint32_t rows, uint32_t D) {
+__host__ __device__ inline size_t part_o_halves(uint32_t splits, uint32_t kv_heads, uint32_t rows, uint32_t D) {
     return static_cast<size_t>(splits) * kv_heads * rows * D;
 }
+// Bytes of one row's record in one split: D fp16 values and an (m, l) pair.
+__host__ __device__ constexpr uint32_t part_row_bytes(uint32_t D) { return 2 * D + 8; }
 
 __device__ __forceinline__ float sfx_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
