@@ -406,20 +406,31 @@ __global__ void __launch_bounds__(256) suffix_combine_kernel(SuffixCombineArgs a
     // Records hold O_s / l_s: each split enters with weight l_s e^{m_s - M}.
     float M = -INFINITY, Ls = 0.0f;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (uint32_t sp = 0; sp < nsplit; ++sp) {
-        const size_t pr = (static_cast<size_t>(sp) * a.kv_heads + h) * rows_cap + row;
-        const float2 e = ml[pr];
-        const half4 v = *reinterpret_cast<const half4*>(po + pr * D + 4 * d4);
-        const float mn = fmaxf(M, e.x);
-        if (mn == -INFINITY) continue;  // no key of this row so far
-        const float fo = exp2f(M - mn);
-        const float ws = e.y * exp2f(e.x - mn);
-        M = mn;
-        Ls = Ls * fo + ws;
-        acc.x = acc.x * fo + static_cast<float>(v[0]) * ws;
-        acc.y = acc.y * fo + static_cast<float>(v[1]) * ws;
-        acc.z = acc.z * fo + static_cast<float>(v[2]) * ws;
-        acc.w = acc.w * fo + static_cast<float>(v[3]) * ws;
+    // Batches of kU splits: every load of a batch is issued before the first merge.
+    constexpr uint32_t kU = 8;
+    for (uint32_t sp0 = 0; sp0 < nsplit; sp0 += kU) {
+        float2 e[kU];
+        half4 v[kU];
+#pragma unroll
+        for (uint32_t j = 0; j < kU; ++j) {
+            const uint32_t sp = min(sp0 + j, nsplit - 1);
+            const size_t pr = (static_cast<size_t>(sp) * a.kv_heads + h) * rows_cap + row;
+            e[j] = ml[pr];
+            v[j] = *reinterpret_cast<const half4*>(po + pr * D + 4 * d4);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kU; ++j) {
+            const float mn = fmaxf(M, e[j].x);
+            if (sp0 + j >= nsplit || mn == -INFINITY) continue;  // past the splits / no key so far
+            const float fo = exp2f(M - mn);
+            const float ws = e[j].y * exp2f(e[j].x - mn);
+            M = mn;
+            Ls = Ls * fo + ws;
+            acc.x = acc.x * fo + static_cast<float>(v[j][0]) * ws;
+            acc.y = acc.y * fo + static_cast<float>(v[j][1]) * ws;
+            acc.z = acc.z * fo + static_cast<float>(v[j][2]) * ws;
+            acc.w = acc.w * fo + static_cast<float>(v[j][3]) * ws;
+        }
     }
     const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
     const float4 o = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
