@@ -156,6 +156,88 @@ __device__ bool locate_item(const SplitArgs& a, uint32_t cpw, uint32_t id, uint3
     return true;
 }
 
+// Fused append for (sequence b, kv head h), by one 256-thread workgroup: quantise
+// the new fp16 K/V rows with the append rule (thread t < D owns dim t; block absmax
+// over 32 lanes), store them at position L-1, score the K row against the G query
+// heads, and write the token's record (m = score, l = 1, O = dequantised V row for
+// every head) at slot nsplit, after the splits, which cover the L-1 cached keys.
+// The row and query loads go out before the context length arrives.
+template <uint32_t D>
+__device__ void append_record(const SplitArgs& a, uint32_t b, uint32_t h, uint32_t cpw) {
+    constexpr uint32_t DJ = D / 64;
+    __shared__ float s_k[D];
+    __shared__ float s_v[D];
+    __shared__ float s_score[16];
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t G = a.group;
+    // Threads past D (whole waves: D is a multiple of 64) load dim D-1 and discard it.
+    const uint32_t t = min(tid, D - 1);
+    const size_t row = (static_cast<size_t>(b) * a.g.kv_heads + h) * D + t;
+    const uint16_t kraw = a.k_new[row], vraw = a.v_new[row];
+    // Wave w scores heads w, w+4, ... with dims lane + 64j; an fp16 query is read as
+    // the 32-bit word holding the value (one load form for both query types).
+    uint32_t qw[4][DJ];
+    const uint32_t* q32 = static_cast<const uint32_t*>(a.q);
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+        const uint32_t g = min(wave + 4 * j, G - 1);
+        const size_t qi = (static_cast<size_t>(b) * a.q_heads + static_cast<size_t>(h) * G + g) * D + lane;
+#pragma unroll
+        for (uint32_t jj = 0; jj < DJ; ++jj) qw[j][jj] = q32[a.q_f32 ? qi + 64 * jj : (qi + 64 * jj) / 2];
+    }
+    const uint32_t L = split_length(a, b);
+    if (L == 0) return;  // no token (the combine writes zeros)
+    const float kx = f16_bits_to_f32(kraw), vx = f16_bits_to_f32(vraw);
+    const float ka = group_reduce<32>(fabsf(kx), MaxOp{});
+    const float va = group_reduce<32>(fabsf(vx), MaxOp{});
+    const float ksc = ka > 0.0f ? ka / 127.0f : 1.0f, vsc = va > 0.0f ? va / 127.0f : 1.0f;
+    const int kq = max(-128, min(127, __float2int_rn(kx * (1.0f / ksc))));
+    const int vq = max(-128, min(127, __float2int_rn(vx * (1.0f / vsc))));
+    const uint16_t kbits = f32_to_f16_bits(ksc), vbits = f32_to_f16_bits(vsc);
+    if (tid < D) {
+        s_k[tid] = static_cast<float>(kq) * f16_bits_to_f32(kbits);
+        s_v[tid] = static_cast<float>(vq) * f16_bits_to_f32(vbits);
+        const uint32_t pos = L - 1;
+        const size_t slab = slab_of(a.g, b, pos, h);
+        const uint32_t tp = pos % a.g.page_tokens;
+        const size_t slab_bytes = static_cast<size_t>(a.g.page_tokens) * D;
+        a.g.k_codes[slab * slab_bytes + k_code_offset(tp, tid & ~7u, D) + (tid & 7u)] = static_cast<int8_t>(kq);
+        a.g.v_codes[slab * slab_bytes + v_code_offset(tp, tid, D)] = static_cast<int8_t>(vq);
+        if ((tid & 31) == 0) {
+            const size_t sidx = (slab * a.g.page_tokens + tp) * (D / 32) + tid / 32;
+            a.g.k_scales[sidx] = kbits;
+            a.g.v_scales[sidx] = vbits;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+        const uint32_t g = wave + 4 * j;
+        if (g >= G) break;  // wave-uniform
+        float dot = 0.0f;
+#pragma unroll
+        for (uint32_t jj = 0; jj < DJ; ++jj) {
+            const uint32_t w = qw[j][jj];
+            const float qx = a.q_f32 ? __uint_as_float(w) : f16_bits_to_f32(static_cast<uint16_t>((lane & 1) ? w >> 16 : w));
+            dot += qx * s_k[lane + 64 * jj];
+        }
+        dot = group_reduce<64>(dot, AddOp{});
+        if (lane == 0) s_score[g] = dot * a.scale_log2;
+    }
+    __syncthreads();
+    const uint32_t rec = record_floats(G, D);
+    float* r = a.part + ((static_cast<size_t>(b) * a.g.kv_heads + h) * (a.max_splits + 1) + split_count(L, cpw)) * rec;
+    for (uint32_t i4 = tid; i4 < G * D / 4; i4 += 256) {
+        const uint32_t d = (4 * i4) % D;
+        *reinterpret_cast<float4*>(r + 4 * i4) = make_float4(s_v[d], s_v[d + 1], s_v[d + 2], s_v[d + 3]);
+    }
+    if (tid < G) {
+        r[G * D + tid] = s_score[tid];
+        r[G * D + G + tid] = 1.0f;
+    }
+    __syncthreads();  // the caller reuses the LDS
+}
+
 template <uint32_t D, bool QF32, bool APPEND>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DecodeTuning<D, QF32>::waves_per_eu)))
 decode_kernel(SplitArgs a) {
@@ -175,6 +257,19 @@ decode_kernel(SplitArgs a) {
     // first ones dispatched and spread evenly over the XCDs and CUs; the grid's
     // tail (bounded by max_context) exits at once.
     const uint32_t cpw = launch_cpw(a);
+    // Fused append: the last batch * kv_heads workgroups of the grid each handle the
+    // new token of one (sequence, kv head).  Dispatched last, they take CU slots left
+    // free by a small grid or freed by the first split workgroups to finish, so they
+    // stay off the critical path.
+    if constexpr (APPEND) {
+        const uint32_t first = gridDim.x - a.batch * a.g.kv_heads;
+        if (blockIdx.x >= first) {
+            const uint32_t x = blockIdx.x - first;
+            const uint32_t ab = x / a.g.kv_heads;
+            if (a.count_ptr == nullptr || ab < *a.count_ptr) append_record<D>(a, ab, x % a.g.kv_heads, cpw);
+            return;
+        }
+    }
     uint32_t split, h, b;
     if (a.batch == 1) {
         b = 0;
@@ -308,8 +403,8 @@ decode_kernel(SplitArgs a) {
     const half4 ones = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
 
     // With the fused append the splits cover the L-1 cached keys; the new token
-    // (position L-1, whose cache slot may still hold older bytes: masked) is stored
-    // and merged by the combine kernel.
+    // (position L-1, whose cache slot may hold older bytes or be written meanwhile
+    // by append_record: masked) has its own record.
     const uint32_t Lc = APPEND ? L - 1 : L;
     const uint32_t nsteps = (Lc + kChunk - 1) / kChunk;
 #ifdef MIIKV_EXP_NO_LOOP
@@ -490,7 +585,7 @@ decode_kernel(SplitArgs a) {
     // Partial record of one split: [O: G*D][m: G][l: G] padded to a multiple of 4 floats,
     // so every record starts 16-byte aligned.
     const uint32_t rec = record_floats(G, D);
-    float* part = a.part + ((static_cast<size_t>(b) * geo.kv_heads + h) * a.max_splits) * rec;
+    float* part = a.part + ((static_cast<size_t>(b) * geo.kv_heads + h) * (a.max_splits + 1)) * rec;
     float* mine = part + static_cast<size_t>(split) * rec;
     if (tid < G) {
         float M = -INFINITY;
@@ -514,7 +609,6 @@ decode_kernel(SplitArgs a) {
         }
         mine[idx] = o;
     }
-
 }
 
 
@@ -561,7 +655,7 @@ Plan make_plan(const miikv_view* v, uint32_t q_heads, uint32_t batch, uint32_t m
     if (p.splits == 0) p.splits = 1;
     const uint64_t G = q_heads / v->kv_heads;
     p.counter_bytes = 0;
-    p.part_bytes = static_cast<uint64_t>(batch) * v->kv_heads * p.splits * record_floats(G, v->head_dim) * 4;
+    p.part_bytes = static_cast<uint64_t>(batch) * v->kv_heads * (p.splits + 1) * record_floats(G, v->head_dim) * 4;
     p.part_bytes = (p.part_bytes + 255) / 256 * 256;
     return p;
 }
@@ -654,8 +748,10 @@ static miikv_status decode_impl(const miikv_view* view, const uint16_t* k_new, c
     const size_t lds = (32 * kWavesPerWg + kWavesPerWg * G * view->head_dim) * sizeof(float) +
                        kWavesPerWg * 2 * kChunk * (view->head_dim / 32) * sizeof(uint16_t);
     if (lds > 64 * 1024) return MIIKV_EUNSUPPORTED;
-    // One workgroup per possible (sequence, kv head, split) work item.
-    const uint64_t wgs = static_cast<uint64_t>(p.splits) * view->kv_heads * batch;
+    // One workgroup per possible (sequence, kv head, split) work item, plus one per
+    // (sequence, kv head) for the new token of the fused append.
+    const uint64_t wgs = static_cast<uint64_t>(p.splits) * view->kv_heads * batch +
+                         (k_new != nullptr ? static_cast<uint64_t>(view->kv_heads) * batch : 0);
     if (wgs > 0x7fffffffu) return MIIKV_EINVAL;
     a.batch = batch;
     a.slots = p.adaptive ? resident_workgroups(view->head_dim, q_dtype == MIIKV_DTYPE_F32) : 0u;

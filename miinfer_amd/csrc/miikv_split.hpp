@@ -31,14 +31,15 @@ struct SplitArgs {
     // batch > 1: resident workgroups of the split kernel; the steps per wave are
     // then chosen on the device from the lengths (at least cpw), 0: always cpw
     uint32_t slots;
-    float* part;          // [batch][kv_heads][max_splits][group*(D+2)]
+    float* part;          // [batch][kv_heads][max_splits + 1][record]: the splits, then
+                          // with the fused append the new token's record at slot nsplit
     float* out;
     const float* gate;
     float* gated_out;
     uint8_t* gated_q8_1;  // nullable: Q8_1 blocks [batch][q_heads][D/32] of gated_out
     const uint16_t* k_new;  // fused append: fp16 rows [batch][kv_heads][D] stored at position L-1
     const uint16_t* v_new;
-    uint32_t q_f32;         // q dtype (the combine scores the appended token)
+    uint32_t q_f32;         // q dtype (scoring the appended token)
 };
 
 __device__ __forceinline__ float exp2_safe(float x) { return exp2f(x); }  // exp2(-inf) == 0
@@ -81,16 +82,20 @@ __device__ uint32_t launch_cpw(const SplitArgs& a) {
     return static_cast<uint32_t>(cpw < a.cpw ? a.cpw : (cpw > 64 ? 64 : cpw));
 }
 
+// Split count of sequence b at `cpw` steps per wave (0 when L == 0).
+__device__ __forceinline__ uint32_t split_count(uint32_t L, uint32_t cpw) {
+    const uint32_t tps = kWavesPerWg * cpw * kChunk;
+    return (L + tps - 1) / tps;
+}
+
 // Cross-split combine.  Workgroup (sequence * kv_heads + head, element block of 64)
 // reads the partial records of every split of that (sequence, kv head): thread
-// (e4 = tid & 15, sg = tid >> 4) folds splits sg, sg+16, ... for 4 consecutive
+// (e4 = tid & 15, sg = tid >> 4) folds records sg, sg+16, ... for 4 consecutive
 // elements with its own running max, so its loads are independent; the 16 split
 // groups are merged in a fixed order through LDS (deterministic result).
-// Fused append (APPEND): the splits covered the L-1 cached keys; this kernel
-// quantises the new row of (b, h) with the append rule (thread t < D owns dim t;
-// block absmax over 32 lanes), stores it at position L-1 (workgroup y == 0),
-// scores it against the query head of this workgroup's elements, and merges it
-// as one more record (m = score, l = 1, O = dequantised V row).
+// Fused append (APPEND): the splits covered the L-1 cached keys and decode_kernel
+// wrote the new token's record (m = score, l = 1, O = its dequantised V row) at
+// slot nsplit, merged here as one more record.
 template <uint32_t D, bool APPEND>
 __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
     const uint32_t bh = blockIdx.x;
@@ -100,20 +105,6 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
     const uint32_t GD = G * D;
     const uint32_t e0 = blockIdx.y * 64;
     if (e0 >= GD) return;
-    // fused append: the new rows (dim tid), issued before the records as raw bits and
-    // converted after them, so no wait on these loads sits ahead of the record loads.
-    // Threads past D load dim D-1 and discard it.
-    uint32_t kraw = 0, vraw = 0, qraw = 0;
-    const uint32_t hq0 = e0 / D;  // query head (within the group) of this workgroup's elements
-    if constexpr (APPEND) {
-        const uint32_t t = min(threadIdx.x, D - 1);
-        const size_t row = (static_cast<size_t>(b) * a.g.kv_heads + h) * D + t;
-        kraw = a.k_new[row];
-        vraw = a.v_new[row];
-        const size_t qi = (static_cast<size_t>(b) * a.q_heads + static_cast<size_t>(h) * G + hq0) * D + t;
-        if (a.q_f32) qraw = static_cast<const uint32_t*>(a.q)[qi];
-        else qraw = static_cast<const uint16_t*>(a.q)[qi];
-    }
     const uint32_t tid = threadIdx.x;
     const uint32_t e4 = tid & 15;
     const uint32_t sg = tid >> 4;
@@ -123,10 +114,11 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
     const size_t out_row0 = (static_cast<size_t>(b) * a.q_heads + static_cast<size_t>(h) * G) * D;
 
     const uint32_t rec = record_floats(G, D);
-    const float* part = a.part + (static_cast<size_t>(bh) * a.max_splits) * rec;
+    const uint32_t slots = a.max_splits + 1;
+    const float* part = a.part + (static_cast<size_t>(bh) * slots) * rec;
 
     // The first kSpec records of this thread are fetched before the context length
-    // (and with it the split count) arrives; records past the count are ignored.
+    // (and with it the record count) arrives; records past the count are ignored.
     constexpr uint32_t kSpec = 4;
     float ms[kSpec], ls[kSpec];
     float4 vv[kSpec];
@@ -136,7 +128,7 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
         ms[j] = -INFINITY;
         ls[j] = 0.0f;
         vv[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (sp < a.max_splits) {
+        if (sp < slots) {
             const float* r = part + static_cast<size_t>(sp) * rec;
             ms[j] = r[GD + hn];
             ls[j] = r[GD + G + hn];
@@ -145,9 +137,8 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
     }
     const uint32_t cpw = launch_cpw(a);
     if (a.count_ptr != nullptr && b >= *a.count_ptr) return;
-    uint32_t L = split_length(a, b);
-    const uint32_t tps = kWavesPerWg * cpw * kChunk;
-    const uint32_t nsplit = (L + tps - 1) / tps;
+    const uint32_t L = split_length(a, b);
+    const uint32_t nrec = split_count(L, cpw) + (APPEND && L > 0 ? 1u : 0u);
 
     float mloc = -INFINITY;
     float lsum = 0.0f;
@@ -166,8 +157,8 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
     };
 #pragma unroll
     for (uint32_t j = 0; j < kSpec; ++j)
-        if (sg + 16 * j < nsplit) merge(ms[j], ls[j], vv[j]);
-    for (uint32_t sp = sg + 16 * kSpec; sp < nsplit; sp += 16) {
+        if (sg + 16 * j < nrec) merge(ms[j], ls[j], vv[j]);
+    for (uint32_t sp = sg + 16 * kSpec; sp < nrec; sp += 16) {
         const float* r = part + static_cast<size_t>(sp) * rec;
         merge(r[GD + hn], r[GD + G + hn],
               active ? *reinterpret_cast<const float4*>(r + e) : make_float4(0.f, 0.f, 0.f, 0.f));
@@ -175,51 +166,10 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
     __shared__ float4 s_acc[16][16];
     __shared__ float s_gm[16][16];
     __shared__ float s_gl[16][16];
-    __shared__ float s_vnew[APPEND ? D : 1];
-    __shared__ float s_dot[4];
     s_acc[sg][e4] = acc;
     s_gm[sg][e4] = mloc;
     s_gl[sg][e4] = lsum;
-    float m_new = -INFINITY;
-    if constexpr (APPEND) {
-        const bool row_lane = threadIdx.x < D;
-        const float kx = row_lane ? f16_bits_to_f32(static_cast<uint16_t>(kraw)) : 0.0f;
-        const float vx = row_lane ? f16_bits_to_f32(static_cast<uint16_t>(vraw)) : 0.0f;
-        const float qx = !row_lane ? 0.0f
-                         : a.q_f32 ? __uint_as_float(qraw) : f16_bits_to_f32(static_cast<uint16_t>(qraw));
-        // Same rule as the append kernel: scale = amax/127 (1 for a zero block),
-        // codes round-to-nearest-even, clamped; the score uses code * fp16(scale).
-        const uint32_t t = threadIdx.x;
-        float ka = fabsf(kx), va = fabsf(vx);
-        ka = group_reduce<32>(ka, MaxOp{});
-        va = group_reduce<32>(va, MaxOp{});
-        const float ksc = ka > 0.0f ? ka / 127.0f : 1.0f, vsc = va > 0.0f ? va / 127.0f : 1.0f;
-        const int kq = max(-128, min(127, __float2int_rn(kx * (1.0f / ksc))));
-        const int vq = max(-128, min(127, __float2int_rn(vx * (1.0f / vsc))));
-        const uint16_t kbits = f32_to_f16_bits(ksc), vbits = f32_to_f16_bits(vsc);
-        float part = t < D ? qx * (static_cast<float>(kq) * f16_bits_to_f32(kbits)) : 0.0f;
-        part = group_reduce<64>(part, AddOp{});
-        if ((t & 63) == 0) s_dot[t >> 6] = part;
-        if (t < D) s_vnew[t] = static_cast<float>(vq) * f16_bits_to_f32(vbits);
-        const uint32_t L = split_length(a, b);
-        if (blockIdx.y == 0 && t < D && L > 0) {
-            const uint32_t pos = L - 1;
-            const size_t slab = slab_of(a.g, b, pos, h);
-            const uint32_t tp = pos % a.g.page_tokens;
-            const size_t slab_bytes = static_cast<size_t>(a.g.page_tokens) * D;
-            a.g.k_codes[slab * slab_bytes + k_code_offset(tp, t & ~7u, D) + (t & 7u)] = static_cast<int8_t>(kq);
-            a.g.v_codes[slab * slab_bytes + v_code_offset(tp, t, D)] = static_cast<int8_t>(vq);
-            if ((t & 31) == 0) {
-                const size_t sidx = (slab * a.g.page_tokens + tp) * (D / 32) + t / 32;
-                a.g.k_scales[sidx] = kbits;
-                a.g.v_scales[sidx] = vbits;
-            }
-        }
-        __syncthreads();
-        if (L > 0) m_new = (s_dot[0] + s_dot[1] + s_dot[2] + s_dot[3]) * a.scale_log2;
-    } else {
-        __syncthreads();
-    }
+    __syncthreads();
     if (sg != 0 || !active) return;
     float M = -INFINITY;
 #pragma unroll
@@ -237,19 +187,6 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
         o.z += f * v.z;
         o.w += f * v.w;
         Ls += f * s_gl[g][e4];
-    }
-    if constexpr (APPEND) {
-        if (m_new != -INFINITY) {
-            const float Mn = fmaxf(M, m_new);
-            const float fo = M == -INFINITY ? 0.0f : exp2_safe(M - Mn);
-            const float fn = exp2_safe(m_new - Mn);
-            const uint32_t d = e % D;
-            o.x = o.x * fo + s_vnew[d] * fn;
-            o.y = o.y * fo + s_vnew[d + 1] * fn;
-            o.z = o.z * fo + s_vnew[d + 2] * fn;
-            o.w = o.w * fo + s_vnew[d + 3] * fn;
-            Ls = Ls * fo + fn;
-        }
     }
     // out = acc / L, 0 when L == 0 (qwen3_primitives.hip:2349); gated = out * sigmoid(gate).
     const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
