@@ -137,13 +137,14 @@ def test_workspace_bytes_scales_with_geometry():
 def test_suffix_workspace_bytes_plan():
     """Suffix workspace: the expanded fp16 tiles of every 32-key step of the capacity
     (2*D*32 halves per step and kv head) plus, when the key range is split, one record
-    (G*D + pad(2G) floats) per token, kv head and split."""
+    per query row (token x head of the group), kv head and split: the row's normalised
+    output in fp16 (2*D bytes) and its (m, l) pair in fp32 (8 bytes)."""
     L = _lib()
     lib = L.lib()
     v = _view(page_tokens=8704, kv_heads=4, head_dim=256)
     tiles = 4 * (8704 // 32) * 2 * 256 * 32 * 2
     ws = lib.miikv_suffix_workspace_bytes(ctypes.byref(v), 24, 512)
-    rec = (6 * 256 + 12) * 4
+    rec = 6 * (2 * 256 + 8)  # G = 6 rows per token
     assert ws > tiles and (ws - tiles) % (512 * 4 * rec) == 0
     assert 2 <= (ws - tiles) // (512 * 4 * rec) <= 64
     short = _view(page_tokens=256, kv_heads=4, head_dim=256)
