@@ -116,3 +116,46 @@ def test_fused_append_decode_paged_batched(gpu, hq, hk, d):
         assert np.array_equal(ks[:, n - 1].view(np.uint16), refs[s][1][:, n - 1])
         assert np.array_equal(vc[:, n - 1], refs[s][2][:, n - 1])
         assert np.array_equal(vs[:, n - 1].view(np.uint16), refs[s][3][:, n - 1])
+
+
+def test_fused_append_q8_1_epilogue_and_empty_sequence(gpu):
+    """Fused append with the Q8_1 output blocks of the gated output, in a batch whose
+    middle sequence is empty (L = 0): its outputs are zeros and no row is stored."""
+    import miinfer_amd as m
+    rng = np.random.default_rng(11)
+    hq, hk, d, pt = 24, 4, 256, 256
+    lens = [700, 0, 300]
+    table = np.array([[0, 1, 2], [3, 4, 5], [6, 7, 8]], np.int32)
+    cache = m.KvCache.paged_cache(hk, d, 9, _dev(table, gpu), page_tokens=pt)
+    before = _canon(cache, 1, 1)
+    refs, knew, vnew = [], [], []
+    for s, n in enumerate(lens):
+        k = randn_f16(rng, (max(n, 1), hk, d))
+        v = randn_f16(rng, (max(n, 1), hk, d))
+        if n > 1:
+            cache.append(_dev(k[:-1], gpu), _dev(v[:-1], gpu), base_position=0, seq=s)
+        knew.append(k[-1])
+        vnew.append(v[-1])
+        kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+        vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+        refs.append((kc, ks, vc, vs))
+    q = randn_f16(rng, (len(lens), hq, d))
+    gate = rng.standard_normal((len(lens), hq, d)).astype(np.float32)
+    blocks = torch.zeros((len(lens) * hq * d // 32, 36), dtype=torch.uint8, device=gpu)
+    out, gated = m.decode_attention(cache, _dev(q, gpu), lengths=_dev(np.array(lens, np.int32), gpu),
+                                    max_context=3 * pt, gate=_dev(gate, gpu),
+                                    out=torch.empty((len(lens), hq, d), device=gpu), gated_q8_1=blocks,
+                                    k_new=_dev(np.stack(knew), gpu), v_new=_dev(np.stack(vnew), gpu))
+    torch.cuda.synchronize()
+    out, gated = out.cpu().numpy(), gated.cpu().numpy()
+    for s, n in enumerate(lens):
+        if n == 0:
+            assert not out[s].any() and not gated[s].any()
+            continue
+        expect = oracle.attention_q8(q[s].astype(np.float32), *refs[s], n, hq, 1 / math.sqrt(d))
+        assert_attention_close(out[s], expect, f"seq {s} L={n}")
+    # Q8_1 blocks are the reference rule applied to the kernel's own gated output
+    assert np.array_equal(blocks.cpu().numpy(), oracle.q8_1_blocks(gated.reshape(-1)))
+    # the empty sequence's first slot keeps its bytes
+    for a, b in zip(_canon(cache, 1, 1), before):
+        assert np.array_equal(a, b)
