@@ -204,3 +204,59 @@ def test_decode_batch_device_chosen_split(gpu):
         (kc, ks), (vc, vs) = refs[s]
         expect = oracle.attention_q8(q[s].astype(np.float32), kc, ks, vc, vs, n, hq, 1 / math.sqrt(d))
         assert_attention_close(out[s], expect, f"seq {s} L={n}")
+
+
+def test_decode_config3_full_size_fused_append(gpu):
+    """Config 3 at full size, as bench.py runs it: 16 sequences of 24q/4kv/D256 with
+    context lengths uniform in [1024, 65536] (seed 3), 256-token pages behind a random
+    permutation table, one appended row per sequence in the same launch pair.  Every
+    sequence's new row is checked byte for byte; the attention of four sequences (the
+    longest and shortest among them) against the oracle."""
+    import miinfer_amd as m
+    hq, hk, d, pt, batch = 24, 4, 256, 256, 16
+    rng = np.random.default_rng(3)
+    lens = rng.integers(1024, 65536 + 1, size=batch)
+    pages = [(int(n) + pt) // pt for n in lens]
+    stride = max(pages)
+    perm = rng.permutation(sum(pages)).astype(np.int32)
+    table = np.zeros((batch, stride), np.int32)
+    o = 0
+    for b, p in enumerate(pages):
+        table[b, :p] = perm[o:o + p]
+        o += p
+    cache = m.KvCache.paged_cache(hk, d, sum(pages), _dev(table, gpu), page_tokens=pt)
+    gen = torch.Generator(device=gpu).manual_seed(0)
+    kv = []
+    for b, n in enumerate(lens):
+        k = torch.randn((int(n), hk, d), device=gpu, generator=gen).half()
+        v = torch.randn((int(n), hk, d), device=gpu, generator=gen).half()
+        cache.append(k[:-1], v[:-1], base_position=0, seq=b)
+        kv.append((k, v))
+    q = randn_f16(rng, (batch, hq, d))
+    knew = torch.stack([k[-1] for k, _ in kv]).contiguous()
+    vnew = torch.stack([v[-1] for _, v in kv]).contiguous()
+    out, _ = m.decode_attention(cache, _dev(q, gpu), lengths=_dev(lens.astype(np.int32), gpu),
+                                max_context=stride * pt, k_new=knew, v_new=vnew)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    order = np.argsort(lens)
+    for b in range(batch):
+        n = int(lens[b])
+        k, v = (t.cpu().numpy() for t in kv[b])
+        kc, ks, vc, vs = _canon_tail(cache, b, n)
+        ekc, eks = oracle.quantize_rows(k[-1:].transpose(1, 0, 2))
+        evc, evs = oracle.quantize_rows(v[-1:].transpose(1, 0, 2))
+        assert np.array_equal(kc, ekc) and np.array_equal(ks.view(np.uint16), eks)
+        assert np.array_equal(vc, evc) and np.array_equal(vs.view(np.uint16), evs)
+        if b in (order[0], order[1], order[-2], order[-1]):
+            rk = oracle.quantize_rows(k.transpose(1, 0, 2))
+            rv = oracle.quantize_rows(v.transpose(1, 0, 2))
+            expect = oracle.attention_q8(q[b].astype(np.float32), *rk, *rv, n, hq, 1 / math.sqrt(d))
+            assert_attention_close(out[b], expect, f"seq {b} L={n}")
+
+
+def _canon_tail(cache, seq, n):
+    """The last row (position n-1) of sequence `seq` in canonical form."""
+    out = cache.export_canonical(seq, n - 1, 1)
+    torch.cuda.synchronize()
+    return [t.cpu().numpy() for t in out]
