@@ -248,6 +248,19 @@ miikv_status miikv_suffix_attn(const miikv_view* view, const void* q, uint32_t q
                                const float* gate, float* gated_out, void* workspace,
                                uint64_t workspace_bytes, void* stream);
 
+/* Fused append + suffix attention: quantises the suffix's own fp16 K/V rows
+ * (k_new, v_new device [token_count][kv_heads][head_dim]) with the append rule,
+ * stores them at positions base_position + t (or the prefill state's), and
+ * attends as miikv_suffix_attn, in one pass over the context instead of the
+ * reference's store launch followed by attention (attention_layer.cpp:297-343).
+ * Cache bytes and results equal miikv_append_f16 followed by miikv_suffix_attn. */
+miikv_status miikv_suffix_append_attn(const miikv_view* view, const uint16_t* k_new, const uint16_t* v_new,
+                                      const void* q, uint32_t q_dtype, uint32_t q_heads, float scale,
+                                      uint32_t token_count, uint32_t base_position, uint32_t seq,
+                                      const miikv_prefill_state* prefill_state, float* out,
+                                      const float* gate, float* gated_out, void* workspace,
+                                      uint64_t workspace_bytes, void* stream);
+
 /* ---- export / import ----------------------------------------------------- */
 
 /* Copy tokens [t0, t0+count) of sequence `seq` out of the tiled cache into

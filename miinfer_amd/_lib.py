@@ -114,6 +114,8 @@ SIGNATURES = {
                                            ctypes.c_size_t, ctypes.c_char_p, ctypes.c_size_t, _P]),
     "miikv_suffix_attn": (ctypes.c_int, [_VP, _P, _U32, _U32, ctypes.c_float, _U32, _U32, _U32, _P,
                                           _P, _P, _P, _P, _U64, _P]),
+    "miikv_suffix_append_attn": (ctypes.c_int, [_VP, _P, _P, _P, _U32, _U32, ctypes.c_float, _U32, _U32, _U32,
+                                                 _P, _P, _P, _P, _P, _U64, _P]),
 }
 
 _lib = None

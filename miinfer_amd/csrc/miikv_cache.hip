@@ -42,17 +42,6 @@ struct AppendIn {
     float epsilon;
 };
 
-__device__ __forceinline__ void load16_f16(const uint16_t* p, float (&x)[16]) {
-    const uint4 a = *reinterpret_cast<const uint4*>(p);
-    const uint4 b = *reinterpret_cast<const uint4*>(p + 8);
-    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        x[2 * i] = f16_bits_to_f32(static_cast<uint16_t>(w[i] & 0xffffu));
-        x[2 * i + 1] = f16_bits_to_f32(static_cast<uint16_t>(w[i] >> 16));
-    }
-}
-
 __device__ __forceinline__ void load16_f32(const float* p, float (&x)[16]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {

@@ -167,6 +167,20 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
     return __half2float(__ushort_as_half(b));
 }
 
+// 16 consecutive fp16 values (two 16-byte words) -> fp32.
+__device__ __forceinline__ void unpack16_f16(const uint4 (&r)[2], float (&x)[16]) {
+    const uint32_t w[8] = {r[0].x, r[0].y, r[0].z, r[0].w, r[1].x, r[1].y, r[1].z, r[1].w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        x[2 * i] = f16_bits_to_f32(static_cast<uint16_t>(w[i] & 0xffffu));
+        x[2 * i + 1] = f16_bits_to_f32(static_cast<uint16_t>(w[i] >> 16));
+    }
+}
+__device__ __forceinline__ void load16_f16(const uint16_t* p, float (&x)[16]) {
+    const uint4 r[2] = {*reinterpret_cast<const uint4*>(p), *reinterpret_cast<const uint4*>(p + 8)};
+    unpack16_f16(r, x);
+}
+
 // Four signed int8 codes (one dword) -> four exact fp16 values, two per dword.
 // u = c ^ 0x80 = c + 128; the fp16 with bits 0x6400|u equals 1024 + u, so
 // subtracting 1152 yields c exactly.

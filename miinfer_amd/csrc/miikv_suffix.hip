@@ -57,14 +57,22 @@ __device__ __forceinline__ uint32_t context_keys(uint32_t host_count, const miik
 
 // One 32-key step of kv head blockIdx.y: 256 threads; keys at or past the context
 // end become 0 (their codes may never have been written).
-template <uint32_t D>
+// Fused append (APPEND, a.k_new set): a step holding any of the suffix's own keys
+// [P, P + T) first assembles its 32-token group in LDS -- the cached codes and
+// scales of the other keys, the suffix rows quantised with the append rule (the
+// bytes miikv_append_f16 stores) -- writes the whole group back to the cache with
+// 16-byte stores and expands it from LDS.
+template <uint32_t D, bool APPEND>
 __global__ void __launch_bounds__(256) expand_kernel(ExpandArgs a) {
     constexpr uint32_t NB = D / 32;
     constexpr uint32_t NKF = D / 16;       // K fragments per step
     constexpr uint32_t PER = D / 64;       // fragment lanes per thread, per operand
     __shared__ __align__(16) _Float16 s_vs[NB * kSufStep];  // [block][key]
+    __shared__ __align__(16) uint8_t s_grp[APPEND ? 2 * kSufStep * D + 2 * kSufStep * NB * 2 : 16];
     const Geo& geo = a.g;
-    const uint32_t step = blockIdx.x;
+    // Last step first: with the fused append the suffix's steps, which carry the
+    // longer quantise-and-store chain, are dispatched ahead of the rest.
+    const uint32_t step = gridDim.x - 1 - blockIdx.x;
     const uint32_t h = blockIdx.y;
     const uint32_t tid = threadIdx.x;
     const uint32_t nkeys = context_keys(a.key_count, a.ps);
@@ -76,9 +84,92 @@ __global__ void __launch_bounds__(256) expand_kernel(ExpandArgs a) {
     const size_t cb = slab * static_cast<size_t>(geo.page_tokens) * D + static_cast<size_t>(tp0) * D;
     const int8_t* kb = geo.k_codes + cb;
     const int8_t* vb = geo.v_codes + cb;
+    const uint16_t* ksc = geo.k_scales + sc0;
+    const uint16_t* vsc = geo.v_scales + sc0;
+    if constexpr (APPEND) {
+        const uint32_t P = a.ps ? a.ps->base_position : a.base_position;
+        const uint32_t T = a.ps ? min(a.token_count, a.ps->token_count) : a.token_count;
+        if (tok0 + kSufStep > P && tok0 < P + T) {
+            // The suffix rows of this step, thread (key tl, 16-dim chunk q16) per item,
+            // loaded first so that they travel with the cached group below.
+            constexpr uint32_t ITEMS = kSufStep * (D / 16) / 256;
+            uint4 rk[ITEMS][2], rv[ITEMS][2];
+#pragma unroll
+            for (uint32_t it = 0; it < ITEMS; ++it) {
+                const uint32_t w = tid + 256 * it, tl = w / (D / 16), q16 = w % (D / 16);
+                const uint32_t key = tok0 + tl;
+                const uint32_t t = key >= P && key < P + T ? key - P : 0;
+                const size_t src = (static_cast<size_t>(t) * geo.kv_heads + h) * D + q16 * 16;
+                rk[it][0] = *reinterpret_cast<const uint4*>(a.k_new + src);
+                rk[it][1] = *reinterpret_cast<const uint4*>(a.k_new + src + 8);
+                rv[it][0] = *reinterpret_cast<const uint4*>(a.v_new + src);
+                rv[it][1] = *reinterpret_cast<const uint4*>(a.v_new + src + 8);
+            }
+            // Group in LDS: [K codes 32*D][V codes 32*D][K scales 32*NB][V scales 32*NB]
+            // in the cache's slab order.  Copy the cached group (its keys outside the
+            // suffix keep their bytes), then overwrite the suffix keys.
+            uint4* g16 = reinterpret_cast<uint4*>(s_grp);
+            constexpr uint32_t CK = kSufStep * D / 16, CS = kSufStep * NB * 2 / 16;
+            for (uint32_t c = tid; c < 2 * CK + 2 * CS; c += 256) {
+                const uint4* src = c < CK ? reinterpret_cast<const uint4*>(kb) + c
+                                 : c < 2 * CK ? reinterpret_cast<const uint4*>(vb) + (c - CK)
+                                 : c < 2 * CK + CS ? reinterpret_cast<const uint4*>(ksc) + (c - 2 * CK)
+                                                   : reinterpret_cast<const uint4*>(vsc) + (c - 2 * CK - CS);
+                g16[c] = *src;
+            }
+            __syncthreads();
+            uint8_t* s_k = s_grp;
+            uint8_t* s_v = s_grp + kSufStep * D;
+            uint16_t* s_ks = reinterpret_cast<uint16_t*>(s_grp + 2 * kSufStep * D);
+            uint16_t* s_vsc = s_ks + kSufStep * NB;
+            // partner lanes q16 ^ 1 hold the two halves of a 32-value block
+#pragma unroll
+            for (uint32_t it = 0; it < ITEMS; ++it) {
+                const uint32_t w = tid + 256 * it, tl = w / (D / 16), q16 = w % (D / 16);
+                const uint32_t key = tok0 + tl;
+                const bool mine = key >= P && key < P + T;
+                float xk[16], xv[16];
+                unpack16_f16(rk[it], xk);
+                unpack16_f16(rv[it], xv);
+                int8_t qk[16], qv[16];
+                float sk, sv;
+                quantize16(xk, qk, sk);  // both lanes of a pair reach the shuffles
+                quantize16(xv, qv, sv);
+                if (!mine) continue;
+                const uint32_t d0 = q16 * 16;
+                uint32_t packed[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    packed[u] = static_cast<uint32_t>(static_cast<uint8_t>(qk[4 * u])) |
+                                (static_cast<uint32_t>(static_cast<uint8_t>(qk[4 * u + 1])) << 8) |
+                                (static_cast<uint32_t>(static_cast<uint8_t>(qk[4 * u + 2])) << 16) |
+                                (static_cast<uint32_t>(static_cast<uint8_t>(qk[4 * u + 3])) << 24);
+                *reinterpret_cast<uint2*>(s_k + k_code_offset(tl, d0, D)) = make_uint2(packed[0], packed[1]);
+                *reinterpret_cast<uint2*>(s_k + k_code_offset(tl, d0 + 8, D)) = make_uint2(packed[2], packed[3]);
+#pragma unroll
+                for (int u = 0; u < 16; ++u) s_v[v_code_offset(tl, d0 + u, D)] = static_cast<uint8_t>(qv[u]);
+                if ((q16 & 1) == 0) {
+                    s_ks[tl * NB + d0 / 32] = f32_to_f16_bits(sk);
+                    s_vsc[tl * NB + d0 / 32] = f32_to_f16_bits(sv);
+                }
+            }
+            __syncthreads();
+            for (uint32_t c = tid; c < 2 * CK + 2 * CS; c += 256) {
+                uint4* dst = c < CK ? reinterpret_cast<uint4*>(geo.k_codes + cb) + c
+                           : c < 2 * CK ? reinterpret_cast<uint4*>(geo.v_codes + cb) + (c - CK)
+                           : c < 2 * CK + CS ? reinterpret_cast<uint4*>(geo.k_scales + sc0) + (c - 2 * CK)
+                                             : reinterpret_cast<uint4*>(geo.v_scales + sc0) + (c - 2 * CK - CS);
+                *dst = g16[c];
+            }
+            kb = reinterpret_cast<const int8_t*>(s_k);
+            vb = reinterpret_cast<const int8_t*>(s_v);
+            ksc = s_ks;
+            vsc = s_vsc;
+        }
+    }
     if (tid < kSufStep * NB) {
         const uint32_t key = tid / NB, blk = tid % NB;
-        s_vs[blk * kSufStep + key] = tok0 + key < nkeys ? clamp_scale(geo.v_scales[sc0 + tid]) : (_Float16)0.0f;
+        s_vs[blk * kSufStep + key] = tok0 + key < nkeys ? clamp_scale(vsc[tid]) : (_Float16)0.0f;
     }
     __syncthreads();
     _Float16* out = a.tiles + (static_cast<size_t>(h) * a.steps + step) * tile_halves(D);
@@ -92,7 +183,7 @@ __global__ void __launch_bounds__(256) expand_kernel(ExpandArgs a) {
         const uint32_t off = (n / 16) * 16 * D + (c / 4) * 1024 + (2 * (c % 2) + hh) * 256 + (n % 16) * 16 +
                              ((c % 4) / 2) * 8;
         const uint2 w = *reinterpret_cast<const uint2*>(kb + off);
-        const _Float16 sc = tok0 + n < nkeys ? clamp_scale(geo.k_scales[sc0 + n * NB + c / 2]) : (_Float16)0.0f;
+        const _Float16 sc = tok0 + n < nkeys ? clamp_scale(ksc[n * NB + c / 2]) : (_Float16)0.0f;
         *reinterpret_cast<half8*>(out + 8 * fl) = codes8_to_half8(w.x, w.y) * (half8)sc;
     }
     // V fragment f = 2mt + kc, lane (n, hh): dim 32mt + n, positions 4*b3 + i hold
@@ -507,11 +598,11 @@ extern "C" uint64_t miikv_suffix_workspace_bytes(const miikv_view* view, uint32_
     return make_suffix_plan(view, q_heads, token_count, view_seq_capacity(view), true).total();
 }
 
-extern "C" miikv_status miikv_suffix_attn(const miikv_view* view, const void* q, uint32_t q_dtype, uint32_t q_heads,
-                                          float scale, uint32_t token_count, uint32_t base_position, uint32_t seq,
-                                          const miikv_prefill_state* prefill_state, float* out, const float* gate,
-                                          float* gated_out, void* workspace, uint64_t workspace_bytes,
-                                          void* stream) {
+static miikv_status suffix_impl(const miikv_view* view, const uint16_t* k_new, const uint16_t* v_new, const void* q,
+                                uint32_t q_dtype, uint32_t q_heads, float scale, uint32_t token_count,
+                                uint32_t base_position, uint32_t seq, const miikv_prefill_state* prefill_state,
+                                float* out, const float* gate, float* gated_out, void* workspace,
+                                uint64_t workspace_bytes, void* stream) {
     const int st = validate_view(view);
     if (st != MIIKV_OK) return st;
     if (q == nullptr || q_heads == 0 || q_heads % view->kv_heads != 0 || !std::isfinite(scale)) return MIIKV_EINVAL;
@@ -548,9 +639,18 @@ extern "C" miikv_status miikv_suffix_attn(const miikv_view* view, const void* q,
     e.ps = prefill_state;
     e.steps = plan.steps;
     e.tiles = tiles;
+    e.k_new = k_new;
+    e.v_new = v_new;
+    e.token_count = token_count;
+    e.base_position = base_position;
     const dim3 egrid(plan.steps, view->kv_heads);
-    if (view->head_dim == 128) hipLaunchKernelGGL(expand_kernel<128>, egrid, dim3(256), 0, s, e);
-    else hipLaunchKernelGGL(expand_kernel<256>, egrid, dim3(256), 0, s, e);
+    if (k_new != nullptr) {
+        if (view->head_dim == 128) hipLaunchKernelGGL((expand_kernel<128, true>), egrid, dim3(256), 0, s, e);
+        else hipLaunchKernelGGL((expand_kernel<256, true>), egrid, dim3(256), 0, s, e);
+    } else {
+        if (view->head_dim == 128) hipLaunchKernelGGL((expand_kernel<128, false>), egrid, dim3(256), 0, s, e);
+        else hipLaunchKernelGGL((expand_kernel<256, false>), egrid, dim3(256), 0, s, e);
+    }
 
     SuffixArgs a;
     a.g = e.g;
@@ -597,4 +697,24 @@ extern "C" miikv_status miikv_suffix_attn(const miikv_view* view, const void* q,
         else hipLaunchKernelGGL(suffix_combine_kernel<256>, cgrid, dim3(256), 0, s, c);
     }
     return hip_status(hipGetLastError());
+}
+
+extern "C" miikv_status miikv_suffix_attn(const miikv_view* view, const void* q, uint32_t q_dtype, uint32_t q_heads,
+                                          float scale, uint32_t token_count, uint32_t base_position, uint32_t seq,
+                                          const miikv_prefill_state* prefill_state, float* out, const float* gate,
+                                          float* gated_out, void* workspace, uint64_t workspace_bytes,
+                                          void* stream) {
+    return suffix_impl(view, nullptr, nullptr, q, q_dtype, q_heads, scale, token_count, base_position, seq,
+                       prefill_state, out, gate, gated_out, workspace, workspace_bytes, stream);
+}
+
+extern "C" miikv_status miikv_suffix_append_attn(const miikv_view* view, const uint16_t* k_new, const uint16_t* v_new,
+                                                 const void* q, uint32_t q_dtype, uint32_t q_heads, float scale,
+                                                 uint32_t token_count, uint32_t base_position, uint32_t seq,
+                                                 const miikv_prefill_state* prefill_state, float* out,
+                                                 const float* gate, float* gated_out, void* workspace,
+                                                 uint64_t workspace_bytes, void* stream) {
+    if (k_new == nullptr || v_new == nullptr) return MIIKV_EINVAL;
+    return suffix_impl(view, k_new, v_new, q, q_dtype, q_heads, scale, token_count, base_position, seq,
+                       prefill_state, out, gate, gated_out, workspace, workspace_bytes, stream);
 }

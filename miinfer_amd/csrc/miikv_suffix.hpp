@@ -29,6 +29,12 @@ struct ExpandArgs {
     const miikv_prefill_state* ps;
     uint32_t steps;      // steps per kv head in the tile area
     _Float16* tiles;
+    // Fused append (k_new set): the suffix's fp16 rows [token_count][kv_heads][D],
+    // quantised and stored at positions base_position + t (or the prefill state's).
+    const uint16_t* k_new;
+    const uint16_t* v_new;
+    uint32_t token_count;
+    uint32_t base_position;
 };
 
 struct SuffixArgs {

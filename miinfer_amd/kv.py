@@ -340,9 +340,12 @@ def suffix_attention(cache: KvCache, q: torch.Tensor, base_position: int, scale:
                      *, seq: int = 0, prefill_state: torch.Tensor | None = None,
                      gate: torch.Tensor | None = None, out: torch.Tensor | None = None,
                      gated_out: torch.Tensor | None = None, split: bool = True,
+                     k_new: torch.Tensor | None = None, v_new: torch.Tensor | None = None,
                      workspace: torch.Tensor | None = None, stream=None):
     """Causal attention of a T-token suffix (rows already appended at base_position..)
     over the cache.  q: [T, q_heads, head_dim] fp16/fp32.  Returns (out, gated_out).
+    With k_new / v_new (fp16 [T, kv_heads, head_dim]) the suffix's rows are quantised
+    and stored in the same pass (fused append) instead of being appended first.
 
     The workspace holds the context's expanded fp16 tiles plus, for split-K, the
     partial records: split=True allocates suffix_workspace_bytes() (unless given);
@@ -373,6 +376,17 @@ def suffix_attention(cache: KvCache, q: torch.Tensor, base_position: int, scale:
             need = cache.kv_heads * ((bound + 31) // 32) * 2 * d * 32 * 2
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
     ws_bytes = workspace.numel() * workspace.element_size()
+    if (k_new is None) != (v_new is None):
+        raise ValueError("k_new and v_new go together")
+    if k_new is not None:
+        for tns in (k_new, v_new):
+            if tns.dtype != torch.float16 or tuple(tns.shape) != (t, cache.kv_heads, d) or \
+                    not tns.is_contiguous():
+                raise ValueError("k_new/v_new must be contiguous fp16 [T, kv_heads, head_dim]")
+        call("miikv_suffix_append_attn", cache.view, _ptr(k_new), _ptr(v_new), _ptr(q), qd, q_heads,
+             float(scale), t, base_position, seq, _ptr(prefill_state), _ptr(out), _ptr(gate),
+             _ptr(gated_out), _ptr(workspace), ws_bytes, _stream(stream))
+        return out, gated_out
     call("miikv_suffix_attn", cache.view, _ptr(q), qd, q_heads, float(scale), t, base_position,
          seq, _ptr(prefill_state), _ptr(out), _ptr(gate), _ptr(gated_out),
          _ptr(workspace), ws_bytes, _stream(stream))

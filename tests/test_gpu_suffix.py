@@ -121,3 +121,77 @@ def test_suffix_workspace_too_small_is_rejected(gpu):
     with pytest.raises(m.MiikvError):
         m.suffix_attention(cache, q, 2048, workspace=torch.empty(need // 2, dtype=torch.uint8,
                                                                   device=gpu))
+
+
+def _canon_all(cache, seq, n):
+    out = cache.export_canonical(seq, 0, n)
+    torch.cuda.synchronize()
+    return [t.cpu().numpy() for t in out]
+
+
+@pytest.mark.parametrize("hq,hk,d,prefix,t,split", [(24, 4, 256, 300, 40, True), (32, 8, 128, 1000, 64, True),
+                                                    (24, 4, 256, 0, 17, False), (6, 1, 128, 64, 1, True),
+                                                    (24, 4, 256, 257, 96, False), (8, 8, 128, 3000, 130, True)])
+def test_suffix_fused_append_matches_append_then_attend(gpu, hq, hk, d, prefix, t, split):
+    """miikv_suffix_append_attn stores the suffix rows with the bytes miikv_append_f16
+    stores (the cache slots start with older bytes) and returns exactly the outputs of
+    append followed by miikv_suffix_attn; the oracle checks the result."""
+    import miinfer_amd as m
+    rng = np.random.default_rng(prefix * 3 + t)
+    cap = ((prefix + t + 63) // 64) * 64
+    k = randn_f16(rng, (prefix + t, hk, d))
+    v = randn_f16(rng, (prefix + t, hk, d))
+    junk = randn_f16(rng, (cap, hk, d)) * np.float16(30)
+    fused = m.KvCache.contiguous(hk, d, cap)
+    plain = m.KvCache.contiguous(hk, d, cap)
+    fused.append(_dev(junk, gpu), _dev(junk, gpu))
+    for c in (fused, plain):
+        if prefix:
+            c.append(_dev(k[:prefix], gpu), _dev(v[:prefix], gpu), base_position=0)
+    plain.append(_dev(k[prefix:], gpu), _dev(v[prefix:], gpu), base_position=prefix)
+    q = _dev(randn_f16(rng, (t, hq, d)), gpu)
+    a, _ = m.suffix_attention(fused, q, prefix, split=split, k_new=_dev(k[prefix:], gpu),
+                              v_new=_dev(v[prefix:], gpu))
+    b, _ = m.suffix_attention(plain, q, prefix, split=split)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    for x, y in zip(_canon_all(fused, 0, prefix + t), _canon_all(plain, 0, prefix + t)):
+        assert np.array_equal(x, y)
+    kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+    vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+    expect = oracle.suffix_attention_q8(q.cpu().numpy().astype(np.float32), kc, ks, vc, vs, prefix, hq,
+                                        1 / math.sqrt(d))
+    assert_attention_close(a.cpu().numpy(), expect, "fused suffix")
+
+
+def test_suffix_fused_append_paged_prefill_state(gpu):
+    """Paged cache, positions from a device prefill state (host bound larger than the
+    device token count): rows past the device count are neither stored nor attended."""
+    import miinfer_amd as m
+    rng = np.random.default_rng(21)
+    hq, hk, d, pt = 24, 4, 256, 256
+    prefix, t = 700, 100
+    npages = (prefix + t + 20 + pt - 1) // pt
+    table = _dev(rng.permutation(npages + 2)[:npages].astype(np.int32).reshape(1, npages), gpu)
+    k = randn_f16(rng, (prefix + t + 20, hk, d))
+    v = randn_f16(rng, (prefix + t + 20, hk, d))
+    fused = m.KvCache.paged_cache(hk, d, npages + 2, table, page_tokens=pt)
+    plain = m.KvCache.paged_cache(hk, d, npages + 2, table, page_tokens=pt)
+    for c in (fused, plain):
+        c.append(_dev(k[:prefix], gpu), _dev(v[:prefix], gpu), base_position=0)
+    plain.append(_dev(k[prefix:prefix + t], gpu), _dev(v[prefix:prefix + t], gpu), base_position=prefix)
+    before = _canon_all(fused, 0, prefix + t + 20)
+    q = _dev(randn_f16(rng, (t + 20, hq, d)), gpu)
+    ps = m.make_prefill_state(prefix, t, device=gpu)
+    a = torch.full((t + 20, hq, d), 5.0, device=gpu)
+    b = torch.full((t + 20, hq, d), 5.0, device=gpu)
+    m.suffix_attention(fused, q, 0, prefill_state=ps, out=a, k_new=_dev(k[prefix:], gpu),
+                       v_new=_dev(v[prefix:], gpu))
+    m.suffix_attention(plain, q, 0, prefill_state=ps, out=b)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    assert bool((a[t:] == 5.0).all())
+    after = _canon_all(fused, 0, prefix + t + 20)
+    for x, y, z in zip(after, _canon_all(plain, 0, prefix + t + 20), before):
+        assert np.array_equal(x[:, :prefix + t], y[:, :prefix + t])
+        assert np.array_equal(x[:, prefix + t:], z[:, prefix + t:])  # past the device count: untouched
