@@ -210,7 +210,7 @@ __global__ void __launch_bounds__(512) append_tile_kernel(Geo g, AppendIn in, ui
     quantize16(xv, qv, sv);
 
     uint8_t* s_k = reinterpret_cast<uint8_t*>(s_tile);  // [32*D] K codes, slab order
-    uint8_t* s_v = s_k + 32 * D;                         // [32*D] V codes, slab order
+    uint8_t* s_v = s_k + 32 * D;                         // [32][D] V codes, token-major
     uint16_t* s_s = reinterpret_cast<uint16_t*>(s_v + 32 * D);  // [2][32][D/32] scales
     const uint32_t d0 = q16 * 16;
     uint32_t packed[4];
@@ -223,8 +223,16 @@ __global__ void __launch_bounds__(512) append_tile_kernel(Geo g, AppendIn in, ui
     }
     *reinterpret_cast<uint2*>(s_k + k_code_offset(tl, d0, D)) = make_uint2(packed[0], packed[1]);
     *reinterpret_cast<uint2*>(s_k + k_code_offset(tl, d0 + 8, D)) = make_uint2(packed[2], packed[3]);
+    // V codes row-major here (one 16-byte store, no bank conflicts); the slab's
+    // token-interleaved order is gathered on the way out.
+    uint32_t vpk[4];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) s_v[v_code_offset(tl, d0 + i, D)] = static_cast<uint8_t>(qv[i]);
+    for (int w = 0; w < 4; ++w)
+        vpk[w] = (static_cast<uint32_t>(static_cast<uint8_t>(qv[4 * w]))) |
+                 (static_cast<uint32_t>(static_cast<uint8_t>(qv[4 * w + 1])) << 8) |
+                 (static_cast<uint32_t>(static_cast<uint8_t>(qv[4 * w + 2])) << 16) |
+                 (static_cast<uint32_t>(static_cast<uint8_t>(qv[4 * w + 3])) << 24);
+    *reinterpret_cast<uint4*>(s_v + tl * D + d0) = make_uint4(vpk[0], vpk[1], vpk[2], vpk[3]);
     if ((q16 & 1) == 0) {
         s_s[tl * (D / 32) + d0 / 32] = f32_to_f16_bits(sk);
         s_s[32 * (D / 32) + tl * (D / 32) + d0 / 32] = f32_to_f16_bits(sv);
@@ -240,7 +248,18 @@ __global__ void __launch_bounds__(512) append_tile_kernel(Geo g, AppendIn in, ui
     const uint32_t chunks = 32 * D / 16;  // 16-byte chunks per code region
     for (uint32_t c = threadIdx.x; c < chunks; c += blockDim.x) {
         kdst[c] = s_tile[c];
-        vdst[c] = s_tile[chunks + c];
+        // V chunk c: dim d = c/2, slab bytes 16*(c%2) .. +15 of that dim hold tokens
+        // 16J + 4G + I at 8G + 4J + I, G = 2*(c%2) + {0, 1}: four 4-token runs.
+        const uint32_t d = c / 2, g0 = 2 * (c % 2);
+        uint32_t w[4];
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k) {
+            const uint32_t t0 = 16 * (k % 2) + 4 * (g0 + k / 2);
+            w[k] = static_cast<uint32_t>(s_v[t0 * D + d]) | (static_cast<uint32_t>(s_v[(t0 + 1) * D + d]) << 8) |
+                   (static_cast<uint32_t>(s_v[(t0 + 2) * D + d]) << 16) |
+                   (static_cast<uint32_t>(s_v[(t0 + 3) * D + d]) << 24);
+        }
+        vdst[c] = make_uint4(w[0], w[1], w[2], w[3]);
     }
     const uint32_t schunks = 32 * (D / 32) * 2 / 16;  // 16-byte chunks per scale region
     const size_t sidx = (slab * g.page_tokens + tp0) * (D / 32);
