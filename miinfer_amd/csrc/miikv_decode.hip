@@ -27,6 +27,11 @@
 // combine (gfx906/kernels/qwen3_primitives.hip:2295-2385): g = max m_s,
 // L = sum l_s e^{m_s-g}, out = sum acc_s e^{m_s-g} / L, 0 when L == 0,
 // gated = out * sigmoid(gate).
+//
+// Measurement switches (never defined by the product build; each gives wrong
+// results by design and exists to time one part of the kernel in isolation):
+// MIIKV_EXP_NO_LOOP (no step: the fixed cost of a launch), MIIKV_EXP_NO_COMPUTE
+// (loads only), MIIKV_EXP_NO_KBIAS (no code bias), MIIKV_EXP_EXP2F (library exp2).
 #include "miikv_common.hpp"
 #include "miikv_split.hpp"
 

@@ -28,6 +28,9 @@
 // and stores its rows; otherwise each (token, kv head, split) writes a partial
 // record (unnormalised O, running max, sum) and suffix_combine_kernel merges
 // them with token t's context length P + t + 1.
+//
+// MIIKV_SFX_EXP_NOLOOP (never defined by the product build) times the kernel's
+// fixed cost with a single step per workgroup; its results are wrong by design.
 #include "miikv_suffix.hpp"
 
 #include <algorithm>
