@@ -485,7 +485,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this path runs on a single MI355X "
-              "(sharding across GPUs is described in DESIGN.md, not run)", file=sys.stderr)
+              "(it would shard by kv head or by sequence with no exchange; only one GPU's share runs here)", file=sys.stderr)
         return 2
 
     import torch
