@@ -1,12 +1,11 @@
 // Split-K GQA decode attention over the tiled q8_0 cache (gfx950, wave64, MFMA).
 //
 // Work decomposition.  A workgroup of 4 waves owns one (sequence, kv head,
-// split); a split is 4 * chunks_per_wave chunks of 64 tokens and each wave
-// streams `chunks_per_wave` consecutive chunks.  All G = q_heads / kv_heads
-// query heads of the kv head are served by the same wave, so every K/V byte
-// is read from HBM exactly once.
+// split); a split is 4 * cpw steps of 32 tokens and each wave streams cpw
+// consecutive steps.  All G = q_heads / kv_heads query heads of the kv head are
+// served by the same wave, so every K/V byte is read from HBM exactly once.
 //
-// Per 64-token chunk a wave computes, for 4 tiles of 16 tokens:
+// Per 32-token step a wave computes, for its 2 tiles of 16 tokens:
 //   S^T[token][head] = K_tile (16 x D, int8 -> fp16) * Q^T (D x 16 heads)
 // with v_mfma_f32_16x16x32_f16, one MFMA per 32-value q8_0 block so the block
 // scale is applied to the fp32 result (exact in the codes).  The output
@@ -20,13 +19,16 @@
 //
 // Cross-wave combine goes through LDS; each workgroup writes one partial record
 // (m, l, unnormalised O) per split into the caller's workspace, and a second,
-// wide kernel merges the splits.  Two launches on one stream need no
-// cross-workgroup synchronisation: a grid-wide arrival counter would need an
-// agent-scope release (an L2 write-back on every XCD) per workgroup, which
-// measured slower than the second launch.  The merge follows the reference
-// combine (gfx906/kernels/qwen3_primitives.hip:2295-2385): g = max m_s,
+// wide kernel merges the splits.  Merging inside this launch instead (records
+// written with device-scope stores, an arrival counter, the last arrivals
+// merging) measured no faster: the merge then costs the counter's and the
+// records' round trips on top of the last split, about what the second launch
+// costs.  The merge follows the reference combine
+// (gfx906/kernels/qwen3_primitives.hip:2295-2385): g = max m_s,
 // L = sum l_s e^{m_s-g}, out = sum acc_s e^{m_s-g} / L, 0 when L == 0,
-// gated = out * sigmoid(gate).
+// gated = out * sigmoid(gate).  With the fused append, the last workgroups of
+// the grid quantise, store and score the new token and write it as one more
+// record (append_record).
 //
 // Measurement switches (never defined by the product build; each gives wrong
 // results by design and exists to time one part of the kernel in isolation):
