@@ -10,10 +10,11 @@
 //     fp16 tiles in the workspace, laid out as the MFMA operand fragments the
 //     attention waves read: K^ = code * k_scale as the A operand of S^T = K^ Q^T,
 //     V^T = code * v_scale as the A operand of O^T += V^T P^T.  Each K/V byte is
-//     dequantised once instead of once per row block.
+//     dequantised once instead of once per row block.  With the fused append it
+//     also quantises and stores the suffix's own rows.
 //  2. suffix_kernel: a workgroup owns 32 query rows per wave and streams the
-//     fp16 tiles of its key range through LDS (direct global->LDS loads,
-//     double-buffered, one barrier per step).  Per 32-key step and wave
+//     fp16 tiles of its key range through LDS (direct global->LDS loads, four
+//     buffers, prefetch two steps ahead, one barrier per step).  Per 32-key step and wave
 //     (v_mfma_f32_32x32x16_f16):
 //        S^T[key][row] (32x32) = sum over D/16 dim chunks of K^[32 keys][16] Q^T
 //        O^T[dim][row]        += V^T[32 dims][16 keys] P^T, two key halves per tile
