@@ -318,8 +318,6 @@ uint32_t miikv_pool_free_pages(const miikv_pool* pool);
 miikv_status miikv_pool_fork(miikv_pool* pool, const int32_t* parent_row, uint32_t length,
                              uint32_t page_tokens, int32_t* child_row, int32_t* copy_src,
                              int32_t* copy_dst, uint32_t* n_copies);
-/* Before appending at `position` (the sequence's current length): allocate a
- * fresh page at a page boundary, or copy a shared page (copy-on-write). */
 /* n forks of one parent in one call (child i's row at child_rows + i*row_stride,
  * row_stride >= pages of `length`); copy_src / copy_dst (capacity n) receive the
  * copy-on-write page pairs and *n_copies their count; *n_done forks completed
@@ -327,6 +325,8 @@ miikv_status miikv_pool_fork(miikv_pool* pool, const int32_t* parent_row, uint32
 miikv_status miikv_pool_fork_n(miikv_pool* pool, const int32_t* parent_row, uint32_t length, uint32_t page_tokens,
                                uint32_t n, int32_t* child_rows, uint32_t row_stride, int32_t* copy_src,
                                int32_t* copy_dst, uint32_t* n_copies, uint32_t* n_done);
+/* Before appending at `position` (the sequence's current length): allocate a
+ * fresh page at a page boundary, or copy a shared page (copy-on-write). */
 miikv_status miikv_pool_prepare_append(miikv_pool* pool, int32_t* row, uint32_t row_capacity,
                                        uint32_t position, uint32_t page_tokens,
                                        int32_t* copy_src, int32_t* copy_dst, uint32_t* n_copies);
