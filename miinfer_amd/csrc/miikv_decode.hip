@@ -348,11 +348,19 @@ decode_kernel(SplitArgs a) {
     // fp16 query bits, issued before the context length so that the two loads
     // overlap (lanes past the group read the group's last head and discard it).
     uint4 qraw[QF32 ? 1 : NB];
-    if constexpr (!QF32) {
+    float4 q32raw[QF32 ? NB : 1][2];
+    {
         const size_t qrow = (static_cast<size_t>(b) * a.q_heads + static_cast<size_t>(h) * G + min(n, G - 1)) * D;
 #pragma unroll
-        for (uint32_t blk = 0; blk < NB; ++blk)
-            qraw[blk] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.q) + qrow + blk * 32 + g4 * 8);
+        for (uint32_t blk = 0; blk < NB; ++blk) {
+            if constexpr (QF32) {
+                const float* qp = static_cast<const float*>(a.q) + qrow + blk * 32 + g4 * 8;
+                q32raw[blk][0] = *reinterpret_cast<const float4*>(qp);
+                q32raw[blk][1] = *reinterpret_cast<const float4*>(qp + 4);
+            } else {
+                qraw[blk] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.q) + qrow + blk * 32 + g4 * 8);
+            }
+        }
     }
     const uint32_t L = split_length(a, b);
     const uint32_t tps = kWavesPerWg * cpw * kChunk;
@@ -374,10 +382,9 @@ decode_kernel(SplitArgs a) {
             half8 lo = {};
             float qs = 0.0f;
             if (n < G) {
-                if (QF32) {
-                    const float* qp = static_cast<const float*>(a.q) + qrow + blk * 32 + g4 * 8;
-                    const float4 x0 = *reinterpret_cast<const float4*>(qp);
-                    const float4 x1 = *reinterpret_cast<const float4*>(qp + 4);
+                if constexpr (QF32) {
+                    const float4 x0 = q32raw[blk][0];
+                    const float4 x1 = q32raw[blk][1];
                     const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
                     for (int i = 0; i < 8; ++i) {
