@@ -19,7 +19,10 @@ def _dev(a, gpu):
     return torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
 
 
-def test_decode_step_graph_replays(gpu):
+@pytest.mark.parametrize("fused", [False, True])
+def test_decode_step_graph_replays(gpu, fused):
+    """fused: the captured step is miikv_decode_append_attn (store + attention in one
+    launch pair) instead of an append followed by attention."""
     import miinfer_amd as m
     rng = np.random.default_rng(41)
     hq, hk, d, cap, p0, steps = 32, 8, 128, 1024, 500, 8
@@ -39,8 +42,12 @@ def test_decode_step_graph_replays(gpu):
     g = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
     with torch.cuda.graph(g, stream=s):
-        cache.append(k_in, v_in, decode_state=ds)
-        m.decode_attention(cache, q_in, decode_state=ds, max_context=cap, out=out, workspace=ws)
+        if fused:
+            m.decode_attention(cache, q_in, decode_state=ds, max_context=cap, out=out, workspace=ws,
+                               k_new=k_in, v_new=v_in)
+        else:
+            cache.append(k_in, v_in, decode_state=ds)
+            m.decode_attention(cache, q_in, decode_state=ds, max_context=cap, out=out, workspace=ws)
         m.advance_decode_state(ds, tokens_out, stop_tokens=(151643, 151645))
     torch.cuda.synchronize()
 
@@ -67,7 +74,9 @@ def test_decode_step_graph_replays(gpu):
     assert list(tokens_out.cpu().numpy()[:steps]) == toks
 
 
-def test_suffix_step_graph_replays(gpu):
+@pytest.mark.parametrize("fused", [False, True])
+def test_suffix_step_graph_replays(gpu, fused):
+    """fused: the captured step is miikv_suffix_append_attn."""
     import miinfer_amd as m
     rng = np.random.default_rng(42)
     hq, hk, d, cap, t = 24, 4, 256, 2048, 64
@@ -86,8 +95,11 @@ def test_suffix_step_graph_replays(gpu):
     g = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
     with torch.cuda.graph(g, stream=s):
-        cache.append(k_in, v_in, prefill_state=ps)
-        m.suffix_attention(cache, q_in, 0, prefill_state=ps, out=out, workspace=ws)
+        if fused:
+            m.suffix_attention(cache, q_in, 0, prefill_state=ps, out=out, workspace=ws, k_new=k_in, v_new=v_in)
+        else:
+            cache.append(k_in, v_in, prefill_state=ps)
+            m.suffix_attention(cache, q_in, 0, prefill_state=ps, out=out, workspace=ws)
     torch.cuda.synchronize()
     kc, ks = oracle.quantize_rows(k_all.transpose(1, 0, 2))
     vc, vs = oracle.quantize_rows(v_all.transpose(1, 0, 2))
