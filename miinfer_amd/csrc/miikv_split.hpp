@@ -119,7 +119,13 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
 
     // The first kSpec records of this thread are fetched before the context length
     // (and with it the record count) arrives; records past the count are ignored.
-    constexpr uint32_t kSpec = 4;
+    // 16 * kSpec = 80 covers a single sequence's 64 splits plus the fused append's
+    // record, so none of them waits for the length (a 65th record fetched after it
+    // added one dependent memory round trip to the combine).
+#ifndef MIIKV_COMBINE_SPEC
+#define MIIKV_COMBINE_SPEC 5
+#endif
+    constexpr uint32_t kSpec = MIIKV_COMBINE_SPEC;
     float ms[kSpec], ls[kSpec];
     float4 vv[kSpec];
 #pragma unroll
