@@ -126,6 +126,13 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
 #define MIIKV_COMBINE_SPEC 5
 #endif
     constexpr uint32_t kSpec = MIIKV_COMBINE_SPEC;
+    // The gate of this thread's outputs (split group 0 writes them) goes out with the
+    // records, so the epilogue does not wait for it.
+    float gv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (a.gate != nullptr && sg == 0 && active) {
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k) gv[k] = a.gate[out_row0 + e + k];
+    }
     float ms[kSpec], ls[kSpec];
     float4 vv[kSpec];
 #pragma unroll
@@ -203,7 +210,7 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
         const size_t oi = out_row0 + e + k;
         if (a.out) a.out[oi] = vals[k];
         if (a.gate) {
-            gated[k] = vals[k] * (1.0f / (1.0f + expf(-a.gate[oi])));
+            gated[k] = vals[k] * (1.0f / (1.0f + expf(-gv[k])));
             if (a.gated_out) a.gated_out[oi] = gated[k];
         }
     }

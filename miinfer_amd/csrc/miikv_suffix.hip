@@ -498,6 +498,10 @@ __global__ void __launch_bounds__(256) suffix_combine_kernel(SuffixCombineArgs a
     const uint32_t nsplit = min(a.splits, (P + t + 1 + a.split_keys - 1) / a.split_keys);
     const _Float16* po = static_cast<const _Float16*>(a.part);
     const float2* ml = reinterpret_cast<const float2*>(po + part_o_halves(a.splits, a.kv_heads, rows_cap, D));
+    const size_t oi = (static_cast<size_t>(t) * a.q_heads + h * G + g) * D + 4 * d4;
+    // The gate goes out with the first batch of records (no round trip of its own).
+    float4 gv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (a.gate && a.gated_out) gv = *reinterpret_cast<const float4*>(a.gate + oi);
     // Records hold O_s / l_s: each split enters with weight l_s e^{m_s - M}.
     float M = -INFINITY, Ls = 0.0f;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -529,10 +533,8 @@ __global__ void __launch_bounds__(256) suffix_combine_kernel(SuffixCombineArgs a
     }
     const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
     const float4 o = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
-    const size_t oi = (static_cast<size_t>(t) * a.q_heads + h * G + g) * D + 4 * d4;
     if (a.out) *reinterpret_cast<float4*>(a.out + oi) = o;
     if (a.gate && a.gated_out) {
-        const float4 gv = *reinterpret_cast<const float4*>(a.gate + oi);
         float4 r;
         r.x = o.x * (1.0f / (1.0f + expf(-gv.x)));
         r.y = o.y * (1.0f / (1.0f + expf(-gv.y)));
