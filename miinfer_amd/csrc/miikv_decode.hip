@@ -246,7 +246,7 @@ __device__ void append_record(const SplitArgs& a, uint32_t b, uint32_t h, uint32
 }
 
 template <uint32_t D, bool QF32, bool APPEND>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DecodeTuning<D, QF32>::waves_per_eu)))
+__global__ void __launch_bounds__(64 * kWavesPerWg) __attribute__((amdgpu_waves_per_eu(DecodeTuning<D, QF32>::waves_per_eu)))
 decode_kernel(SplitArgs a) {
     constexpr uint32_t NB = D / 32;   // q8_0 blocks per row
     constexpr uint32_t NC = D / 64;   // 16-byte K loads per tile row group
