@@ -87,6 +87,10 @@ struct DecodeTuning {
     static constexpr bool vbias = D == 128 ? MIIKV_VBIAS_D128 != 0 : (QF32 ? MIIKV_VBIAS_D256_F32 != 0 : MIIKV_VBIAS_D256 != 0);
 };
 constexpr uint32_t kTargetWaves = 256 * 8;  // 256 CUs x 8 resident waves
+#ifndef MIIKV_INTERLEAVE_CPW
+#define MIIKV_INTERLEAVE_CPW 4
+#endif
+constexpr uint32_t kInterleaveCpw = MIIKV_INTERLEAVE_CPW;  // steps per wave at which waves interleave
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kCodeBias = 1152.0f;  // codes enter the MFMA as fp16(code + 1152)
 constexpr float kRescaleSlack = 6.0f;  // log2 units: p <= 64, and 64 * (65504/127) < 65504
@@ -295,9 +299,18 @@ decode_kernel(SplitArgs a) {
 
     // Steps this wave may own, from the host bound alone: the first loads are issued
     // before the context length arrives from memory.
-    const uint32_t c_begin = (split * kWavesPerWg + wave) * cpw;
+    // A split is 4*cpw consecutive steps.  At cpw == kInterleaveCpw wave w takes
+    // steps w, w+4, ... of it (the four waves of a workgroup then read one contiguous
+    // region at a time); otherwise each wave streams the w-th run of cpw steps.  A
+    // measured choice, not a model: config 2 shape, interleaved against runs, cpw 2
+    // (16k) +0.3 us, cpw 4 (32k) -0.4 us, cpw 8 (64k) +0.15 us.  The wave's local
+    // step i (0 <= i < n_steps) is split step first + i * stride.
     const uint32_t nsteps_max = (a.max_context + kChunk - 1) / kChunk;
-    const uint32_t c_end_max = min(c_begin + cpw, nsteps_max);
+    const bool interleave = cpw == kInterleaveCpw;
+    const uint32_t stride = interleave ? kWavesPerWg : 1u;
+    const uint32_t first = interleave ? split * kWavesPerWg * cpw + wave : (split * kWavesPerWg + wave) * cpw;
+    const uint32_t last_excl = min(interleave ? (split + 1) * kWavesPerWg * cpw : first + cpw, nsteps_max);
+    const uint32_t n_max = first < last_excl ? (last_excl - first + stride - 1) / stride : 0;
     const size_t slab_bytes = static_cast<size_t>(geo.page_tokens) * D;
 
     // Registers of one 32-token step: two K tiles, one V group, their scales.
@@ -310,13 +323,13 @@ decode_kernel(SplitArgs a) {
     // Load cursor: the page (slab) is looked up once per page, not per step.  Page
     // indices are clamped into the pool, so a speculative load past the sequence end
     // reads a valid (unused) page rather than whatever an unset table entry holds.
-    uint32_t ld_tok = c_begin * kChunk;
+    uint32_t ld_tok = first * kChunk;
     uint32_t ld_tp = ld_tok % geo.page_tokens;
     size_t ld_slab = 0;
-    if (c_begin < c_end_max) ld_slab = slab_of_clamped(geo, b, ld_tok, h);
+    if (n_max > 0) ld_slab = slab_of_clamped(geo, b, ld_tok, h);
     auto load_step = [&](Step& st) {
-        if (ld_tp == geo.page_tokens) {
-            ld_tp = 0;
+        if (ld_tp >= geo.page_tokens) {
+            ld_tp = ld_tok % geo.page_tokens;
             ld_slab = slab_of_clamped(geo, b, ld_tok, h);
         }
         const int8_t* kb = geo.k_codes + ld_slab * slab_bytes + static_cast<size_t>(ld_tp) * D;
@@ -334,8 +347,8 @@ decode_kernel(SplitArgs a) {
 #pragma unroll
         for (uint32_t mt = 0; mt < NM; ++mt)
             st.v[mt] = load8(vb + (16 * mt + n) * 32 + g4 * 8);
-        ld_tok += kChunk;
-        ld_tp += kChunk;
+        ld_tok += stride * kChunk;
+        ld_tp += stride * kChunk;
     };
 
     // Ring of kRing step buffers; the first kRing-1 are loaded before L is known.
@@ -343,7 +356,7 @@ decode_kernel(SplitArgs a) {
     Step S[kRing];
 #pragma unroll
     for (uint32_t r = 0; r + 1 < kRing; ++r)
-        if (c_begin + r < c_end_max) load_step(S[r]);
+        if (r < n_max) load_step(S[r]);
 
     // fp16 query bits, issued before the context length so that the two loads
     // overlap (lanes past the group read the group's last head and discard it).
@@ -422,9 +435,9 @@ decode_kernel(SplitArgs a) {
     const uint32_t Lc = APPEND ? L - 1 : L;
     const uint32_t nsteps = (Lc + kChunk - 1) / kChunk;
 #ifdef MIIKV_EXP_NO_LOOP
-    const uint32_t c_end = c_begin;
+    const uint32_t n_steps = 0;
 #else
-    const uint32_t c_end = min(c_end_max, nsteps);
+    const uint32_t n_steps = first < nsteps ? min(n_max, (nsteps - first + stride - 1) / stride) : 0;
 #endif
     // Per-wave LDS staging of one step's scales: [K: 32*NB][V: 32*NB] fp16.  Each lane
     // loads NB/2 scales (no redundancy) and re-reads the 4*NB it needs from LDS.
@@ -563,14 +576,15 @@ decode_kernel(SplitArgs a) {
         }
     };
 
-    // Software pipeline over [c_begin, c_end): while step c computes, the loads of
-    // steps c+1 .. c+kRing-1 are in flight (fully unrolled so S[] stays in registers).
-    for (uint32_t c = c_begin; c < c_end; c += kRing) {
+    // Software pipeline over the local steps [0, n_steps): while step i computes, the
+    // loads of steps i+1 .. i+kRing-1 are in flight (fully unrolled so S[] stays in
+    // registers).
+    for (uint32_t i = 0; i < n_steps; i += kRing) {
 #pragma unroll
         for (uint32_t r = 0; r < kRing; ++r) {
-            if (c + r >= c_end) break;
-            if (c + r + kRing - 1 < c_end) load_step(S[(r + kRing - 1) % kRing]);
-            compute_step(c + r, S[r]);
+            if (i + r >= n_steps) break;
+            if (i + r + kRing - 1 < n_steps) load_step(S[(r + kRing - 1) % kRing]);
+            compute_step(first + (i + r) * stride, S[r]);
         }
     }
     if constexpr (kVBias) {
