@@ -78,6 +78,12 @@ namespace {
 #ifndef MIIKV_VBIAS_D128
 #define MIIKV_VBIAS_D128 1
 #endif
+#ifndef MIIKV_NT_SCALES_D128
+#define MIIKV_NT_SCALES_D128 1
+#endif
+#ifndef MIIKV_NT_SCALES_D256
+#define MIIKV_NT_SCALES_D256 0
+#endif
 // An fp32 query carries a second (low-half) set of query fragments and a second
 // MFMA per block; those variants keep a deeper ring at lower occupancy.
 template <uint32_t D, bool QF32>
@@ -85,6 +91,9 @@ struct DecodeTuning {
     static constexpr uint32_t ring = D == 128 ? MIIKV_RING_D128 : (QF32 ? MIIKV_RING_D256_F32 : MIIKV_RING_D256);
     static constexpr uint32_t waves_per_eu = D == 128 ? (QF32 ? 2 : MIIKV_WPE_D128) : (QF32 ? MIIKV_WPE_D256_F32 : MIIKV_WPE_D256);
     static constexpr bool vbias = D == 128 ? MIIKV_VBIAS_D128 != 0 : (QF32 ? MIIKV_VBIAS_D256_F32 != 0 : MIIKV_VBIAS_D256 != 0);
+    // Nontemporal scale loads: config 2 (D = 128) at 32k 20.5 -> 20.2 us; config 3
+    // (D = 256) 157 -> 160 us, so cached there.
+    static constexpr bool nt_scales = D == 128 ? MIIKV_NT_SCALES_D128 != 0 : MIIKV_NT_SCALES_D256 != 0;
 };
 constexpr uint32_t kTargetWaves = 256 * 8;  // 256 CUs x 8 resident waves
 #ifndef MIIKV_INTERLEAVE_CPW
@@ -107,6 +116,20 @@ __device__ __forceinline__ uint2 load8(const int8_t* p) {
     typedef unsigned int u2v __attribute__((ext_vector_type(2)));
     const u2v t = __builtin_nontemporal_load(reinterpret_cast<const u2v*>(p));
     return make_uint2(t.x, t.y);
+}
+
+// One lane's NB/2 block scales of a step; NT: nontemporal, like the codes.
+template <typename T, bool NT>
+__device__ __forceinline__ T load_scales(const uint16_t* p) {
+    if constexpr (!NT) {
+        return *reinterpret_cast<const T*>(p);
+    } else if constexpr (sizeof(T) == 4) {
+        return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+    } else {
+        typedef unsigned int u2v __attribute__((ext_vector_type(2)));
+        const u2v t = __builtin_nontemporal_load(reinterpret_cast<const u2v*>(p));
+        return T{t.x, t.y};
+    }
 }
 
 __device__ __forceinline__ float wave_max_xor_16_32(float x) {
@@ -337,13 +360,13 @@ decode_kernel(SplitArgs a) {
         const size_t sc0 = (ld_slab * geo.page_tokens + ld_tp) * NB;
         // Scales first, each ahead of its codes: loads complete in issue order, so the
         // score MFMAs wait only for the K scales and codes while V is still in flight.
-        st.ks = *reinterpret_cast<const ScaleVec*>(geo.k_scales + sc0 + lane * (NB / 2));
+        st.ks = load_scales<ScaleVec, DecodeTuning<D, QF32>::nt_scales>(geo.k_scales + sc0 + lane * (NB / 2));
 #pragma unroll
         for (uint32_t J = 0; J < 2; ++J)
 #pragma unroll
             for (uint32_t cc = 0; cc < NC; ++cc)
                 st.k[J][cc] = load16(kb + J * 16 * D + cc * 1024 + g4 * 256 + n * 16);
-        st.vs = *reinterpret_cast<const ScaleVec*>(geo.v_scales + sc0 + lane * (NB / 2));
+        st.vs = load_scales<ScaleVec, DecodeTuning<D, QF32>::nt_scales>(geo.v_scales + sc0 + lane * (NB / 2));
 #pragma unroll
         for (uint32_t mt = 0; mt < NM; ++mt)
             st.v[mt] = load8(vb + (16 * mt + n) * 32 + g4 * 8);
