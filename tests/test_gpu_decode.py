@@ -260,3 +260,34 @@ def _canon_tail(cache, seq, n):
     out = cache.export_canonical(seq, n - 1, 1)
     torch.cuda.synchronize()
     return [t.cpu().numpy() for t in out]
+
+
+@pytest.mark.parametrize("length", [1, 129, 20000, 30001, 32768])
+def test_decode_c2_capacity_32k_partial(gpu, length):
+    """Config 2 shape planned for a 32768-token bound (4 steps per wave, the four waves
+    of a workgroup interleaving their split's steps) at shorter contexts, so that
+    splits end mid-way, some hold no key and the last step is masked.  With the fused
+    append the new row (position length-1) is stored and scored in the same launch
+    pair; the cache held junk at that position before."""
+    import miinfer_amd as m
+    hq, hk, d, cap = 32, 8, 128, 32768
+    rng = np.random.default_rng(length + 11)
+    k = randn_f16(rng, (length, hk, d))
+    v = randn_f16(rng, (length, hk, d))
+    cache = m.KvCache.contiguous(hk, d, cap)
+    junk = randn_f16(rng, (1, hk, d)) * np.float16(50)
+    if length > 1:
+        cache.append(_dev(k[:-1], gpu), _dev(v[:-1], gpu))
+    cache.append(_dev(junk, gpu), _dev(junk, gpu), base_position=length - 1)
+    q = randn_f16(rng, (1, hq, d))
+    lens = _dev(np.array([length], np.int32), gpu)
+    out, _ = m.decode_attention(cache, _dev(q, gpu), lengths=lens, max_context=cap,
+                                k_new=_dev(k[-1:], gpu), v_new=_dev(v[-1:], gpu))
+    torch.cuda.synchronize()
+    rk = oracle.quantize_rows(k.transpose(1, 0, 2))
+    rv = oracle.quantize_rows(v.transpose(1, 0, 2))
+    expect = oracle.attention_q8(q[0].astype(np.float32), *rk, *rv, length, hq, 1 / math.sqrt(d))
+    assert_attention_close(out[0].cpu().numpy(), expect, f"L={length}")
+    kc, ks, vc, vs = _canon_tail(cache, 0, length)
+    assert np.array_equal(kc, rk[0][:, -1:]) and np.array_equal(ks.view(np.uint16), rk[1][:, -1:])
+    assert np.array_equal(vc, rv[0][:, -1:]) and np.array_equal(vs.view(np.uint16), rv[1][:, -1:])
