@@ -475,8 +475,14 @@ __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
         }
 }
 
-// Merge the splits of each (row, kv head): thread = 4 consecutive dims of one
-// row.  Token t sees P + t + 1 keys, so splits at or past ceil((P + t + 1) /
+// Dims per thread of suffix_combine_kernel.
+#ifndef MIIKV_SFX_COMBINE_VEC
+#define MIIKV_SFX_COMBINE_VEC 8
+#endif
+constexpr uint32_t kCombVec = MIIKV_SFX_COMBINE_VEC;
+
+// Merge the splits of each (row, kv head): thread = kCombVec consecutive dims of
+// one row.  Token t sees P + t + 1 keys, so splits at or past ceil((P + t + 1) /
 // split_keys) hold no key of its row and are skipped; the rest are merged in
 // split order (out = sum e^{m_s-M} O_s / sum e^{m_s-M} l_s, 0 when the sum is 0).
 template <uint32_t D>
@@ -490,32 +496,39 @@ __global__ void __launch_bounds__(256) suffix_combine_kernel(SuffixCombineArgs a
     const uint32_t G = a.group;
     const uint32_t h = blockIdx.y;
     const uint32_t idx = blockIdx.x * 256 + threadIdx.x;
-    const uint32_t row = idx / (D / 4);
-    const uint32_t d4 = idx % (D / 4);
+    const uint32_t row = idx / (D / kCombVec);
+    const uint32_t dv = idx % (D / kCombVec);
     if (row >= T * G) return;
     const uint32_t rows_cap = a.token_count * G;
     const uint32_t t = row / G, g = row % G;
     const uint32_t nsplit = min(a.splits, (P + t + 1 + a.split_keys - 1) / a.split_keys);
     const _Float16* po = static_cast<const _Float16*>(a.part);
     const float2* ml = reinterpret_cast<const float2*>(po + part_o_halves(a.splits, a.kv_heads, rows_cap, D));
-    const size_t oi = (static_cast<size_t>(t) * a.q_heads + h * G + g) * D + 4 * d4;
+    const size_t oi = (static_cast<size_t>(t) * a.q_heads + h * G + g) * D + kCombVec * dv;
     // The gate goes out with the first batch of records (no round trip of its own).
-    float4 gv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (a.gate && a.gated_out) gv = *reinterpret_cast<const float4*>(a.gate + oi);
+    float gv[kCombVec] = {};
+    if (a.gate && a.gated_out) {
+#pragma unroll
+        for (uint32_t c = 0; c < kCombVec; c += 4) {
+            const float4 x = *reinterpret_cast<const float4*>(a.gate + oi + c);
+            gv[c] = x.x; gv[c + 1] = x.y; gv[c + 2] = x.z; gv[c + 3] = x.w;
+        }
+    }
     // Records hold O_s / l_s: each split enters with weight l_s e^{m_s - M}.
+    using HalfV = _Float16 __attribute__((ext_vector_type(kCombVec)));
     float M = -INFINITY, Ls = 0.0f;
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float acc[kCombVec] = {};
     // Batches of kU splits: every load of a batch is issued before the first merge.
     constexpr uint32_t kU = 8;
     for (uint32_t sp0 = 0; sp0 < nsplit; sp0 += kU) {
         float2 e[kU];
-        half4 v[kU];
+        HalfV v[kU];
 #pragma unroll
         for (uint32_t j = 0; j < kU; ++j) {
             const uint32_t sp = min(sp0 + j, nsplit - 1);
             const size_t pr = (static_cast<size_t>(sp) * a.kv_heads + h) * rows_cap + row;
             e[j] = ml[pr];
-            v[j] = *reinterpret_cast<const half4*>(po + pr * D + 4 * d4);
+            v[j] = *reinterpret_cast<const HalfV*>(po + pr * D + kCombVec * dv);
         }
 #pragma unroll
         for (uint32_t j = 0; j < kU; ++j) {
@@ -525,22 +538,23 @@ __global__ void __launch_bounds__(256) suffix_combine_kernel(SuffixCombineArgs a
             const float ws = e[j].y * exp2f(e[j].x - mn);
             M = mn;
             Ls = Ls * fo + ws;
-            acc.x = acc.x * fo + static_cast<float>(v[j][0]) * ws;
-            acc.y = acc.y * fo + static_cast<float>(v[j][1]) * ws;
-            acc.z = acc.z * fo + static_cast<float>(v[j][2]) * ws;
-            acc.w = acc.w * fo + static_cast<float>(v[j][3]) * ws;
+#pragma unroll
+            for (uint32_t c = 0; c < kCombVec; ++c) acc[c] = acc[c] * fo + static_cast<float>(v[j][c]) * ws;
         }
     }
     const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
-    const float4 o = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
-    if (a.out) *reinterpret_cast<float4*>(a.out + oi) = o;
-    if (a.gate && a.gated_out) {
-        float4 r;
-        r.x = o.x * (1.0f / (1.0f + expf(-gv.x)));
-        r.y = o.y * (1.0f / (1.0f + expf(-gv.y)));
-        r.z = o.z * (1.0f / (1.0f + expf(-gv.z)));
-        r.w = o.w * (1.0f / (1.0f + expf(-gv.w)));
-        *reinterpret_cast<float4*>(a.gated_out + oi) = r;
+#pragma unroll
+    for (uint32_t c = 0; c < kCombVec; c += 4) {
+        const float4 o = make_float4(acc[c] * inv, acc[c + 1] * inv, acc[c + 2] * inv, acc[c + 3] * inv);
+        if (a.out) *reinterpret_cast<float4*>(a.out + oi + c) = o;
+        if (a.gate && a.gated_out) {
+            float4 r;
+            r.x = o.x * (1.0f / (1.0f + expf(-gv[c])));
+            r.y = o.y * (1.0f / (1.0f + expf(-gv[c + 1])));
+            r.z = o.z * (1.0f / (1.0f + expf(-gv[c + 2])));
+            r.w = o.w * (1.0f / (1.0f + expf(-gv[c + 3])));
+            *reinterpret_cast<float4*>(a.gated_out + oi + c) = r;
+        }
     }
 }
 
@@ -697,7 +711,7 @@ static miikv_status suffix_impl(const miikv_view* view, const uint16_t* k_new, c
         c.out = out;
         c.gate = gate;
         c.gated_out = gated_out;
-        const uint64_t threads = static_cast<uint64_t>(token_count) * G * (view->head_dim / 4);
+        const uint64_t threads = static_cast<uint64_t>(token_count) * G * (view->head_dim / kCombVec);
         const dim3 cgrid(static_cast<uint32_t>((threads + 255) / 256), view->kv_heads);
         if (view->head_dim == 128) hipLaunchKernelGGL(suffix_combine_kernel<128>, cgrid, dim3(256), 0, s, c);
         else hipLaunchKernelGGL(suffix_combine_kernel<256>, cgrid, dim3(256), 0, s, c);
