@@ -220,7 +220,12 @@ __global__ void __launch_bounds__(256) expand_kernel(ExpandArgs a) {
 #define MIIKV_SUFFIX_STAGGER 1
 #endif
 constexpr bool kSufStagger = MIIKV_SUFFIX_STAGGER != 0;
-constexpr uint32_t kDist = 2;                                       // prefetch distance (steps)
+// Prefetch distance in steps (config 4, same box: 1 and 3 both ~1-2 us slower
+// than 2; 3 takes all 160 KB of LDS).
+#ifndef MIIKV_SUFFIX_DIST
+#define MIIKV_SUFFIX_DIST 2
+#endif
+constexpr uint32_t kDist = MIIKV_SUFFIX_DIST;
 constexpr uint32_t kSufBufs = kSufStagger ? kDist + 2 : kDist + 1;  // LDS tile buffers
 
 
