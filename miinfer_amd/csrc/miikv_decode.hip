@@ -809,7 +809,8 @@ static miikv_status decode_impl(const miikv_view* view, const uint16_t* k_new, c
     const dim3 grid(static_cast<uint32_t>(wgs));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool f32 = q_dtype == MIIKV_DTYPE_F32;
-    const dim3 cgrid(batch * view->kv_heads, (G * view->head_dim + 63) / 64);
+    // combine: one workgroup per (sequence, kv head, 32 output elements)
+    const dim3 cgrid(batch * view->kv_heads, G * view->head_dim / 32);
     const bool app = k_new != nullptr;
     if (view->head_dim == 128) {
         if (app) {
@@ -861,3 +862,4 @@ extern "C" miikv_status miikv_decode_append_attn(const miikv_view* view, const u
     return decode_impl(view, k_new, v_new, q, q_dtype, q_heads, scale, batch, d_lengths, decode_state, max_context,
                        out, gate, gated_out, gated_q8_1, workspace, workspace_bytes, stream);
 }
+

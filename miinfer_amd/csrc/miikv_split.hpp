@@ -42,6 +42,7 @@ struct SplitArgs {
     uint32_t q_f32;         // q dtype (scoring the appended token)
 };
 
+
 __device__ __forceinline__ float exp2_safe(float x) { return exp2f(x); }  // exp2(-inf) == 0
 
 // Floats in one split's partial record: O [G*D], m [G], l [G], padded to 4.
@@ -88,14 +89,34 @@ __device__ __forceinline__ uint32_t split_count(uint32_t L, uint32_t cpw) {
     return (L + tps - 1) / tps;
 }
 
-// Cross-split combine.  Workgroup (sequence * kv_heads + head, element block of 64)
-// reads the partial records of every split of that (sequence, kv head): thread
-// (e4 = tid & 15, sg = tid >> 4) folds records sg, sg+16, ... for 4 consecutive
-// elements with its own running max, so its loads are independent; the 16 split
-// groups are merged in a fixed order through LDS (deterministic result).
+// Cross-split combine.  Workgroup (sequence * kv_heads + head, block of 32
+// consecutive output elements, all in one query-head row) holds one record slot per
+// thread group: thread (q = tid & 7, rg = tid >> 3) reads elements 4q..4q+3 of records
+// rg, rg + 32, rg + 64 (issued before the context length arrives, so one memory round
+// trip covers a single sequence's 64 splits and the fused append's record) and of any
+// further ones after it, folding them with its own running max.  The 32 record groups
+// are then merged in a fixed butterfly (lanes 8, 16, 32 apart) and across the four
+// waves in LDS, so the result is deterministic.
 // Fused append (APPEND): the splits covered the L-1 cached keys and decode_kernel
 // wrote the new token's record (m = score, l = 1, O = its dequantised V row) at
-// slot nsplit, merged here as one more record.
+// slot nsplit, merged here as one more record.  The merge follows the reference
+// combine (gfx906/kernels/qwen3_primitives.hip:2295-2385).
+__device__ __forceinline__ void merge_state(float& m, float& l, float4& acc, float m2, float l2, float4 a2) {
+    if (m2 == -INFINITY) return;
+    if (m == -INFINITY) {
+        m = m2; l = l2; acc = a2;
+        return;
+    }
+    const float mn = fmaxf(m, m2);
+    const float f1 = exp2_safe(m - mn), f2 = exp2_safe(m2 - mn);
+    m = mn;
+    l = l * f1 + l2 * f2;
+    acc.x = acc.x * f1 + a2.x * f2;
+    acc.y = acc.y * f1 + a2.y * f2;
+    acc.z = acc.z * f1 + a2.z * f2;
+    acc.w = acc.w * f1 + a2.w * f2;
+}
+
 template <uint32_t D, bool APPEND>
 __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
     const uint32_t bh = blockIdx.x;
@@ -103,41 +124,26 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
     const uint32_t h = bh % a.g.kv_heads;
     const uint32_t G = a.group;
     const uint32_t GD = G * D;
-    const uint32_t e0 = blockIdx.y * 64;
-    if (e0 >= GD) return;
     const uint32_t tid = threadIdx.x;
-    const uint32_t e4 = tid & 15;
-    const uint32_t sg = tid >> 4;
-    const uint32_t e = e0 + e4 * 4;
-    const bool active = e < GD;
-    const uint32_t hn = active ? e / D : 0;
+    const uint32_t q = tid & 7, rg = tid >> 3;
+    const uint32_t e = blockIdx.y * 32 + 4 * q;  // < GD: the grid covers GD / 32 blocks
+    const uint32_t hn = (blockIdx.y * 32) / D;
     const size_t out_row0 = (static_cast<size_t>(b) * a.q_heads + static_cast<size_t>(h) * G) * D;
-
     const uint32_t rec = record_floats(G, D);
     const uint32_t slots = a.max_splits + 1;
     const float* part = a.part + (static_cast<size_t>(bh) * slots) * rec;
 
-    // The first kSpec records of this thread are fetched before the context length
-    // (and with it the record count) arrives; records past the count are ignored.
-    // 16 * kSpec = 80 covers a single sequence's 64 splits plus the fused append's
-    // record, so none of them waits for the length (a 65th record fetched after it
-    // added one dependent memory round trip to the combine).
-#ifndef MIIKV_COMBINE_SPEC
-#define MIIKV_COMBINE_SPEC 5
-#endif
-    constexpr uint32_t kSpec = MIIKV_COMBINE_SPEC;
-    // The gate of this thread's outputs (split group 0 writes them) goes out with the
-    // records, so the epilogue does not wait for it.
+    constexpr uint32_t kSpec = 3;
     float gv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (a.gate != nullptr && sg == 0 && active) {
-#pragma unroll
-        for (uint32_t k = 0; k < 4; ++k) gv[k] = a.gate[out_row0 + e + k];
+    if (a.gate != nullptr && tid < 8) {
+        const float4 g4 = *reinterpret_cast<const float4*>(a.gate + out_row0 + e);
+        gv[0] = g4.x; gv[1] = g4.y; gv[2] = g4.z; gv[3] = g4.w;
     }
     float ms[kSpec], ls[kSpec];
     float4 vv[kSpec];
 #pragma unroll
     for (uint32_t j = 0; j < kSpec; ++j) {
-        const uint32_t sp = sg + 16 * j;
+        const uint32_t sp = rg + 32 * j;
         ms[j] = -INFINITY;
         ls[j] = 0.0f;
         vv[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -145,7 +151,7 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
             const float* r = part + static_cast<size_t>(sp) * rec;
             ms[j] = r[GD + hn];
             ls[j] = r[GD + G + hn];
-            if (active) vv[j] = *reinterpret_cast<const float4*>(r + e);
+            vv[j] = *reinterpret_cast<const float4*>(r + e);
         }
     }
     const uint32_t cpw = launch_cpw(a);
@@ -153,70 +159,52 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
     const uint32_t L = split_length(a, b);
     const uint32_t nrec = split_count(L, cpw) + (APPEND && L > 0 ? 1u : 0u);
 
-    float mloc = -INFINITY;
-    float lsum = 0.0f;
+    float m = -INFINITY, l = 0.0f;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    auto merge = [&](float m_s, float l_s, float4 v) {
-        if (m_s == -INFINITY) return;  // a split with no key (possible with the fused append)
-        const float mn = fmaxf(mloc, m_s);
-        const float fo = exp2_safe(mloc - mn);  // 0 on the first split
-        const float fs = exp2_safe(m_s - mn);
-        mloc = mn;
-        lsum = lsum * fo + l_s * fs;
-        acc.x = acc.x * fo + v.x * fs;
-        acc.y = acc.y * fo + v.y * fs;
-        acc.z = acc.z * fo + v.z * fs;
-        acc.w = acc.w * fo + v.w * fs;
-    };
 #pragma unroll
     for (uint32_t j = 0; j < kSpec; ++j)
-        if (sg + 16 * j < nrec) merge(ms[j], ls[j], vv[j]);
-    for (uint32_t sp = sg + 16 * kSpec; sp < nrec; sp += 16) {
+        if (rg + 32 * j < nrec) merge_state(m, l, acc, ms[j], ls[j], vv[j]);
+    for (uint32_t sp = rg + 32 * kSpec; sp < nrec; sp += 32) {
         const float* r = part + static_cast<size_t>(sp) * rec;
-        merge(r[GD + hn], r[GD + G + hn],
-              active ? *reinterpret_cast<const float4*>(r + e) : make_float4(0.f, 0.f, 0.f, 0.f));
+        merge_state(m, l, acc, r[GD + hn], r[GD + G + hn], *reinterpret_cast<const float4*>(r + e));
     }
-    __shared__ float4 s_acc[16][16];
-    __shared__ float s_gm[16][16];
-    __shared__ float s_gl[16][16];
-    s_acc[sg][e4] = acc;
-    s_gm[sg][e4] = mloc;
-    s_gl[sg][e4] = lsum;
+    // Butterfly over the 8 record groups of this wave (lanes 8, 16, 32 apart).
+#pragma unroll
+    for (uint32_t off = 8; off < 64; off <<= 1) {
+        const float m2 = __shfl_xor(m, off), l2 = __shfl_xor(l, off);
+        float4 a2;
+        a2.x = __shfl_xor(acc.x, off);
+        a2.y = __shfl_xor(acc.y, off);
+        a2.z = __shfl_xor(acc.z, off);
+        a2.w = __shfl_xor(acc.w, off);
+        merge_state(m, l, acc, m2, l2, a2);
+    }
+    __shared__ float4 s_acc[4][8];
+    __shared__ float s_m[4][8], s_l[4][8];
+    const uint32_t wave = tid >> 6;
+    if ((tid & 63) < 8) {
+        s_acc[wave][q] = acc;
+        s_m[wave][q] = m;
+        s_l[wave][q] = l;
+    }
     __syncthreads();
-    if (sg != 0 || !active) return;
-    float M = -INFINITY;
+    if (tid >= 8) return;
 #pragma unroll
-    for (uint32_t g = 0; g < 16; ++g) M = fmaxf(M, s_gm[g][e4]);
-    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    float Ls = 0.0f;
-#pragma unroll
-    for (uint32_t g = 0; g < 16; ++g) {
-        const float mg = s_gm[g][e4];
-        if (mg == -INFINITY) continue;  // split group without splits
-        const float f = exp2_safe(mg - M);
-        const float4 v = s_acc[g][e4];
-        o.x += f * v.x;
-        o.y += f * v.y;
-        o.z += f * v.z;
-        o.w += f * v.w;
-        Ls += f * s_gl[g][e4];
-    }
+    for (uint32_t w = 1; w < 4; ++w) merge_state(m, l, acc, s_m[w][q], s_l[w][q], s_acc[w][q]);
     // out = acc / L, 0 when L == 0 (qwen3_primitives.hip:2349); gated = out * sigmoid(gate).
-    const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
-    const float vals[4] = {o.x * inv, o.y * inv, o.z * inv, o.w * inv};
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const float vals[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
     float gated[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (a.out) *reinterpret_cast<float4*>(a.out + out_row0 + e) = make_float4(vals[0], vals[1], vals[2], vals[3]);
+    if (a.gate) {
 #pragma unroll
-    for (uint32_t k = 0; k < 4; ++k) {
-        const size_t oi = out_row0 + e + k;
-        if (a.out) a.out[oi] = vals[k];
-        if (a.gate) {
-            gated[k] = vals[k] * (1.0f / (1.0f + expf(-gv[k])));
-            if (a.gated_out) a.gated_out[oi] = gated[k];
-        }
+        for (uint32_t k = 0; k < 4; ++k) gated[k] = vals[k] * (1.0f / (1.0f + expf(-gv[k])));
+        if (a.gated_out)
+            *reinterpret_cast<float4*>(a.gated_out + out_row0 + e) = make_float4(gated[0], gated[1], gated[2], gated[3]);
     }
     if (a.gate && a.gated_q8_1) {
-        // Q8_1 block of 32 gated values = 8 consecutive lanes (qwen3_primitives.hip:
-        // 2354-2384): d = amax/127, q = clamp(roundf(x/d), -127, 127), s = sum(q)*d.
+        // Q8_1 block of these 32 gated values (qwen3_primitives.hip:2354-2384):
+        // d = amax/127, q = clamp(roundf(x/d), -127, 127), s = sum(q)*d.
         float amax = fmaxf(fmaxf(fabsf(gated[0]), fabsf(gated[1])), fmaxf(fabsf(gated[2]), fabsf(gated[3])));
         amax = group_reduce<8>(amax, MaxOp{});
         const float d = amax / 127.0f;
@@ -229,12 +217,12 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
             sum += qs[k];
         }
         sum = group_reduce<8>(sum, AddOp{});
-        const size_t blk = (out_row0 + e) / 32;
+        const size_t blk = (out_row0 + blockIdx.y * 32) / 32;
         uint8_t* bp = a.gated_q8_1 + blk * 36;
-        *reinterpret_cast<uint32_t*>(bp + 4 + 4 * (e4 & 7)) =
+        *reinterpret_cast<uint32_t*>(bp + 4 + 4 * q) =
             (static_cast<uint32_t>(qs[0]) & 0xffu) | ((static_cast<uint32_t>(qs[1]) & 0xffu) << 8) |
             ((static_cast<uint32_t>(qs[2]) & 0xffu) << 16) | ((static_cast<uint32_t>(qs[3]) & 0xffu) << 24);
-        if ((e4 & 7) == 0) {
+        if (q == 0) {
             *reinterpret_cast<uint16_t*>(bp) = f32_to_f16_bits(d);
             *reinterpret_cast<uint16_t*>(bp + 2) = f32_to_f16_bits(static_cast<float>(sum) * d);
         }
