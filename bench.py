@@ -42,33 +42,42 @@ def append_bytes(hkv=HKV, d=D) -> int:
     return 2 * hkv * d * 2 + kv_bytes_per_token(hkv, d)
 
 
-def cpu_baseline(ctx_cpu: int = 32768) -> dict:
-    """The same decode workload on the host CPU: the oracle's C restatement of the reference
-    CPU attention path (fp32 loop over a dequantised cache, double-denominator softmax)."""
+def _cpu_case(ctx, seed, threads, warmup, reps):
     import numpy as np
 
     import oracle
-    rng = np.random.default_rng(1)
-    k = rng.standard_normal((HKV, ctx_cpu, D)).astype(np.float32).astype(np.float16)
-    v = rng.standard_normal((HKV, ctx_cpu, D)).astype(np.float32).astype(np.float16)
+    rng = np.random.default_rng(seed)
+    k = rng.standard_normal((HKV, ctx, D)).astype(np.float32).astype(np.float16)
+    v = rng.standard_normal((HKV, ctx, D)).astype(np.float32).astype(np.float16)
     q = rng.standard_normal((HQ, D)).astype(np.float32).astype(np.float16).astype(np.float32)
     kc, ks = oracle.quantize_rows(k)
     vc, vs = oracle.quantize_rows(v)
-    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    cores = max(1, min(cores, 16))
-    t1 = oracle.time_attention_q8(q, kc, ks, vc, vs, ctx_cpu, HQ, 1 / math.sqrt(D), threads=1,
-                                  warmup=1, reps=3)
-    tn = oracle.time_attention_q8(q, kc, ks, vc, vs, ctx_cpu, HQ, 1 / math.sqrt(D),
-                                  threads=cores, warmup=2, reps=10)
-    b = decode_bytes(ctx_cpu)
+    return oracle.time_attention_q8(q, kc, ks, vc, vs, ctx, HQ, 1 / math.sqrt(D), threads=threads,
+                                    warmup=warmup, reps=reps)
+
+
+def cpu_baseline() -> dict:
+    """BASELINE config 1 on the host CPU: the oracle's C restatement of the reference
+    CPU attention path (fp32 loop over a dequantised cache, double-denominator softmax),
+    32q/8kv/D128, one fp16 query, context 4096; plus the GPU headline's context (32768)."""
+    nproc = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = max(1, min(nproc, HQ))  # the port splits query heads over threads
+    t1 = _cpu_case(4096, 1, 1, 3, 20)
+    tn = _cpu_case(4096, 1, threads, 3, 20)
+    t32 = _cpu_case(32768, 1, threads, 2, 10)
+    b = decode_bytes(4096)
     return {
-        "value": round(b / tn / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+        "value": round(b / tn / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "host_cores_nproc": nproc,
         "us_per_layer_token": round(tn * 1e6, 1),
         "single_thread": {"value": round(b / t1 / 1e9, 3), "us_per_layer_token": round(t1 * 1e6, 1)},
-        "sample": f"32q/8kv/D128 q8_0 decode, one query token, context {ctx_cpu} (the GPU "
-                  f"workload, attention only): median of 10 calls after 2 warm-ups on {cores} "
-                  "threads (query heads split), median of 3 calls on 1 thread; the cache is "
-                  "dequantised to fp32 once, outside timing, as the reference CPU path holds it",
+        "context_32768": {"value": round(decode_bytes(32768) / t32 / 1e9, 3),
+                          "us_per_layer_token": round(t32 * 1e6, 1), "cores": threads},
+        "sample": f"config 1: 32q/8kv/D128 q8_0 decode, one query token, context 4096, attention "
+                  f"only: median of 20 calls after 3 warm-ups on {threads} threads (query heads "
+                  f"split; {nproc} cores available) and on 1 thread; context 32768 median of 10 "
+                  "after 2; the cache is dequantised to fp32 once, outside timing, as the reference "
+                  "CPU path holds it",
     }
 
 
@@ -469,8 +478,8 @@ def traffic_from_profile():
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=6400)
+    ap.add_argument("--warmup", type=int, default=640)
     ap.add_argument("--context", type=int, default=32768)
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
@@ -483,6 +492,8 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a 256 MiB device copy (known bytes) to calibrate PMC counters")
     args = ap.parse_args()
+    if args.steps < 1:
+        ap.error("--steps must be at least 1")
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this path runs on a single MI355X "
               "(it would shard by kv head or by sequence with no exchange; only one GPU's share runs here)", file=sys.stderr)
@@ -549,55 +560,87 @@ def main() -> int:
             raise RuntimeError(f"launch failed: {st}")
 
     stream = torch.cuda.Stream()
-    graph_steps = nl * 8  # one graph = 8 rounds over the layer caches
+    graph_steps = nl * 8  # one full graph = 8 rounds over the layer caches
 
-    def make_graph(fn):
+    def make_graph(fn, n):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=stream):
-            for i in range(graph_steps):
+            for i in range(n):
                 fn(i, torch.cuda.current_stream())
         return g
 
     use_graph = not args.no_graph
+    full, rem = divmod(args.steps, graph_steps)
     graphs = {}
     if use_graph:
         try:
-            graphs["step"] = make_graph(step)
-            graphs["decode"] = make_graph(decode_only)
+            for kind, fn in (("step", step), ("decode", decode_only)):
+                graphs[kind] = make_graph(fn, graph_steps)
+                if rem:
+                    graphs[kind + "_rem"] = make_graph(fn, rem)
         except Exception as e:  # pragma: no cover - reported, then eager launches
             print(f"graph capture failed ({e}); timing eager launches", file=sys.stderr)
             use_graph = False
 
-    def run(kind, nsteps):
-        """Run nsteps steps of `kind` on `stream`; returns elapsed ms (HIP events)."""
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
+    def run(kind, nsteps, timed=True):
+        """Run exactly nsteps steps of `kind` on `stream`: full graph replays, then one
+        replay of the remainder graph.  Returns (total ms, per-replay us per step of the
+        full replays, or of the remainder when there is none)."""
+        nfull, nrem = divmod(nsteps, graph_steps)
+        marks = []
         with torch.cuda.stream(stream):
-            reps = max(1, nsteps // graph_steps) if use_graph else nsteps
-            e0.record(stream)
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record(stream)
+            marks.append(ev)
             if use_graph:
-                for _ in range(reps):
+                for _ in range(nfull):
                     graphs[kind].replay()
+                    ev = torch.cuda.Event(enable_timing=True)
+                    ev.record(stream)
+                    marks.append(ev)
+                if nrem:
+                    (graphs[kind + "_rem"] if nrem == rem else make_graph(
+                        step if kind == "step" else decode_only, nrem)).replay()
+                    ev = torch.cuda.Event(enable_timing=True)
+                    ev.record(stream)
+                    marks.append(ev)
             else:
                 fn = step if kind == "step" else decode_only
-                for i in range(reps):
+                for i in range(nsteps):
                     fn(i, stream)
-            e1.record(stream)
-        e1.synchronize()
-        done = reps * graph_steps if use_graph else reps
-        return e0.elapsed_time(e1), done
+                ev = torch.cuda.Event(enable_timing=True)
+                ev.record(stream)
+                marks.append(ev)
+        marks[-1].synchronize()
+        total = marks[0].elapsed_time(marks[-1])
+        if not timed:
+            return total, []
+        if use_graph and nfull:
+            per = [marks[i].elapsed_time(marks[i + 1]) * 1e3 / graph_steps for i in range(nfull)]
+        else:
+            per = [total * 1e3 / nsteps]
+        return total, per
 
-    run("step", args.warmup)
-    run("decode", args.warmup)
+    def stats(per):
+        per = sorted(per)
+        return per[len(per) // 2], per[len(per) // 10], per[(9 * len(per)) // 10]
+
+    # At least --warmup steps, in whole replays and no fewer than five (clocks and the
+    # graphs' first-replay upload settle), and one replay of each remainder graph.
+    warm = max(-(-max(args.warmup, 1) // graph_steps), 5) * graph_steps
+    for kind in ("step", "decode"):
+        run(kind, warm, timed=False)
+        if rem:
+            run(kind, rem, timed=False)
     torch.cuda.synchronize()
     t_start = time.perf_counter()
-    ms, done = run("step", args.steps)
+    ms, per = run("step", args.steps)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_start
-    ms_dec, done_dec = run("decode", args.steps)
+    ms_dec, per_dec = run("decode", args.steps)
 
-    us_step = ms * 1e3 / done
-    us_dec = ms_dec * 1e3 / done_dec
+    us_step, us_p10, us_p90 = stats(per)
+    us_dec, us_dec_p10, us_dec_p90 = stats(per_dec)
     step_bytes = decode_bytes(ctx) + append_bytes()
     value = step_bytes / (us_step * 1e-6) / 1e9
     dec_gbs = decode_bytes(ctx) / (us_dec * 1e-6) / 1e9
@@ -610,10 +653,19 @@ def main() -> int:
         "value": round(value, 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": done,
+        "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(us_step / 1e3, 6),
         "us_per_layer_token": round(us_step, 3),
+        "us_per_layer_token_p10": round(us_p10, 3),
+        "us_per_layer_token_p90": round(us_p90, 3),
+        "timing": {"steps_requested": args.steps, "steps_timed": args.steps,
+                   "timed_ms_total": round(ms, 4), "mean_us_per_step": round(ms * 1e3 / args.steps, 3),
+                   "samples": len(per),
+                   "protocol": f"exactly --steps steps: graph replays of {graph_steps} steps "
+                               f"(8 rounds over {nl} rotated layer caches) plus one remainder replay, "
+                               "HIP events around each replay; value and us_per_layer_token are the "
+                               "median over the full replays (p10/p90 beside them)"},
         "pct_hbm_peak": round(100 * value / PEAK_HBM_GBS, 2),
         "higher_is_better": True,
         "scaling": "weak",
@@ -631,7 +683,8 @@ def main() -> int:
                      "algorithmic_bytes_per_launch": step_bytes,
                      "avg_launch_us": round(us_step, 3)},
         "decode_only": {"kernel": "miikv_decode_attn = decode_kernel<128,false,false> + combine_kernel<128>",
-                        "avg_launch_us": round(us_dec, 3), "GBs": round(dec_gbs, 1),
+                        "avg_launch_us": round(us_dec, 3), "p10_us": round(us_dec_p10, 3),
+                        "p90_us": round(us_dec_p90, 3), "GBs": round(dec_gbs, 1),
                         "algorithmic_bytes_per_launch": decode_bytes(ctx)},
     }
     line["roofline"]["stream_read_ceiling"] = stream_read_ceiling(dev, decode_bytes(ctx))
