@@ -159,3 +159,34 @@ def test_fused_append_q8_1_epilogue_and_empty_sequence(gpu):
     # the empty sequence's first slot keeps its bytes
     for a, b in zip(_canon(cache, 1, 1), before):
         assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("fused", [False, True])
+@pytest.mark.parametrize("length", [1, 8193, 16384])
+def test_decode_c2_16k_plan(gpu, fused, length):
+    """Config 2 at its middle context: a 16384-token cache with max_context 16384 runs
+    the plan the bench times there (two 32-token steps per wave, waves not interleaved)."""
+    import miinfer_amd as m
+    rng = np.random.default_rng(length + 16)
+    hq, hk, d, cap = 32, 8, 128, 16384
+    cache = m.KvCache.contiguous(hk, d, cap)
+    k = randn_f16(rng, (length, hk, d))
+    v = randn_f16(rng, (length, hk, d))
+    n_cached = length - 1 if fused else length
+    for t0 in range(0, n_cached, 8192):
+        n = min(8192, n_cached - t0)
+        cache.append(_dev(k[t0:t0 + n], gpu), _dev(v[t0:t0 + n], gpu), base_position=t0)
+    q = randn_f16(rng, (1, hq, d))
+    lens = torch.tensor([length], dtype=torch.int32, device=gpu)
+    extra = dict(k_new=_dev(k[-1:], gpu), v_new=_dev(v[-1:], gpu)) if fused else {}
+    out, _ = m.decode_attention(cache, _dev(q, gpu), lengths=lens, max_context=cap, **extra)
+    torch.cuda.synchronize()
+    kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+    vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+    if fused:
+        got = _canon(cache, 0, length)
+        assert np.array_equal(got[0][:, -1], kc[:, -1]) and np.array_equal(got[2][:, -1], vc[:, -1])
+        assert np.array_equal(got[1][:, -1].view(np.uint16), ks[:, -1])
+        assert np.array_equal(got[3][:, -1].view(np.uint16), vs[:, -1])
+    expect = oracle.attention_q8(q[0].astype(np.float32), kc, ks, vc, vs, length, hq, 1 / math.sqrt(d))
+    assert_attention_close(out.cpu().numpy()[0], expect, f"L={length} fused={fused}")
