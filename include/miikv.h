@@ -2,10 +2,12 @@
  * miikv — MI355X-native (gfx950) quantized KV-cache path: C ABI.
  *
  * Launch-only, asynchronous entry points with plain pointers and sizes.  The
- * caller owns every device buffer (including the workspace); nothing here
- * allocates device memory.  Each entry point returns a miikv_status: 0 on
- * success, > 0 for an invalid argument (nothing was launched), < 0 for a HIP
- * error (the negated hipError_t).  The reference aborts the process on invalid
+ * caller owns every device buffer (including the workspace); no launch entry
+ * point allocates device memory.  The exceptions are the host-synchronous file
+ * calls miikv_session_save / miikv_session_load, which stage one layer through
+ * a device buffer they allocate and free (documented at each).  Each entry
+ * point returns a miikv_status: 0 on success, > 0 for an invalid argument
+ * (nothing was launched), < 0 for a HIP error (the negated hipError_t).  The reference aborts the process on invalid
  * arguments (include/miinfer/hip_check.hpp:11-38); this ABI reports instead.
  *
  * Streams are passed as `void*` holding a hipStream_t (NULL = default stream).
@@ -19,8 +21,11 @@
  * ---------------------------------------------------------------------------
  * The cache is a set of pages of `page_tokens` tokens (a multiple of 64).  A
  * CONTIGUOUS cache is the special case of a single page whose page_tokens is the
- * capacity, which reproduces the reference's [kv_head][capacity][head_dim]
- * ordering (include/miinfer/prefill_v2/kv_cache.hpp:24-46).  A PAGED cache maps
+ * capacity: its slabs are ordered [kv_head][capacity] like the reference's
+ * planes (include/miinfer/prefill_v2/kv_cache.hpp:24-46), but the bytes inside a
+ * slab are tiled as below, not [capacity][head_dim] row-major, so code that
+ * reads or writes the raw planes must go through miikv_export_canonical /
+ * miikv_import_canonical (or miikv_export_dequant).  A PAGED cache maps
  * logical page i of sequence b to physical page block_table[b*table_stride + i].
  *
  * Each of the four planes is [page][kv_head][slab]; one slab holds page_tokens
@@ -271,6 +276,14 @@ miikv_status miikv_export_canonical(const miikv_view* view, uint32_t seq, uint32
                                     uint32_t count, int8_t* k_codes, uint16_t* k_scales,
                                     int8_t* v_codes, uint16_t* v_scales, void* stream);
 
+/* Dequantised rows of tokens [t0, t0+count) of sequence `seq`: k_out / v_out
+ * device fp32 [kv_heads][count][head_dim] (16-byte aligned; either may be NULL),
+ * value = float(code) * float(scale).  The device half of the q8 branch of
+ * AttentionLayerKvCacheStorage::download_key / download_value
+ * (src/prefill_v2/kv_cache.cpp:132-212), for debug dumps and float read-back. */
+miikv_status miikv_export_dequant(const miikv_view* view, uint32_t seq, uint32_t t0, uint32_t count,
+                                  float* k_out, float* v_out, void* stream);
+
 /* Inverse of miikv_export_canonical (device half of upload_raw,
  * src/prefill_v2/kv_cache.cpp:299-369). */
 miikv_status miikv_import_canonical(const miikv_view* view, uint32_t seq, uint32_t t0,
@@ -314,10 +327,12 @@ uint32_t miikv_pool_refcount(const miikv_pool* pool, int32_t page);
 uint32_t miikv_pool_free_pages(const miikv_pool* pool);
 /* Fork a sequence of `length` tokens: child_row[0..pages) shares the parent's
  * full pages (reference +1); a partial last page gets a fresh page and one
- * (copy_src, copy_dst) pair to run with miikv_copy_pages. */
-miikv_status miikv_pool_fork(miikv_pool* pool, const int32_t* parent_row, uint32_t length,
-                             uint32_t page_tokens, int32_t* child_row, int32_t* copy_src,
-                             int32_t* copy_dst, uint32_t* n_copies);
+ * (copy_src, copy_dst) pair to run with miikv_copy_pages.  parent_row and
+ * child_row each hold row_capacity entries (MIIKV_EINVAL if the sequence needs
+ * more pages). */
+miikv_status miikv_pool_fork(miikv_pool* pool, const int32_t* parent_row, uint32_t row_capacity,
+                             uint32_t length, uint32_t page_tokens, int32_t* child_row,
+                             int32_t* copy_src, int32_t* copy_dst, uint32_t* n_copies);
 /* n forks of one parent in one call (child i's row at child_rows + i*row_stride,
  * row_stride >= pages of `length`); copy_src / copy_dst (capacity n) receive the
  * copy-on-write page pairs and *n_copies their count; *n_done forks completed
@@ -326,7 +341,9 @@ miikv_status miikv_pool_fork_n(miikv_pool* pool, const int32_t* parent_row, uint
                                uint32_t n, int32_t* child_rows, uint32_t row_stride, int32_t* copy_src,
                                int32_t* copy_dst, uint32_t* n_copies, uint32_t* n_done);
 /* Before appending at `position` (the sequence's current length): allocate a
- * fresh page at a page boundary, or copy a shared page (copy-on-write). */
+ * fresh page at a page boundary, or copy a shared page (copy-on-write).  Row
+ * entries not backing a token yet must be -1; an entry that already holds a page
+ * (a repeated call for the same position) keeps it, copied only if shared. */
 miikv_status miikv_pool_prepare_append(miikv_pool* pool, int32_t* row, uint32_t row_capacity,
                                        uint32_t position, uint32_t page_tokens,
                                        int32_t* copy_src, int32_t* copy_dst, uint32_t* n_copies);

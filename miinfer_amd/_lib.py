@@ -78,6 +78,7 @@ SIGNATURES = {
                                                  _U32, _P, _P, _P, _P, _P, _U64, _P]),
     "miikv_export_canonical": (ctypes.c_int, [_VP, _U32, _U32, _U32, _P, _P, _P, _P, _P]),
     "miikv_import_canonical": (ctypes.c_int, [_VP, _U32, _U32, _U32, _P, _P, _P, _P, _P]),
+    "miikv_export_dequant": (ctypes.c_int, [_VP, _U32, _U32, _U32, _P, _P, _P]),
     "miikv_copy_pages": (ctypes.c_int, [_VP, _P, _P, _U32, _P]),
     "miikv_copy_segments": (ctypes.c_int, [_P, _U32, _P]),
     "miikv_decode_state_advance": (ctypes.c_int, [_P, _P, _U32, _P, _U32, _P]),
@@ -91,7 +92,7 @@ SIGNATURES = {
     "miikv_pool_unref": (ctypes.c_int, [_P, ctypes.c_int32]),
     "miikv_pool_refcount": (_U32, [_P, ctypes.c_int32]),
     "miikv_pool_free_pages": (_U32, [_P]),
-    "miikv_pool_fork": (ctypes.c_int, [_P, _P, _U32, _U32, _P, _P, _P, _P]),
+    "miikv_pool_fork": (ctypes.c_int, [_P, _P, _U32, _U32, _U32, _P, _P, _P, _P]),
     "miikv_pool_fork_n": (ctypes.c_int, [_P, _P, _U32, _U32, _U32, _P, _U32, _P, _P, _P, _P]),
     "miikv_pool_prepare_append": (ctypes.c_int, [_P, _P, _U32, _U32, _U32, _P, _P, _P]),
     "miikv_pool_release": (ctypes.c_int, [_P, _P, _U32, _U32]),

@@ -355,6 +355,53 @@ __global__ void __launch_bounds__(256) canonical_kernel(
     }
 }
 
+// Tiled -> dequantised fp32 rows [kv_head][count][head_dim], value = float(code) *
+// float(scale) (src/prefill_v2/kv_cache.cpp:161-169), one thread per (token, kv head,
+// 16-dim group).
+__global__ void __launch_bounds__(256) dequant_kernel(Geo g, uint32_t seq, uint32_t t0, uint32_t count,
+                                                      float* kout, float* vout) {
+    const uint32_t D = g.head_dim;
+    const uint32_t groups = D / 16;
+    const uint64_t gid = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const uint64_t total = static_cast<uint64_t>(count) * g.kv_heads * groups;
+    if (gid >= total) return;
+    const uint32_t q16 = static_cast<uint32_t>(gid % groups);
+    const uint64_t r = gid / groups;
+    const uint32_t t = static_cast<uint32_t>(r % count);
+    const uint32_t head = static_cast<uint32_t>(r / count);
+    const uint32_t pos = t0 + t;
+    const size_t slab = slab_of(g, seq, pos, head);
+    const uint32_t tp = pos % g.page_tokens;
+    const size_t slab_bytes = static_cast<size_t>(g.page_tokens) * D;
+    const uint32_t d0 = q16 * 16;
+    const size_t row = (static_cast<size_t>(head) * count + t) * D + d0;
+    const size_t sidx = (slab * g.page_tokens + tp) * (D / 32) + d0 / 32;
+    if (kout != nullptr) {
+        const int8_t* kslab = g.k_codes + slab * slab_bytes;
+        const uint2 a = *reinterpret_cast<const uint2*>(kslab + k_code_offset(tp, d0, D));
+        const uint2 b = *reinterpret_cast<const uint2*>(kslab + k_code_offset(tp, d0 + 8, D));
+        const uint32_t w[4] = {a.x, a.y, b.x, b.y};
+        const float sc = f16_bits_to_f32(g.k_scales[sidx]);
+        float4* o = reinterpret_cast<float4*>(kout + row);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            o[i] = make_float4(static_cast<float>(static_cast<int8_t>(w[i] & 0xffu)) * sc,
+                               static_cast<float>(static_cast<int8_t>((w[i] >> 8) & 0xffu)) * sc,
+                               static_cast<float>(static_cast<int8_t>((w[i] >> 16) & 0xffu)) * sc,
+                               static_cast<float>(static_cast<int8_t>(w[i] >> 24)) * sc);
+    }
+    if (vout != nullptr) {
+        const int8_t* vslab = g.v_codes + slab * slab_bytes;
+        const float sc = f16_bits_to_f32(g.v_scales[sidx]);
+        float x[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) x[i] = static_cast<float>(vslab[v_code_offset(tp, d0 + i, D)]) * sc;
+        float4* o = reinterpret_cast<float4*>(vout + row);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = make_float4(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+    }
+}
+
 // Copy [src, src+bytes) to dst with 16-byte vectors; `bytes` is a multiple of 16.
 __device__ __forceinline__ void copy16(uint4* __restrict__ dst, const uint4* __restrict__ src, uint64_t n16,
                                        uint64_t start, uint64_t stride) {
@@ -598,6 +645,22 @@ extern "C" miikv_status miikv_import_canonical(const miikv_view* view, uint32_t 
     return launch_canonical<false>(view, seq, t0, count, const_cast<int8_t*>(k_codes),
                                    const_cast<uint16_t*>(k_scales), const_cast<int8_t*>(v_codes),
                                    const_cast<uint16_t*>(v_scales), stream);
+}
+
+extern "C" miikv_status miikv_export_dequant(const miikv_view* view, uint32_t seq, uint32_t t0, uint32_t count,
+                                             float* k_out, float* v_out, void* stream) {
+    const int st = validate_view(view);
+    if (st != MIIKV_OK) return st;
+    if (static_cast<uint64_t>(t0) + count > view_seq_capacity(view)) return MIIKV_EINVAL;
+    if (view->layout == MIIKV_LAYOUT_CONTIGUOUS && seq != 0) return MIIKV_EINVAL;
+    if ((reinterpret_cast<uintptr_t>(k_out) | reinterpret_cast<uintptr_t>(v_out)) & 15u) return MIIKV_EINVAL;
+    const uint64_t threads = static_cast<uint64_t>(count) * view->kv_heads * (view->head_dim / 16);
+    if (threads == 0 || (k_out == nullptr && v_out == nullptr)) return MIIKV_OK;
+    const uint64_t blocks = (threads + 255) / 256;
+    if (blocks > 0x7fffffffu) return MIIKV_EINVAL;
+    hipLaunchKernelGGL(dequant_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), make_geo(*view), seq, t0, count, k_out, v_out);
+    return launch_status();
 }
 
 extern "C" miikv_status miikv_copy_pages(const miikv_view* view, const int32_t* d_src_pages,

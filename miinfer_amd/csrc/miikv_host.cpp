@@ -69,14 +69,15 @@ static uint32_t pages_for(uint32_t tokens, uint32_t page_tokens) {
     return (tokens + page_tokens - 1) / page_tokens;
 }
 
-extern "C" miikv_status miikv_pool_fork(miikv_pool* p, const int32_t* parent_row, uint32_t length,
-                                        uint32_t page_tokens, int32_t* child_row, int32_t* copy_src,
-                                        int32_t* copy_dst, uint32_t* n_copies) {
+extern "C" miikv_status miikv_pool_fork(miikv_pool* p, const int32_t* parent_row, uint32_t row_capacity,
+                                        uint32_t length, uint32_t page_tokens, int32_t* child_row,
+                                        int32_t* copy_src, int32_t* copy_dst, uint32_t* n_copies) {
     if (p == nullptr || page_tokens == 0 || (length > 0 && (parent_row == nullptr || child_row == nullptr)) ||
         n_copies == nullptr)
         return MIIKV_EINVAL;
     *n_copies = 0;
     const uint32_t np = pages_for(length, page_tokens);
+    if (np > row_capacity) return MIIKV_EINVAL;  // both rows hold row_capacity entries
     for (uint32_t i = 0; i < np; ++i)
         if (!valid_page(p, parent_row[i]) || p->refs[static_cast<size_t>(parent_row[i])] == 0) return MIIKV_EINVAL;
     const bool partial = (length % page_tokens) != 0;
@@ -116,7 +117,7 @@ extern "C" miikv_status miikv_pool_fork_n(miikv_pool* p, const int32_t* parent_r
     for (uint32_t i = 0; i < n; ++i) {
         uint32_t c = 0;
         const miikv_status st =
-            miikv_pool_fork(p, parent_row, length, page_tokens, child_rows + static_cast<size_t>(i) * row_stride,
+            miikv_pool_fork(p, parent_row, row_stride, length, page_tokens, child_rows + static_cast<size_t>(i) * row_stride,
                             copy_src ? copy_src + *n_copies : nullptr, copy_dst ? copy_dst + *n_copies : nullptr, &c);
         if (st != MIIKV_OK) return st;
         *n_copies += c;
@@ -132,8 +133,10 @@ extern "C" miikv_status miikv_pool_prepare_append(miikv_pool* p, int32_t* row, u
     *n_copies = 0;
     const uint32_t i = position / page_tokens;
     if (i >= row_capacity) return MIIKV_EINVAL;
-    if (position % page_tokens == 0) {
+    if (position % page_tokens == 0 && row[i] < 0) {
         // First token of a new page: allocate it (a shared full page is never written).
+        // An entry that already names a page (a repeated call) is handled below, so the
+        // page it holds is neither leaked nor replaced.
         const int32_t fresh = miikv_pool_alloc(p);
         if (fresh < 0) return MIIKV_EINVAL;
         row[i] = fresh;

@@ -9,9 +9,11 @@ through libmiikv; there is no fallback path.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import math
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -22,6 +24,13 @@ QBLOCK = 32
 
 def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p | None:
     return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _on_stream(stream):
+    """Context for allocating a launch's temporaries: with a caller stream they are
+    allocated while that stream is current, so the caching allocator does not hand
+    their memory out again before the work queued on it has run."""
+    return torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext()
 
 
 def _stream(stream) -> ctypes.c_void_p:
@@ -197,6 +206,35 @@ class KvCache:
              _ptr(vs), _stream(stream))
         return kc, ks, vc, vs
 
+    def export_dequant(self, seq: int, t0: int, count: int, keys: bool = True, values: bool = True,
+                       stream=None):
+        """Dequantised rows code * scale as fp32 device tensors [kv_heads, count, head_dim]
+        (None for a plane not asked for)."""
+        self._check_seq(seq)
+        dev = self.k_codes.device
+        shape = (self.kv_heads, count, self.head_dim)
+        with _on_stream(stream):
+            k = torch.empty(shape, dtype=torch.float32, device=dev) if keys else None
+            v = torch.empty(shape, dtype=torch.float32, device=dev) if values else None
+        call("miikv_export_dequant", self.view, seq, t0, count, _ptr(k), _ptr(v), _stream(stream))
+        return k, v
+
+    def download_key(self, tokens: int, seq: int = 0) -> np.ndarray:
+        """Host fp32 keys [kv_heads, tokens, head_dim] of positions [0, tokens): the
+        q8 branch of AttentionLayerKvCacheStorage::download_key
+        (src/prefill_v2/kv_cache.cpp:132-170), float(code) * float(scale)."""
+        if tokens > self.capacity:
+            raise ValueError("tokens exceeds capacity")
+        k, _ = self.export_dequant(seq, 0, tokens, values=False)
+        return k.cpu().numpy()
+
+    def download_value(self, tokens: int, seq: int = 0) -> np.ndarray:
+        """Host fp32 values, as download_key (kv_cache.cpp:172-210)."""
+        if tokens > self.capacity:
+            raise ValueError("tokens exceeds capacity")
+        _, v = self.export_dequant(seq, 0, tokens, keys=False)
+        return v.cpu().numpy()
+
     def import_canonical(self, seq: int, t0: int, kc, ks, vc, vs, stream=None) -> None:
         self._check_seq(seq)
         count = kc.shape[1]
@@ -303,15 +341,16 @@ def decode_attention(cache: KvCache, q: torch.Tensor, scale: float | None = None
         scale = 1.0 / math.sqrt(d)
     if max_context is None:
         max_context = cache.capacity
-    if workspace is None:
-        workspace = DecodeWorkspace(cache, q_heads, batch, max_context)
-    elif workspace.bytes < int(lib().miikv_decode_workspace_bytes(cache.view, q_heads, batch,
-                                                                   max_context)):
-        raise ValueError("workspace too small for this geometry")
-    if out is None and gate is None:
-        out = torch.empty((batch, q_heads, d), dtype=torch.float32, device=q.device)
-    if gate is not None and gated_out is None:
-        gated_out = torch.empty((batch, q_heads, d), dtype=torch.float32, device=q.device)
+    with _on_stream(stream):
+        if workspace is None:
+            workspace = DecodeWorkspace(cache, q_heads, batch, max_context)
+        elif workspace.bytes < int(lib().miikv_decode_workspace_bytes(cache.view, q_heads, batch,
+                                                                       max_context)):
+            raise ValueError("workspace too small for this geometry")
+        if out is None and gate is None:
+            out = torch.empty((batch, q_heads, d), dtype=torch.float32, device=q.device)
+        if gate is not None and gated_out is None:
+            gated_out = torch.empty((batch, q_heads, d), dtype=torch.float32, device=q.device)
     if gated_q8_1 is not None:
         if gate is None:
             raise ValueError("gated_q8_1 needs a gate")
@@ -363,18 +402,19 @@ def suffix_attention(cache: KvCache, q: torch.Tensor, base_position: int, scale:
         raise ValueError("prefill_state must be a 64-byte device buffer")
     if scale is None:
         scale = 1.0 / math.sqrt(d)
-    if out is None and gate is None:
-        out = torch.empty((t, q_heads, d), dtype=torch.float32, device=q.device)
-    if gate is not None and gated_out is None:
-        gated_out = torch.empty((t, q_heads, d), dtype=torch.float32, device=q.device)
     qd = _lib.DTYPE_F16 if q.dtype == torch.float16 else _lib.DTYPE_F32
-    if workspace is None:
-        if split:
-            need = suffix_workspace_bytes(cache, q_heads, t)
-        else:
-            bound = cache.capacity if prefill_state is not None else base_position + t
-            need = cache.kv_heads * ((bound + 31) // 32) * 2 * d * 32 * 2
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    with _on_stream(stream):
+        if out is None and gate is None:
+            out = torch.empty((t, q_heads, d), dtype=torch.float32, device=q.device)
+        if gate is not None and gated_out is None:
+            gated_out = torch.empty((t, q_heads, d), dtype=torch.float32, device=q.device)
+        if workspace is None:
+            if split:
+                need = suffix_workspace_bytes(cache, q_heads, t)
+            else:
+                bound = cache.capacity if prefill_state is not None else base_position + t
+                need = cache.kv_heads * ((bound + 31) // 32) * 2 * d * 32 * 2
+            workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
     ws_bytes = workspace.numel() * workspace.element_size()
     if (k_new is None) != (v_new is None):
         raise ValueError("k_new and v_new go together")

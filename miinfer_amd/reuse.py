@@ -12,7 +12,7 @@ import numpy as np
 import torch
 
 from ._lib import call, lib
-from .kv import KvCache, _ptr, _stream
+from .kv import KvCache, _on_stream, _ptr, _stream
 
 
 class MatchResult(enum.IntEnum):
@@ -65,8 +65,8 @@ class PagePool:
         src = np.zeros(1, np.int32)
         dst = np.zeros(1, np.int32)
         n = ctypes.c_uint32(0)
-        call("miikv_pool_fork", self._h, _i32p(parent_row), length, page_tokens, _i32p(child),
-             _i32p(src), _i32p(dst), ctypes.byref(n))
+        call("miikv_pool_fork", self._h, _i32p(parent_row), parent_row.size, length, page_tokens,
+             _i32p(child), _i32p(src), _i32p(dst), ctypes.byref(n))
         return child, [(int(src[0]), int(dst[0]))] if n.value else []
 
     def fork_many(self, parent_row: np.ndarray, length: int, page_tokens: int, n: int):
@@ -106,8 +106,9 @@ def run_page_copies(cache: KvCache, copies, stream=None) -> None:
     if not copies:
         return
     dev = cache.k_codes.device
-    src = torch.tensor([c[0] for c in copies], dtype=torch.int32, device=dev)
-    dst = torch.tensor([c[1] for c in copies], dtype=torch.int32, device=dev)
+    with _on_stream(stream):  # the page lists live until the copy has run on `stream`
+        src = torch.tensor([c[0] for c in copies], dtype=torch.int32, device=dev)
+        dst = torch.tensor([c[1] for c in copies], dtype=torch.int32, device=dev)
     cache.copy_pages(src, dst, stream)
 
 

@@ -231,3 +231,28 @@ def test_append_tile_path_matches_row_path(gpu, hk, d, monkeypatch):
     assert np.array_equal(vc[:, 45:345], evc) and np.array_equal(vs[:, 45:345], evs)
     ek, eks = oracle.quantize_rows_f32(k32[100:400].transpose(1, 0, 2))
     assert np.array_equal(kc[:, 445:745], ek) and np.array_equal(ks[:, 445:745], eks)
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_export_dequant_matches_oracle(gpu, paged):
+    """miikv_export_dequant / download_key / download_value: float(code) * float(scale)
+    rows, equal to the oracle's dequantisation of the oracle's codes (exact)."""
+    import miinfer_amd as m
+    rng = np.random.default_rng(21 + paged)
+    hk, d, n = 4, 256, 700
+    if paged:
+        table = np.array([[2, 0, 1]], np.int32)
+        cache = m.KvCache.paged_cache(hk, d, 3, torch.from_numpy(table).to(gpu), page_tokens=256)
+    else:
+        cache = m.KvCache.contiguous(hk, d, 768)
+    k = rng.standard_normal((n, hk, d)).astype(np.float32).astype(np.float16)
+    v = rng.standard_normal((n, hk, d)).astype(np.float32).astype(np.float16)
+    cache.append(torch.from_numpy(k).to(gpu), torch.from_numpy(v).to(gpu))
+    kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+    vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+    assert np.array_equal(cache.download_key(n), oracle.dequantize_rows(kc, ks))
+    assert np.array_equal(cache.download_value(n), oracle.dequantize_rows(vc, vs))
+    kd, vd = cache.export_dequant(0, 100, 300)
+    torch.cuda.synchronize()
+    assert np.array_equal(kd.cpu().numpy(), oracle.dequantize_rows(kc, ks)[:, 100:400])
+    assert np.array_equal(vd.cpu().numpy(), oracle.dequantize_rows(vc, vs)[:, 100:400])

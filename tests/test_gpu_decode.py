@@ -291,3 +291,34 @@ def test_decode_c2_capacity_32k_partial(gpu, length):
     kc, ks, vc, vs = _canon_tail(cache, 0, length)
     assert np.array_equal(kc, rk[0][:, -1:]) and np.array_equal(ks.view(np.uint16), rk[1][:, -1:])
     assert np.array_equal(vc, rv[0][:, -1:]) and np.array_equal(vs.view(np.uint16), rv[1][:, -1:])
+
+
+def test_side_stream_temporaries(gpu):
+    """Helpers given a side stream allocate their temporaries on it: decode attention
+    with an auto-allocated workspace and page copies run there and give the results of
+    the default-stream calls."""
+    import miinfer_amd as m
+    from miinfer_amd import reuse
+    rng = np.random.default_rng(11)
+    hq, hk, d, pt = 24, 4, 256, 256
+    table = np.array([[0, 1, 2], [3, 4, 5]], np.int32)
+    cache = m.KvCache.paged_cache(hk, d, 8, _dev(table, gpu), page_tokens=pt)
+    k = randn_f16(rng, (700, hk, d))
+    v = randn_f16(rng, (700, hk, d))
+    cache.append(_dev(k, gpu), _dev(v, gpu), base_position=0, seq=0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    reuse.run_page_copies(cache, [(0, 3), (1, 4), (2, 5)], stream=side)
+    q = _dev(randn_f16(rng, (2, hq, d)), gpu)
+    lens = torch.tensor([700, 700], dtype=torch.int32, device=gpu)
+    out_side, _ = m.decode_attention(cache, q, lengths=lens, max_context=3 * pt, stream=side)
+    side.synchronize()
+    out_ref, _ = m.decode_attention(cache, q, lengths=lens, max_context=3 * pt)
+    torch.cuda.synchronize()
+    assert torch.equal(out_side, out_ref)
+    kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+    vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+    for s in range(2):  # row 1 reads the copied pages
+        expect = oracle.attention_q8(q[s].cpu().numpy().astype(np.float32), kc, ks, vc, vs, 700, hq,
+                                     1 / math.sqrt(d))
+        assert_attention_close(out_ref[s].cpu().numpy(), expect, f"row {s}")

@@ -148,3 +148,30 @@ def test_fork_many_matches_repeated_fork():
     assert [a.refcount(p) for p in range(40)] == [b.refcount(p) for p in range(40)]
     with pytest.raises(MemoryError):
         PagePool(5).fork_many(np.array([0, 1, 2, 3], np.int32), length, pt, 3)
+
+
+def test_pool_fork_rejects_short_rows():
+    from miinfer_amd import MiikvError
+    from miinfer_amd import reuse
+    pool = reuse.PagePool(16)
+    row = np.array([pool.alloc() for _ in range(2)], np.int32)
+    with pytest.raises(MiikvError):  # 3 pages needed, the row holds 2
+        pool.fork(row, 600, 256)
+    assert pool.free_pages == 14
+
+
+def test_pool_prepare_append_twice_at_a_boundary_keeps_one_page():
+    from miinfer_amd import reuse
+    pool = reuse.PagePool(8)
+    row = np.full(4, -1, np.int32)
+    row[0] = pool.alloc()
+    assert pool.prepare_append(row, 256, 256) == []
+    page = int(row[1])
+    free = pool.free_pages
+    assert pool.prepare_append(row, 256, 256) == []  # again: the page it holds stays
+    assert int(row[1]) == page and pool.free_pages == free and pool.refcount(page) == 1
+    # a shared page at the boundary is copied, not leaked
+    child, _ = pool.fork(row, 512, 256)
+    assert pool.refcount(page) == 2
+    cps = pool.prepare_append(child, 256, 256)
+    assert cps == [(page, int(child[1]))] and pool.refcount(page) == 1
