@@ -231,6 +231,25 @@ miikv_status miikv_decode_append_attn(const miikv_view* view, const uint16_t* k_
                                       const float* gate, float* gated_out, void* gated_q8_1, void* workspace,
                                       uint64_t workspace_bytes, void* stream);
 
+/* miikv_decode_append_attn without the workspace arguments, for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference.  The split records go
+ * to a fixed device array inside the library, one per GPU, of
+ * miikv_decode_scratch_max_bytes() bytes (16 MiB: one 32q/8kv/D128 sequence at
+ * any context needs ~1.1 MB, 16 sequences of 24q/4kv/D256 up to 64k ~13 MB); a
+ * geometry whose
+ * miikv_decode_workspace_bytes() exceeds it returns MIIKV_EWORKSPACE.  Nothing is
+ * allocated (the array's address is looked up once per device).  All calls on one
+ * GPU share that array: calls that overlap on one GPU (other streams, other
+ * threads) race and must be serialised by the caller. */
+uint64_t miikv_decode_scratch_max_bytes(void);
+miikv_status miikv_decode_append_attn_noalloc(const miikv_view* view, const uint16_t* k_new,
+                                              const uint16_t* v_new, const void* q, uint32_t q_dtype,
+                                              uint32_t q_heads, float scale, uint32_t batch,
+                                              const uint32_t* d_lengths, const miikv_decode_state* decode_state,
+                                              uint32_t max_context, float* out, const float* gate,
+                                              float* gated_out, void* gated_q8_1, void* stream);
+
 /* ---- suffix (multi-token) attention over a cached prefix ----------------- */
 
 /* Causal attention of a token_count-token suffix whose rows already sit in the

@@ -39,6 +39,7 @@
 
 #include <cmath>
 #include <cstdlib>
+#include <mutex>
 #include <type_traits>
 
 namespace miikv {
@@ -863,3 +864,55 @@ extern "C" miikv_status miikv_decode_append_attn(const miikv_view* view, const u
                        out, gate, gated_out, gated_q8_1, workspace, workspace_bytes, stream);
 }
 
+
+// ---- decode without a caller workspace ---------------------------------------
+// The split records live in a file-scope device array instead of a caller
+// workspace.  Every GPU the library runs on holds its own copy until the process
+// ends; host code uses its per-device address from hipGetSymbolAddress, never the
+// array's name (a host-side stand-in that is not a device address).
+namespace {
+constexpr uint64_t kScratchBytes = 16ull << 20;
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_scratch_mutex;
+
+// Device address of this device's `scratch`, looked up once per device (with that
+// device current).  Returns a HIP status.
+int scratch_for_current_device(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e);
+    if (dev < 0 || dev >= kMaxDevices) return MIIKV_EUNSUPPORTED;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_status(e);
+        if (ptr == nullptr) return MIIKV_EUNSUPPORTED;
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return MIIKV_OK;
+}
+}  // namespace
+
+extern "C" uint64_t miikv_decode_scratch_max_bytes(void) { return kScratchBytes; }
+
+extern "C" miikv_status miikv_decode_append_attn_noalloc(const miikv_view* view, const uint16_t* k_new,
+                                                         const uint16_t* v_new, const void* q, uint32_t q_dtype,
+                                                         uint32_t q_heads, float scale, uint32_t batch,
+                                                         const uint32_t* d_lengths,
+                                                         const miikv_decode_state* decode_state,
+                                                         uint32_t max_context, float* out, const float* gate,
+                                                         float* gated_out, void* gated_q8_1, void* stream) {
+    if (k_new == nullptr || v_new == nullptr) return MIIKV_EINVAL;
+    const uint64_t need = miikv_decode_workspace_bytes(view, q_heads, batch, max_context);
+    if (need == 0) return MIIKV_EINVAL;
+    if (need > kScratchBytes) return MIIKV_EWORKSPACE;  // beyond the fixed scratch: use miikv_decode_append_attn
+    void* ptr = nullptr;
+    const int st = scratch_for_current_device(&ptr);
+    if (st != MIIKV_OK) return st;
+    return decode_impl(view, k_new, v_new, q, q_dtype, q_heads, scale, batch, d_lengths, decode_state, max_context,
+                       out, gate, gated_out, gated_q8_1, ptr, kScratchBytes, stream);
+}
