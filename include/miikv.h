@@ -394,6 +394,43 @@ uint32_t miikv_prefix_length(const miikv_prefix_ctx* ctx);
 uint64_t miikv_prefix_hash(const miikv_prefix_ctx* ctx);
 void miikv_prefix_set_layout_version(miikv_prefix_ctx* ctx, uint32_t version);
 
+/* Registry of several saved prefixes over one page pool (the reference keeps a
+ * single ReusableContext slot: src/prefill_v2/reusable_context.cpp:130-207, used
+ * by src/prefill_v2/model.cpp:752-871).  An entry holds the fingerprint (tokens,
+ * FNV-1a hash, layout version; model and quantization are the registry's) and
+ * one pool reference on each page of its row, so its KV pages outlive the
+ * session that wrote them.  `tag` is the caller's handle for the entry's
+ * recurrent-state checkpoint (device memory the caller owns).
+ *   save:    register tokens[0..count) held by row[0..pages); the same tokens
+ *            again refresh the existing entry; MIIKV_EWORKSPACE when full
+ *            (evict first).
+ *   lookup:  the longest entry whose prefix matches under check_match's rule
+ *            (reusable_context.cpp:155-185; strict != 0 also requires a shorter
+ *            prefix than the prompt, as generate() does); without a match the
+ *            verdict for the most recently used entry, EMPTY_CACHE when empty.
+ *   fork:    a session row from an entry (full pages shared, partial last page
+ *            copied: one (copy_src, copy_dst) pair for miikv_copy_pages).
+ *   release / evict_lru: drop an entry (its page references go back to the
+ *            pool); report its tag so the caller frees the checkpoint. */
+typedef struct miikv_registry miikv_registry;
+miikv_registry* miikv_registry_create(miikv_pool* pool, uint32_t page_tokens, uint32_t max_entries,
+                                      const char* model_id, const char* quantization);
+void miikv_registry_destroy(miikv_registry* reg);
+uint32_t miikv_registry_count(const miikv_registry* reg);
+miikv_status miikv_registry_save(miikv_registry* reg, const uint32_t* tokens, uint32_t count, const int32_t* row,
+                                 uint32_t row_capacity, uint64_t tag, uint32_t* entry_id_out);
+int miikv_registry_lookup(const miikv_registry* reg, const uint32_t* prompt, uint32_t count,
+                          const char* model_id, const char* quantization, uint32_t strict,
+                          uint32_t* entry_id_out, uint32_t* prefix_length_out);
+miikv_status miikv_registry_fork(miikv_registry* reg, uint32_t entry_id, int32_t* child_row,
+                                 uint32_t row_capacity, int32_t* copy_src, int32_t* copy_dst,
+                                 uint32_t* n_copies);
+miikv_status miikv_registry_release(miikv_registry* reg, uint32_t entry_id, uint64_t* tag_out);
+miikv_status miikv_registry_evict_lru(miikv_registry* reg, uint32_t* entry_id_out, uint64_t* tag_out);
+miikv_status miikv_registry_info(const miikv_registry* reg, uint32_t entry_id, uint32_t* length,
+                                 uint64_t* token_hash, uint64_t* tag, int32_t* pages, uint32_t pages_cap);
+miikv_status miikv_registry_set_layout_version(miikv_registry* reg, uint32_t entry_id, uint32_t version);
+
 /* ---- persistent session file (.miinfer) ----------------------------------- */
 
 /* On-disk session state, the reference's PersistentSessionHeader

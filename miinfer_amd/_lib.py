@@ -81,6 +81,16 @@ SIGNATURES = {
     "miikv_decode_scratch_max_bytes": (ctypes.c_uint64, []),
     "miikv_decode_append_attn_noalloc": (ctypes.c_int, [_VP, _P, _P, _P, _U32, _U32, ctypes.c_float, _U32, _P,
                                                          _P, _U32, _P, _P, _P, _P, _P]),
+    "miikv_registry_create": (ctypes.c_void_p, [_P, _U32, _U32, ctypes.c_char_p, ctypes.c_char_p]),
+    "miikv_registry_destroy": (None, [_P]),
+    "miikv_registry_count": (_U32, [_P]),
+    "miikv_registry_save": (ctypes.c_int, [_P, _P, _U32, _P, _U32, ctypes.c_uint64, _P]),
+    "miikv_registry_lookup": (ctypes.c_int, [_P, _P, _U32, ctypes.c_char_p, ctypes.c_char_p, _U32, _P, _P]),
+    "miikv_registry_fork": (ctypes.c_int, [_P, _U32, _P, _U32, _P, _P, _P]),
+    "miikv_registry_release": (ctypes.c_int, [_P, _U32, _P]),
+    "miikv_registry_evict_lru": (ctypes.c_int, [_P, _P, _P]),
+    "miikv_registry_info": (ctypes.c_int, [_P, _U32, _P, _P, _P, _P, _U32]),
+    "miikv_registry_set_layout_version": (ctypes.c_int, [_P, _U32, _U32]),
     "miikv_export_dequant": (ctypes.c_int, [_VP, _U32, _U32, _U32, _P, _P, _P]),
     "miikv_copy_pages": (ctypes.c_int, [_VP, _P, _P, _U32, _P]),
     "miikv_copy_segments": (ctypes.c_int, [_P, _U32, _P]),

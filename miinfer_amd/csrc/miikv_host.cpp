@@ -246,3 +246,202 @@ extern "C" uint64_t miikv_prefix_hash(const miikv_prefix_ctx* c) { return c ? c-
 extern "C" void miikv_prefix_set_layout_version(miikv_prefix_ctx* c, uint32_t version) {
     if (c) c->layout_version = version;
 }
+
+// ---------------------------------------------------------------------------
+// Prefix registry: several saved prefixes over one page pool.  Each entry keeps
+// the fingerprint of ReusableContext (model, quantization, layout version,
+// tokens + FNV-1a hash; reusable_context.hpp:17-129) and holds one reference on
+// every page of its page row, so its KV pages outlive the session that wrote
+// them; forks share the full pages and copy the partial last page, as
+// miikv_pool_fork does.  The reference keeps a single slot
+// (reusable_context.cpp:130-207, used by model.cpp:752-871); the registry applies
+// the same match rule to each entry and picks the longest matching prefix.
+// ---------------------------------------------------------------------------
+struct miikv_registry {
+    struct Entry {
+        uint32_t id;
+        std::vector<uint32_t> tokens;
+        uint64_t hash;
+        uint32_t layout_version;
+        std::vector<int32_t> pages;
+        uint64_t tag;
+        uint64_t last_use;
+    };
+    miikv_pool* pool = nullptr;
+    uint32_t page_tokens = 0;
+    uint32_t max_entries = 0;
+    std::string model_id;
+    std::string quantization;
+    std::vector<Entry> entries;
+    uint32_t next_id = 1;
+    uint64_t clock = 0;
+
+    Entry* find(uint32_t id) {
+        for (auto& e : entries)
+            if (e.id == id) return &e;
+        return nullptr;
+    }
+    void drop(size_t i) {
+        for (int32_t pg : entries[i].pages) miikv_pool_unref(pool, pg);
+        entries.erase(entries.begin() + static_cast<std::ptrdiff_t>(i));
+    }
+};
+
+extern "C" miikv_registry* miikv_registry_create(miikv_pool* pool, uint32_t page_tokens, uint32_t max_entries,
+                                                 const char* model_id, const char* quantization) {
+    if (pool == nullptr || page_tokens == 0 || max_entries == 0) return nullptr;
+    miikv_registry* r = new (std::nothrow) miikv_registry;
+    if (r == nullptr) return nullptr;
+    r->pool = pool;
+    r->page_tokens = page_tokens;
+    r->max_entries = max_entries;
+    r->model_id = model_id ? model_id : "";
+    r->quantization = quantization ? quantization : "";
+    return r;
+}
+
+extern "C" void miikv_registry_destroy(miikv_registry* r) {
+    if (r == nullptr) return;
+    while (!r->entries.empty()) r->drop(r->entries.size() - 1);
+    delete r;
+}
+
+extern "C" uint32_t miikv_registry_count(const miikv_registry* r) {
+    return r ? static_cast<uint32_t>(r->entries.size()) : 0u;
+}
+
+extern "C" miikv_status miikv_registry_save(miikv_registry* r, const uint32_t* tokens, uint32_t count,
+                                            const int32_t* row, uint32_t row_capacity, uint64_t tag,
+                                            uint32_t* entry_id_out) {
+    if (r == nullptr || count == 0 || tokens == nullptr || row == nullptr || entry_id_out == nullptr)
+        return MIIKV_EINVAL;
+    const uint32_t np = pages_for(count, r->page_tokens);
+    if (np > row_capacity) return MIIKV_EINVAL;
+    for (uint32_t i = 0; i < np; ++i)
+        if (!valid_page(r->pool, row[i]) || r->pool->refs[static_cast<size_t>(row[i])] == 0) return MIIKV_EINVAL;
+    // The same token sequence again: refresh the existing entry (its pages hold the
+    // same prefix), do not store a second copy.
+    const uint64_t hash = miikv_token_hash(tokens, count);
+    for (auto& e : r->entries) {
+        if (e.tokens.size() == count && e.hash == hash &&
+            std::memcmp(e.tokens.data(), tokens, sizeof(uint32_t) * count) == 0) {
+            e.last_use = ++r->clock;
+            *entry_id_out = e.id;
+            return MIIKV_OK;
+        }
+    }
+    if (r->entries.size() >= r->max_entries) return MIIKV_EWORKSPACE;  // full: evict first
+    miikv_registry::Entry e;
+    e.id = r->next_id++;
+    e.tokens.assign(tokens, tokens + count);
+    e.hash = hash;
+    e.layout_version = MIIKV_STATE_LAYOUT_VERSION;
+    e.pages.assign(row, row + np);
+    e.tag = tag;
+    e.last_use = ++r->clock;
+    for (int32_t pg : e.pages) miikv_pool_ref(r->pool, pg);
+    *entry_id_out = e.id;
+    r->entries.push_back(std::move(e));
+    return MIIKV_OK;
+}
+
+// The ReusableContext::check_match rule for one entry (reusable_context.cpp:155-185).
+static int registry_check(const miikv_registry& r, const miikv_registry::Entry& e, const uint32_t* prompt,
+                          uint32_t count, const char* model_id, const char* quantization) {
+    if (e.layout_version != MIIKV_STATE_LAYOUT_VERSION) return MIIKV_MATCH_VERSION_MISMATCH;
+    if (r.model_id != (model_id ? model_id : "")) return MIIKV_MATCH_MODEL_MISMATCH;
+    if (r.quantization != (quantization ? quantization : "")) return MIIKV_MATCH_QUANTIZATION_MISMATCH;
+    if (count < e.tokens.size()) return MIIKV_MATCH_PROMPT_SHORTER;
+    if (prompt == nullptr || std::memcmp(prompt, e.tokens.data(), sizeof(uint32_t) * e.tokens.size()) != 0)
+        return MIIKV_MATCH_PREFIX_MISMATCH;
+    return MIIKV_MATCH_EXACT;
+}
+
+extern "C" int miikv_registry_lookup(const miikv_registry* r, const uint32_t* prompt, uint32_t count,
+                                     const char* model_id, const char* quantization, uint32_t strict,
+                                     uint32_t* entry_id_out, uint32_t* prefix_length_out) {
+    if (entry_id_out) *entry_id_out = 0;
+    if (prefix_length_out) *prefix_length_out = 0;
+    if (r == nullptr || r->entries.empty()) return MIIKV_MATCH_EMPTY_CACHE;
+    const miikv_registry::Entry* best = nullptr;
+    const miikv_registry::Entry* recent = nullptr;
+    int recent_result = MIIKV_MATCH_EMPTY_CACHE;
+    for (const auto& e : r->entries) {
+        int res = registry_check(*r, e, prompt, count, model_id, quantization);
+        // strict: the prefix must leave at least one prompt token to run (model.cpp:758-763)
+        if (res == MIIKV_MATCH_EXACT && strict && e.tokens.size() >= count) res = MIIKV_MATCH_PROMPT_SHORTER;
+        if (res == MIIKV_MATCH_EXACT) {
+            if (best == nullptr || e.tokens.size() > best->tokens.size()) best = &e;
+        } else if (recent == nullptr || e.last_use > recent->last_use) {
+            recent = &e;
+            recent_result = res;
+        }
+    }
+    if (best == nullptr) return recent_result;  // the most recently used entry's verdict
+    if (entry_id_out) *entry_id_out = best->id;
+    if (prefix_length_out) *prefix_length_out = static_cast<uint32_t>(best->tokens.size());
+    return MIIKV_MATCH_EXACT;
+}
+
+extern "C" miikv_status miikv_registry_fork(miikv_registry* r, uint32_t entry_id, int32_t* child_row,
+                                            uint32_t row_capacity, int32_t* copy_src, int32_t* copy_dst,
+                                            uint32_t* n_copies) {
+    if (r == nullptr) return MIIKV_EINVAL;
+    miikv_registry::Entry* e = r->find(entry_id);
+    if (e == nullptr) return MIIKV_EINVAL;
+    if (row_capacity < e->pages.size()) return MIIKV_EINVAL;
+    const miikv_status st = miikv_pool_fork(r->pool, e->pages.data(), static_cast<uint32_t>(e->pages.size()),
+                                            static_cast<uint32_t>(e->tokens.size()), r->page_tokens, child_row,
+                                            copy_src, copy_dst, n_copies);
+    if (st == MIIKV_OK) e->last_use = ++r->clock;
+    return st;
+}
+
+extern "C" miikv_status miikv_registry_release(miikv_registry* r, uint32_t entry_id, uint64_t* tag_out) {
+    if (r == nullptr) return MIIKV_EINVAL;
+    for (size_t i = 0; i < r->entries.size(); ++i) {
+        if (r->entries[i].id == entry_id) {
+            if (tag_out) *tag_out = r->entries[i].tag;
+            r->drop(i);
+            return MIIKV_OK;
+        }
+    }
+    return MIIKV_EINVAL;
+}
+
+extern "C" miikv_status miikv_registry_evict_lru(miikv_registry* r, uint32_t* entry_id_out, uint64_t* tag_out) {
+    if (r == nullptr || r->entries.empty()) return MIIKV_EINVAL;
+    size_t lru = 0;
+    for (size_t i = 1; i < r->entries.size(); ++i)
+        if (r->entries[i].last_use < r->entries[lru].last_use) lru = i;
+    if (entry_id_out) *entry_id_out = r->entries[lru].id;
+    if (tag_out) *tag_out = r->entries[lru].tag;
+    r->drop(lru);
+    return MIIKV_OK;
+}
+
+extern "C" miikv_status miikv_registry_info(const miikv_registry* r, uint32_t entry_id, uint32_t* length,
+                                            uint64_t* token_hash, uint64_t* tag, int32_t* pages,
+                                            uint32_t pages_cap) {
+    if (r == nullptr) return MIIKV_EINVAL;
+    for (const auto& e : r->entries) {
+        if (e.id != entry_id) continue;
+        if (length) *length = static_cast<uint32_t>(e.tokens.size());
+        if (token_hash) *token_hash = e.hash;
+        if (tag) *tag = e.tag;
+        if (pages) {
+            if (pages_cap < e.pages.size()) return MIIKV_EINVAL;
+            std::memcpy(pages, e.pages.data(), sizeof(int32_t) * e.pages.size());
+        }
+        return MIIKV_OK;
+    }
+    return MIIKV_EINVAL;
+}
+
+extern "C" miikv_status miikv_registry_set_layout_version(miikv_registry* r, uint32_t entry_id, uint32_t version) {
+    if (r == nullptr) return MIIKV_EINVAL;
+    miikv_registry::Entry* e = r->find(entry_id);
+    if (e == nullptr) return MIIKV_EINVAL;
+    e->layout_version = version;
+    return MIIKV_OK;
+}

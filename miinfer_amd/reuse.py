@@ -11,7 +11,7 @@ import enum
 import numpy as np
 import torch
 
-from ._lib import call, lib
+from ._lib import MIIKV_EWORKSPACE, call, check, lib
 from .kv import KvCache, _on_stream, _ptr, _stream
 
 
@@ -214,3 +214,127 @@ class PrefixContext:
 def token_hash(tokens) -> int:
     t = np.ascontiguousarray(tokens, np.uint32)
     return int(lib().miikv_token_hash(t.ctypes.data_as(ctypes.c_void_p), t.size))
+
+
+class PrefixRegistry:
+    """Several saved prefixes over one page pool (one block-table row shared by every
+    attention layer's cache).  Each entry keeps the ReusableContext fingerprint
+    (reusable_context.hpp:17-129), a pool reference on each page of its row and,
+    optionally, a recurrent-state checkpoint; lookup picks the longest prefix that
+    passes check_match's rule (reusable_context.cpp:155-185), fork gives a new
+    session a row sharing the entry's pages (the partial last page copied) and
+    restores the checkpoint.  A full registry evicts its least recently used entry."""
+
+    def __init__(self, pool: PagePool, page_tokens: int = 256, max_entries: int = 16,
+                 model_id: str = "Qwen3.8-27B", quantization: str = "Q4_K_M"):
+        self.pool = pool
+        self.page_tokens = page_tokens
+        self.model_id = model_id
+        self.quantization = quantization
+        self._h = lib().miikv_registry_create(pool._h, page_tokens, max_entries, model_id.encode(),
+                                              quantization.encode())
+        if not self._h:
+            raise ValueError("invalid registry geometry")
+        self._checkpoints: dict[int, RecurrentStates] = {}
+        self._next_tag = 1
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            lib().miikv_registry_destroy(h)
+            self._h = None
+
+    def __len__(self) -> int:
+        return int(lib().miikv_registry_count(self._h))
+
+    def save(self, tokens, row: np.ndarray, states: RecurrentStates | None = None) -> int:
+        """Register tokens held by the pages of `row` (+ a checkpoint of `states`);
+        returns the entry id.  Evicts least recently used entries while full."""
+        t = np.ascontiguousarray(tokens, np.uint32)
+        row = np.ascontiguousarray(row, np.int32)
+        tag = self._next_tag
+        eid = ctypes.c_uint32(0)
+        while True:
+            st = lib().miikv_registry_save(self._h, t.ctypes.data_as(ctypes.c_void_p), t.size, _i32p(row),
+                                           row.size, tag, ctypes.byref(eid))
+            if st != MIIKV_EWORKSPACE or len(self) == 0:  # EWORKSPACE: the registry is full
+                break
+            self.evict_lru()
+        check("miikv_registry_save", st)
+        info = self.info(eid.value)
+        if info["tag"] == tag:  # a new entry (an existing one keeps its checkpoint)
+            self._next_tag += 1
+            if states is not None:
+                ck = RecurrentStates(states.layers, states.state_elems, states.conv_elems,
+                                     device=states.buf.device)
+                clone_states(states, [ck])
+                ck.position = t.size
+                self._checkpoints[tag] = ck
+        return eid.value
+
+    def lookup(self, prompt, model_id: str | None = None, quantization: str | None = None,
+               strict: bool = True):
+        """(MatchResult, entry id, prefix length) of the longest matching entry."""
+        p = np.ascontiguousarray(prompt, np.uint32)
+        eid = ctypes.c_uint32(0)
+        n = ctypes.c_uint32(0)
+        r = lib().miikv_registry_lookup(self._h, p.ctypes.data_as(ctypes.c_void_p), p.size,
+                                        (model_id or self.model_id).encode(),
+                                        (quantization or self.quantization).encode(), int(strict),
+                                        ctypes.byref(eid), ctypes.byref(n))
+        return MatchResult(r), eid.value, n.value
+
+    def fork(self, entry_id: int, row_capacity: int, states: RecurrentStates | None = None):
+        """A session row from an entry: (child_row, [(src, dst)] page copies to run);
+        restores the entry's checkpoint into `states` (restore_gdn_states,
+        reusable_context.cpp:187-200)."""
+        child = np.full(row_capacity, -1, np.int32)
+        src = np.zeros(1, np.int32)
+        dst = np.zeros(1, np.int32)
+        n = ctypes.c_uint32(0)
+        call("miikv_registry_fork", self._h, entry_id, _i32p(child), row_capacity, _i32p(src), _i32p(dst),
+             ctypes.byref(n))
+        if states is not None:
+            info = self.info(entry_id)
+            ck = self._checkpoints.get(info["tag"])
+            if ck is None:
+                raise RuntimeError("entry has no recurrent-state checkpoint")
+            clone_states(ck, [states])
+            states.position = info["length"]
+        return child, [(int(src[0]), int(dst[0]))] if n.value else []
+
+    def _drop_tag(self, tag: int) -> None:
+        self._checkpoints.pop(tag, None)
+
+    def release(self, entry_id: int) -> None:
+        tag = ctypes.c_uint64(0)
+        call("miikv_registry_release", self._h, entry_id, ctypes.byref(tag))
+        self._drop_tag(tag.value)
+
+    def evict_lru(self) -> int:
+        eid = ctypes.c_uint32(0)
+        tag = ctypes.c_uint64(0)
+        call("miikv_registry_evict_lru", self._h, ctypes.byref(eid), ctypes.byref(tag))
+        self._drop_tag(tag.value)
+        return eid.value
+
+    def evict_until_free(self, min_free_pages: int) -> list[int]:
+        """Evict least recently used entries until the pool has min_free_pages free
+        pages (or the registry is empty); returns the evicted ids."""
+        out = []
+        while self.pool.free_pages < min_free_pages and len(self):
+            out.append(self.evict_lru())
+        return out
+
+    def info(self, entry_id: int) -> dict:
+        length = ctypes.c_uint32(0)
+        h = ctypes.c_uint64(0)
+        tag = ctypes.c_uint64(0)
+        call("miikv_registry_info", self._h, entry_id, ctypes.byref(length), ctypes.byref(h),
+             ctypes.byref(tag), None, 0)
+        pages = np.zeros(-(-length.value // self.page_tokens), np.int32)
+        call("miikv_registry_info", self._h, entry_id, None, None, None, _i32p(pages), pages.size)
+        return {"length": length.value, "hash": h.value, "tag": tag.value, "pages": pages}
+
+    def _set_layout_version(self, entry_id: int, v: int) -> None:
+        call("miikv_registry_set_layout_version", self._h, entry_id, v)

@@ -175,3 +175,89 @@ def test_pool_prepare_append_twice_at_a_boundary_keeps_one_page():
     assert pool.refcount(page) == 2
     cps = pool.prepare_append(child, 256, 256)
     assert cps == [(page, int(child[1]))] and pool.refcount(page) == 1
+
+
+def _session(pool, n, pt=256):
+    row = np.full(-(-n // pt) + 2, -1, np.int32)
+    for i in range(-(-n // pt)):
+        row[i] = pool.alloc()
+    return row
+
+
+def test_registry_longest_prefix_and_precedence():
+    from miinfer_amd import reuse
+    M = reuse.MatchResult
+    pool = reuse.PagePool(64)
+    reg = reuse.PrefixRegistry(pool, 256, 8, "m", "q")
+    assert reg.lookup(np.arange(10))[0] == M.EMPTY_CACHE
+    a = np.arange(300, dtype=np.uint32)
+    b = np.arange(800, dtype=np.uint32)          # extends a
+    c = np.arange(1000, 1600, dtype=np.uint32)   # unrelated
+    ea = reg.save(a, _session(pool, 300))
+    eb = reg.save(b, _session(pool, 800))
+    ec = reg.save(c, _session(pool, 600))
+    assert len(reg) == 3
+    # longest matching prefix wins; strict needs a token left to run
+    assert reg.lookup(np.arange(900))[:3] == (M.EXACT_MATCH, eb, 800)
+    assert reg.lookup(np.arange(500))[:3] == (M.EXACT_MATCH, ea, 300)
+    assert reg.lookup(np.arange(800))[:3] == (M.EXACT_MATCH, ea, 300)
+    assert reg.lookup(np.arange(800), strict=False)[:3] == (M.EXACT_MATCH, eb, 800)
+    assert reg.lookup(np.concatenate([c, [7]]))[:2] == (M.EXACT_MATCH, ec)
+    # no match: the most recently used entry's verdict, in check_match's precedence
+    assert reg.lookup(np.arange(5, 900))[0] == M.PREFIX_MISMATCH
+    assert reg.lookup(np.arange(900), model_id="other")[0] == M.MODEL_MISMATCH
+    assert reg.lookup(np.arange(900), quantization="Q8")[0] == M.QUANTIZATION_MISMATCH
+    reg._set_layout_version(ea, 1)
+    reg._set_layout_version(eb, 1)
+    reg._set_layout_version(ec, 1)
+    assert reg.lookup(np.arange(900))[0] == M.VERSION_MISMATCH
+    # same tokens again: the existing entry, no duplicate
+    assert reg.save(a, _session(pool, 300)) == ea and len(reg) == 3
+    info = reg.info(eb)
+    assert info["length"] == 800 and info["hash"] == reuse.token_hash(b) and info["pages"].size == 4
+
+
+def test_registry_refcounts_fork_and_release():
+    from miinfer_amd import reuse
+    pool = reuse.PagePool(32)
+    reg = reuse.PrefixRegistry(pool, 256, 4)
+    row = _session(pool, 600)                    # 3 pages, the last partial
+    e = reg.save(np.arange(600), row)
+    pages = row[:3].copy()
+    assert all(pool.refcount(int(p)) == 2 for p in pages)
+    pool.release(row, 600, 256)                  # the session ends; the entry keeps them
+    assert all(pool.refcount(int(p)) == 1 for p in pages)
+    child, copies = reg.fork(e, 5)
+    assert (child[:2] == pages[:2]).all() and child[2] not in pages
+    assert copies == [(int(pages[2]), int(child[2]))]
+    assert pool.refcount(int(pages[0])) == 2 and pool.refcount(int(pages[2])) == 1
+    free = pool.free_pages
+    reg.release(e)
+    assert len(reg) == 0
+    assert pool.refcount(int(pages[0])) == 1 and pool.refcount(int(pages[2])) == 0
+    assert pool.free_pages == free + 1
+    pool.release(child, 600, 256)
+    assert pool.free_pages == 32
+
+
+def test_registry_lru_eviction():
+    from miinfer_amd import reuse
+    pool = reuse.PagePool(32)
+    reg = reuse.PrefixRegistry(pool, 256, 2)
+    rows = {}
+    ids = {}
+    for name, base in (("a", 0), ("b", 10000)):
+        rows[name] = _session(pool, 512)
+        ids[name] = reg.save(np.arange(base, base + 512), rows[name])
+        pool.release(rows[name], 512, 256)
+    child, _ = reg.fork(ids["a"], 4)               # a is now the most recent
+    pool.release(child, 512, 256)
+    rows["c"] = _session(pool, 256)
+    ids["c"] = reg.save(np.arange(20000, 20256), rows["c"])  # full: b is evicted
+    pool.release(rows["c"], 256, 256)
+    assert len(reg) == 2
+    assert reg.lookup(np.arange(10000, 10600))[0] != reuse.MatchResult.EXACT_MATCH
+    assert reg.lookup(np.arange(0, 600))[1] == ids["a"]
+    before = pool.free_pages
+    evicted = reg.evict_until_free(before + 1)     # a (least recent) holds 2 pages alone
+    assert evicted == [ids["a"]] and pool.free_pages == before + 2
