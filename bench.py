@@ -404,6 +404,115 @@ def stream_read_ceiling(dev, span_bytes: int, spans: int = 8, reps: int = 20) ->
                     f"{spans} spans), {8 * spans} back-to-back launches per graph replay"}
 
 
+def _graph_median(fn, steps_per_graph: int, replays: int = 30, warm: int = 5):
+    """Capture fn(i, stream) for i < steps_per_graph into one graph; per-replay HIP
+    events; returns (median, p10, p90) us per step."""
+    import torch
+    stream = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for i in range(steps_per_graph):
+            fn(i, torch.cuda.current_stream())
+    times = []
+    with torch.cuda.stream(stream):
+        for _ in range(warm):
+            g.replay()
+        for _ in range(replays):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            g.replay()
+            e1.record(stream)
+            e1.synchronize()
+            times.append(e0.elapsed_time(e1) * 1e3 / steps_per_graph)
+    times.sort()
+    return times[len(times) // 2], times[len(times) // 10], times[(9 * len(times)) // 10]
+
+
+def decode_variants(dev, ctx: int = 32768, nl: int = 8) -> dict:
+    """Two more config 2 lines at 32k, same rotation and protocol as the headline:
+    * reference_signature: the drop-in call sequence of the reference's decode step
+      (attention_layer.cpp:599-632): miikv_append_f32 with the fused K RMSNorm + RoPE
+      prologue on fp32 rows at the decode-state position, then miikv_decode_attn_q8_1 with
+      an fp32 query, gate, gated output and the Q8_1 epilogue;
+    * fp16_control: attention over an FP16_FP16 cache (the reference's production default,
+      qwen3_primitives.hip:2198-2293), attention only, 2x the KV bytes of q8_0."""
+    import ctypes
+
+    import torch
+
+    import miinfer_amd as m
+    from miinfer_amd import _lib
+    L = _lib.lib()
+    P = ctypes.c_void_p
+    torch.manual_seed(5)
+    out = {}
+    # reference-signature step over q8_0 caches
+    caches = []
+    for _ in range(nl):
+        c = m.KvCache.contiguous(HKV, D, ctx, device=dev)
+        for t0 in range(0, ctx, 8192):
+            n = min(8192, ctx - t0)
+            c.append(torch.randn((n, HKV, D), device=dev).half(), torch.randn((n, HKV, D), device=dev).half(),
+                     base_position=t0)
+        caches.append(c)
+    q32 = torch.randn((1, HQ, D), device=dev)
+    gate = torch.randn((1, HQ, D), device=dev)
+    gated = torch.empty((1, HQ, D), device=dev)
+    q81 = torch.empty(HQ * D // 32 * 36, dtype=torch.uint8, device=dev)
+    k32 = torch.randn((1, HKV, D), device=dev)
+    v32 = torch.randn((1, HKV, D), device=dev)
+    w = torch.rand(D, device=dev) + 0.5
+    ds = m.make_decode_state(ctx - 1, device=dev)
+    ws = m.DecodeWorkspace(caches[0], HQ, 1, ctx)
+
+    def ref_step(i, s):
+        c = caches[i % nl]
+        assert L.miikv_append_f32(c.view, P(k32.data_ptr()), P(v32.data_ptr()), P(w.data_ptr()), 1, 0, 0,
+                                  ctypes.c_float(1.0e6), ctypes.c_float(1e-6), None, P(ds.data_ptr()),
+                                  P(s.cuda_stream)) == 0
+        assert L.miikv_decode_attn_q8_1(c.view, P(q32.data_ptr()), _lib.DTYPE_F32, HQ,
+                                        ctypes.c_float(1 / math.sqrt(D)), 1, None, P(ds.data_ptr()), ctx, None,
+                                        P(gate.data_ptr()), P(gated.data_ptr()), P(q81.data_ptr()),
+                                        P(ws.buf.data_ptr()), ws.bytes, P(s.cuda_stream)) == 0
+    med, p10, p90 = _graph_median(ref_step, 8 * nl)
+    nbytes = decode_bytes(ctx) + 2 * HKV * D * 4 + kv_bytes_per_token() + HQ * D * 4 * 2
+    out["reference_signature"] = {
+        "calls": "miikv_append_f32 (K RMSNorm + RoPE prologue, fp32 rows, decode state) + "
+                 "miikv_decode_attn_q8_1 (fp32 query, gate, gated output, Q8_1 blocks)",
+        "us_median": round(med, 3), "us_p10": round(p10, 3), "us_p90": round(p90, 3),
+        "GBs_median": round(nbytes / (med * 1e-6) / 1e9, 1)}
+    del caches
+    torch.cuda.empty_cache()
+    # fp16 control
+    caches = []
+    for _ in range(nl):
+        c = m.KvCache.contiguous(HKV, D, ctx, device=dev, quant_mode=_lib.KV_FP16_FP16)
+        for t0 in range(0, ctx, 8192):
+            n = min(8192, ctx - t0)
+            c.append(torch.randn((n, HKV, D), device=dev).half(), torch.randn((n, HKV, D), device=dev).half(),
+                     base_position=t0)
+        caches.append(c)
+    q = torch.randn((1, HQ, D), device=dev).half()
+    o = torch.empty((1, HQ, D), device=dev)
+    lens = torch.tensor([ctx], dtype=torch.int32, device=dev)
+    ws = m.DecodeWorkspace(caches[0], HQ, 1, ctx)
+
+    def f16_step(i, s):
+        assert L.miikv_decode_attn(caches[i % nl].view, P(q.data_ptr()), _lib.DTYPE_F16, HQ,
+                                   ctypes.c_float(1 / math.sqrt(D)), 1, P(lens.data_ptr()), None, ctx,
+                                   P(o.data_ptr()), None, None, P(ws.buf.data_ptr()), ws.bytes,
+                                   P(s.cuda_stream)) == 0
+    med, p10, p90 = _graph_median(f16_step, 8 * nl)
+    fbytes = ctx * 2 * HKV * D * 2 + HQ * D * 6
+    out["fp16_control"] = {
+        "kv_mode": "FP16_FP16", "us_median": round(med, 3), "us_p10": round(p10, 3), "us_p90": round(p90, 3),
+        "GBs_median": round(fbytes / (med * 1e-6) / 1e9, 1), "kv_bytes_per_launch": fbytes}
+    del caches
+    torch.cuda.empty_cache()
+    return out
+
+
 def decode_at(dev, ctx: int, nl: int, replays: int = 30) -> dict:
     """Fused append + decode (config 2 shape) at context `ctx` over `nl` rotated layer
     caches: per-replay HIP-event times (one replay = 8 rounds over the layers) give the
@@ -688,11 +797,14 @@ def main() -> int:
                         "algorithmic_bytes_per_launch": decode_bytes(ctx)},
     }
     line["roofline"]["stream_read_ceiling"] = stream_read_ceiling(dev, decode_bytes(ctx))
+    if not args.no_sweep:
+        del caches, graphs
+        caches = graphs = None
+        torch.cuda.empty_cache()
+        line.update(decode_variants(dev, ctx, nl))
     # The other contexts of config 2, cold (enough rotated layers to exceed the 256 MB
     # Infinity Cache) and hot (one layer, MALL-resident), with per-replay spread.
     if not args.no_sweep:
-        del caches, graphs
-        torch.cuda.empty_cache()
         line["contexts"] = {
             "cold": [decode_at(dev, c, max(8, -(-300_000_000 // (c * kv_bytes_per_token())))) for c in (4096, 16384, 32768)],
             "hot": [decode_at(dev, c, 1) for c in (4096, 16384, 32768)],

@@ -63,7 +63,13 @@ enum {
 enum { MIIKV_LAYOUT_CONTIGUOUS = 0, MIIKV_LAYOUT_PAGED = 1 };
 
 /* Mirrors KvCacheQuantMode (include/miinfer/prefill_v2/kv_cache.hpp:16-21).
- * Only MIIKV_KV_Q8_Q8 is implemented by this library. */
+ * A q8 plane (K or V) holds int8 codes plus one fp16 scale per 32 values; an fp16
+ * plane holds the fp16 rows themselves in the same tiled element order (2 bytes per
+ * element, twice the bytes of a q8 code plane) and has no scales (its scale pointer
+ * may be NULL).  Every mode is accepted by append, decode, suffix attention,
+ * export/import, the dequantising export and page copies; the fused append +
+ * attention entry points and the session file store q8 rows only (MIIKV_KV_Q8_Q8,
+ * MIIKV_EUNSUPPORTED otherwise). */
 enum { MIIKV_KV_FP16_FP16 = 0, MIIKV_KV_Q8_FP16 = 1, MIIKV_KV_FP16_Q8 = 2, MIIKV_KV_Q8_Q8 = 3 };
 
 enum { MIIKV_DTYPE_F16 = 0, MIIKV_DTYPE_F32 = 1 };
@@ -77,7 +83,7 @@ typedef struct miikv_view {
     int8_t* v_codes;
     uint16_t* v_scales; /* fp16 bits */
     uint32_t layout;      /* MIIKV_LAYOUT_* */
-    uint32_t quant_mode;  /* MIIKV_KV_* (must be MIIKV_KV_Q8_Q8) */
+    uint32_t quant_mode;  /* MIIKV_KV_* */
     uint32_t kv_heads;
     uint32_t head_dim;    /* 128 or 256 */
     uint32_t page_tokens; /* multiple of 64; CONTIGUOUS: the capacity */

@@ -9,9 +9,11 @@ namespace miikv {
 // Host-side validation of a view (shared with the decode launcher).
 int validate_view(const miikv_view* v) {
     if (v == nullptr) return MIIKV_EINVAL;
-    if (v->k_codes == nullptr || v->k_scales == nullptr || v->v_codes == nullptr || v->v_scales == nullptr)
+    if (v->quant_mode > MIIKV_KV_Q8_Q8) return MIIKV_EINVAL;
+    // q8 planes need their scales; fp16 planes have none
+    if (v->k_codes == nullptr || v->v_codes == nullptr || (!mode_k_f16(v->quant_mode) && v->k_scales == nullptr) ||
+        (!mode_v_f16(v->quant_mode) && v->v_scales == nullptr))
         return MIIKV_EINVAL;
-    if (v->quant_mode != MIIKV_KV_Q8_Q8) return MIIKV_EUNSUPPORTED;
     if (v->head_dim != 128 && v->head_dim != 256) return MIIKV_EUNSUPPORTED;
     if (v->kv_heads == 0 || v->page_tokens == 0 || v->page_tokens % 64 != 0) return MIIKV_EINVAL;
     if (v->layout == MIIKV_LAYOUT_CONTIGUOUS) {
@@ -92,6 +94,15 @@ __device__ __forceinline__ void k_norm_rope16(float (&x)[16], const float* w, ui
     }
 }
 
+// Eight values -> eight fp16 (round to nearest even) in one 16-byte word.
+__device__ __forceinline__ uint4 pack8_f16(const float* x) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        w[i] = static_cast<uint32_t>(f32_to_f16_bits(x[2 * i])) | (static_cast<uint32_t>(f32_to_f16_bits(x[2 * i + 1])) << 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 // One thread per (row, 16-dim group); a row is (token, kv_head).  Adjacent
 // lanes (2i, 2i+1) hold the two halves of one 32-value block, and the D/16
 // lanes of a row are consecutive.
@@ -150,28 +161,40 @@ __global__ void __launch_bounds__(256) append_kernel(
     const size_t slab_bytes = static_cast<size_t>(g.page_tokens) * D;
     const uint32_t d0 = q16 * 16;
 
-    // K: dims d0..d0+7 and d0+8..d0+15 are two 8-byte runs of the tiled layout.
-    int8_t* kslab = g.k_codes + slab * slab_bytes;
-    uint32_t packed[4];
+    // K: dims d0..d0+7 and d0+8..d0+15 are two 8-element runs of the tiled layout.
+    if (g.k_f16) {
+        uint16_t* kslab = reinterpret_cast<uint16_t*>(g.k_codes) + slab * slab_bytes;
+        *reinterpret_cast<uint4*>(kslab + k_code_offset(tp, d0, D)) = pack8_f16(xk);
+        *reinterpret_cast<uint4*>(kslab + k_code_offset(tp, d0 + 8, D)) = pack8_f16(xk + 8);
+    } else {
+        int8_t* kslab = g.k_codes + slab * slab_bytes;
+        uint32_t packed[4];
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        packed[w] = (static_cast<uint32_t>(static_cast<uint8_t>(qk[4 * w]))) |
-                    (static_cast<uint32_t>(static_cast<uint8_t>(qk[4 * w + 1])) << 8) |
-                    (static_cast<uint32_t>(static_cast<uint8_t>(qk[4 * w + 2])) << 16) |
-                    (static_cast<uint32_t>(static_cast<uint8_t>(qk[4 * w + 3])) << 24);
+        for (int w = 0; w < 4; ++w) {
+            packed[w] = (static_cast<uint32_t>(static_cast<uint8_t>(qk[4 * w]))) |
+                        (static_cast<uint32_t>(static_cast<uint8_t>(qk[4 * w + 1])) << 8) |
+                        (static_cast<uint32_t>(static_cast<uint8_t>(qk[4 * w + 2])) << 16) |
+                        (static_cast<uint32_t>(static_cast<uint8_t>(qk[4 * w + 3])) << 24);
+        }
+        *reinterpret_cast<uint2*>(kslab + k_code_offset(tp, d0, D)) = make_uint2(packed[0], packed[1]);
+        *reinterpret_cast<uint2*>(kslab + k_code_offset(tp, d0 + 8, D)) = make_uint2(packed[2], packed[3]);
     }
-    *reinterpret_cast<uint2*>(kslab + k_code_offset(tp, d0, D)) = make_uint2(packed[0], packed[1]);
-    *reinterpret_cast<uint2*>(kslab + k_code_offset(tp, d0 + 8, D)) = make_uint2(packed[2], packed[3]);
 
-    // V: each dim is its own token-contiguous run; one byte per dim.
-    int8_t* vslab = g.v_codes + slab * slab_bytes;
+    // V: each dim is its own token-contiguous run; one element per dim.
+    if (g.v_f16) {
+        uint16_t* vslab = reinterpret_cast<uint16_t*>(g.v_codes) + slab * slab_bytes;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) vslab[v_code_offset(tp, d0 + i, D)] = qv[i];
+        for (int i = 0; i < 16; ++i) vslab[v_code_offset(tp, d0 + i, D)] = f32_to_f16_bits(xv[i]);
+    } else {
+        int8_t* vslab = g.v_codes + slab * slab_bytes;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) vslab[v_code_offset(tp, d0 + i, D)] = qv[i];
+    }
 
     if ((q16 & 1) == 0) {
         const size_t sidx = (slab * g.page_tokens + tp) * (D / 32) + d0 / 32;
-        g.k_scales[sidx] = f32_to_f16_bits(sk);
-        g.v_scales[sidx] = f32_to_f16_bits(sv);
+        if (!g.k_f16) g.k_scales[sidx] = f32_to_f16_bits(sk);
+        if (!g.v_f16) g.v_scales[sidx] = f32_to_f16_bits(sv);
     }
 }
 
@@ -317,6 +340,38 @@ __global__ void __launch_bounds__(256) canonical_kernel(
     int8_t* vslab = g.v_codes + slab * slab_bytes;
     const size_t sidx = (slab * g.page_tokens + tp) * (D / 32) + d0 / 32;
     const size_t csidx = (static_cast<size_t>(head) * count + t) * (D / 32) + d0 / 32;
+    // fp16 planes: canonical rows are fp16 [kv_head][count][D]; no scales.
+    uint16_t* kslab16 = reinterpret_cast<uint16_t*>(g.k_codes) + slab * slab_bytes;
+    uint16_t* vslab16 = reinterpret_cast<uint16_t*>(g.v_codes) + slab * slab_bytes;
+    uint16_t* kc16 = reinterpret_cast<uint16_t*>(kc);
+    uint16_t* vc16 = reinterpret_cast<uint16_t*>(vc);
+    if (g.k_f16) {
+        if (kc != nullptr) {
+            uint4* kslab4_lo = reinterpret_cast<uint4*>(kslab16 + k_code_offset(tp, d0, D));
+            uint4* kslab4_hi = reinterpret_cast<uint4*>(kslab16 + k_code_offset(tp, d0 + 8, D));
+            uint4* krow = reinterpret_cast<uint4*>(kc16 + crow);
+            if (EXPORT) {
+                krow[0] = *kslab4_lo;
+                krow[1] = *kslab4_hi;
+            } else {
+                *kslab4_lo = krow[0];
+                *kslab4_hi = krow[1];
+            }
+        }
+        kc = nullptr;
+        ks = nullptr;
+    }
+    if (g.v_f16) {
+        if (vc != nullptr) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                if (EXPORT) vc16[crow + i] = vslab16[v_code_offset(tp, d0 + i, D)];
+                else vslab16[v_code_offset(tp, d0 + i, D)] = vc16[crow + i];
+            }
+        }
+        vc = nullptr;
+        vs = nullptr;
+    }
     if (EXPORT) {
         if (kc != nullptr) {
             const uint2 a = *reinterpret_cast<const uint2*>(kslab + k_code_offset(tp, d0, D));
@@ -376,6 +431,27 @@ __global__ void __launch_bounds__(256) dequant_kernel(Geo g, uint32_t seq, uint3
     const uint32_t d0 = q16 * 16;
     const size_t row = (static_cast<size_t>(head) * count + t) * D + d0;
     const size_t sidx = (slab * g.page_tokens + tp) * (D / 32) + d0 / 32;
+    if (kout != nullptr && g.k_f16) {
+        const uint16_t* kslab = reinterpret_cast<const uint16_t*>(g.k_codes) + slab * slab_bytes;
+        float x[16];
+        unpack16_f16({*reinterpret_cast<const uint4*>(kslab + k_code_offset(tp, d0, D)),
+                      *reinterpret_cast<const uint4*>(kslab + k_code_offset(tp, d0 + 8, D))}, x);
+        float4* o = reinterpret_cast<float4*>(kout + row);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = make_float4(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+        kout = nullptr;
+    }
+    if (vout != nullptr && g.v_f16) {
+        const uint16_t* vslab = reinterpret_cast<const uint16_t*>(g.v_codes) + slab * slab_bytes;
+        float4* o = reinterpret_cast<float4*>(vout + row);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            o[i] = make_float4(f16_bits_to_f32(vslab[v_code_offset(tp, d0 + 4 * i, D)]),
+                               f16_bits_to_f32(vslab[v_code_offset(tp, d0 + 4 * i + 1, D)]),
+                               f16_bits_to_f32(vslab[v_code_offset(tp, d0 + 4 * i + 2, D)]),
+                               f16_bits_to_f32(vslab[v_code_offset(tp, d0 + 4 * i + 3, D)]));
+        vout = nullptr;
+    }
     if (kout != nullptr) {
         const int8_t* kslab = g.k_codes + slab * slab_bytes;
         const uint2 a = *reinterpret_cast<const uint2*>(kslab + k_code_offset(tp, d0, D));
@@ -415,19 +491,22 @@ __global__ void __launch_bounds__(256) copy_pages_kernel(Geo g, const int32_t* _
     const size_t s = static_cast<size_t>(srcp[i]);
     const size_t d = static_cast<size_t>(dstp[i]);
     const uint64_t code_bytes = static_cast<uint64_t>(g.kv_heads) * g.page_tokens * g.head_dim;
+    const uint64_t kbytes = code_bytes * (g.k_f16 ? 2 : 1), vbytes = code_bytes * (g.v_f16 ? 2 : 1);
     const uint64_t scale_bytes = static_cast<uint64_t>(g.kv_heads) * g.page_tokens * (g.head_dim / 32) * 2;
     const uint64_t start = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
-    copy16(reinterpret_cast<uint4*>(g.k_codes + d * code_bytes),
-           reinterpret_cast<const uint4*>(g.k_codes + s * code_bytes), code_bytes / 16, start, stride);
-    copy16(reinterpret_cast<uint4*>(g.v_codes + d * code_bytes),
-           reinterpret_cast<const uint4*>(g.v_codes + s * code_bytes), code_bytes / 16, start, stride);
-    copy16(reinterpret_cast<uint4*>(reinterpret_cast<uint8_t*>(g.k_scales) + d * scale_bytes),
-           reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(g.k_scales) + s * scale_bytes),
-           scale_bytes / 16, start, stride);
-    copy16(reinterpret_cast<uint4*>(reinterpret_cast<uint8_t*>(g.v_scales) + d * scale_bytes),
-           reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(g.v_scales) + s * scale_bytes),
-           scale_bytes / 16, start, stride);
+    copy16(reinterpret_cast<uint4*>(g.k_codes + d * kbytes),
+           reinterpret_cast<const uint4*>(g.k_codes + s * kbytes), kbytes / 16, start, stride);
+    copy16(reinterpret_cast<uint4*>(g.v_codes + d * vbytes),
+           reinterpret_cast<const uint4*>(g.v_codes + s * vbytes), vbytes / 16, start, stride);
+    if (!g.k_f16)
+        copy16(reinterpret_cast<uint4*>(reinterpret_cast<uint8_t*>(g.k_scales) + d * scale_bytes),
+               reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(g.k_scales) + s * scale_bytes),
+               scale_bytes / 16, start, stride);
+    if (!g.v_f16)
+        copy16(reinterpret_cast<uint4*>(reinterpret_cast<uint8_t*>(g.v_scales) + d * scale_bytes),
+               reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(g.v_scales) + s * scale_bytes),
+               scale_bytes / 16, start, stride);
 }
 
 // grid (blocks, n): block y copies segment y.  16-byte path when both ends and
@@ -539,8 +618,10 @@ static miikv_status launch_append(const miikv_view* view, const AppendIn& in, ui
                                   uint32_t seq, const miikv_prefill_state* ps, const miikv_decode_state* ds,
                                   const uint32_t* positions, void* stream) {
     // Positions known on the host: [head partial group][whole groups][tail partial group].
+    // (The grouped store assembles q8 codes and scales; caches with an fp16 plane take
+    // the per-row kernel.)
     if (ps == nullptr && ds == nullptr && positions == nullptr && rows_tokens >= kTileAppendMin &&
-        std::getenv("MIIKV_APPEND_ROWS_ONLY") == nullptr) {
+        view->quant_mode == MIIKV_KV_Q8_Q8 && std::getenv("MIIKV_APPEND_ROWS_ONLY") == nullptr) {
         const uint32_t D = view->head_dim;
         const uint32_t head = (32 - base % 32) % 32;
         const uint32_t whole = (rows_tokens - head) / 32;

@@ -34,7 +34,14 @@ struct Geo {
     uint32_t page_tokens;
     uint32_t table_stride;
     uint32_t num_pages;
+    // fp16 planes (quant modes FP16_*): the plane holds the fp16 rows in the same
+    // tiled element order as the codes, 2 bytes per element, and has no scales.
+    uint32_t k_f16;
+    uint32_t v_f16;
 };
+
+inline bool mode_k_f16(uint32_t mode) { return mode == MIIKV_KV_FP16_FP16 || mode == MIIKV_KV_FP16_Q8; }
+inline bool mode_v_f16(uint32_t mode) { return mode == MIIKV_KV_FP16_FP16 || mode == MIIKV_KV_Q8_FP16; }
 
 inline Geo make_geo(const miikv_view& v) {
     Geo g;
@@ -49,6 +56,8 @@ inline Geo make_geo(const miikv_view& v) {
     g.page_tokens = v.page_tokens;
     g.table_stride = v.table_stride;
     g.num_pages = v.num_pages;
+    g.k_f16 = mode_k_f16(v.quant_mode) ? 1u : 0u;
+    g.v_f16 = mode_v_f16(v.quant_mode) ? 1u : 0u;
     return g;
 }
 

@@ -273,8 +273,19 @@ __device__ void append_record(const SplitArgs& a, uint32_t b, uint32_t h, uint32
     __syncthreads();  // the caller reuses the LDS
 }
 
-template <uint32_t D, bool QF32, bool APPEND>
-__global__ void __launch_bounds__(64 * kWavesPerWg) __attribute__((amdgpu_waves_per_eu(DecodeTuning<D, QF32>::waves_per_eu)))
+// KF16 / VF16: the K / V plane holds fp16 rows (quant modes FP16_*, the reference's
+// control path, qwen3_wave64_splitk_stage1_f16_kernel at qwen3_primitives.hip:2198-2293):
+// the fragments are loaded as fp16 and enter the MFMAs unscaled; those variants run a
+// one-step ring (fp16 fragments take twice the registers).
+// Waves per SIMD of a decode_kernel instance: the tuned value, except q8 keys with fp16
+// values at D = 256, which need a wave's full register file (two waves spilled 122).
+template <uint32_t D, bool QF32, bool KF16, bool VF16>
+constexpr uint32_t decode_waves_per_eu() {
+    return (D == 256 && VF16 && !KF16) ? 1u : DecodeTuning<D, QF32>::waves_per_eu;
+}
+template <uint32_t D, bool QF32, bool APPEND, bool KF16 = false, bool VF16 = false>
+__global__ void __launch_bounds__(64 * kWavesPerWg)
+__attribute__((amdgpu_waves_per_eu(decode_waves_per_eu<D, QF32, KF16, VF16>())))
 decode_kernel(SplitArgs a) {
     constexpr uint32_t NB = D / 32;   // q8_0 blocks per row
     constexpr uint32_t NC = D / 64;   // 16-byte K loads per tile row group
@@ -282,7 +293,8 @@ decode_kernel(SplitArgs a) {
     using ScaleVec = typename std::conditional<NB == 4, uint32_t, uint2>::type;  // NB/2 fp16 scales
     // V codes enter the PV MFMA biased (one v_perm per two codes) and the bias is removed
     // with column sums, or exactly (perm + subtract): the fold costs NB accumulators.
-    constexpr bool kVBias = DecodeTuning<D, QF32>::vbias;
+    constexpr bool kVBias = DecodeTuning<D, QF32>::vbias && !VF16;
+    static_assert(!APPEND || (!KF16 && !VF16), "the fused append stores q8 rows");
     extern __shared__ float smem[];
 
     // Work item of this workgroup: one (sequence b, kv head h, split) of 4 waves x
@@ -339,8 +351,8 @@ decode_kernel(SplitArgs a) {
 
     // Registers of one 32-token step: two K tiles, one V group, their scales.
     struct Step {
-        uint4 k[2][NC];
-        uint2 v[NM];
+        uint4 k[2][NC][KF16 ? 2 : 1];                            // fp16: two words per fragment
+        typename std::conditional<VF16, uint4, uint2>::type v[NM];  // fp16: 8 values per lane
         ScaleVec ks, vs;
     };
 
@@ -356,27 +368,34 @@ decode_kernel(SplitArgs a) {
             ld_tp = ld_tok % geo.page_tokens;
             ld_slab = slab_of_clamped(geo, b, ld_tok, h);
         }
-        const int8_t* kb = geo.k_codes + ld_slab * slab_bytes + static_cast<size_t>(ld_tp) * D;
-        const int8_t* vb = geo.v_codes + ld_slab * slab_bytes + static_cast<size_t>(ld_tp) * D;
+        constexpr uint32_t KE = KF16 ? 2 : 1, VE = VF16 ? 2 : 1;  // bytes per element
+        const int8_t* kb = geo.k_codes + (ld_slab * slab_bytes + static_cast<size_t>(ld_tp) * D) * KE;
+        const int8_t* vb = geo.v_codes + (ld_slab * slab_bytes + static_cast<size_t>(ld_tp) * D) * VE;
         const size_t sc0 = (ld_slab * geo.page_tokens + ld_tp) * NB;
         // Scales first, each ahead of its codes: loads complete in issue order, so the
         // score MFMAs wait only for the K scales and codes while V is still in flight.
-        st.ks = load_scales<ScaleVec, DecodeTuning<D, QF32>::nt_scales>(geo.k_scales + sc0 + lane * (NB / 2));
+        if constexpr (!KF16)
+            st.ks = load_scales<ScaleVec, DecodeTuning<D, QF32>::nt_scales>(geo.k_scales + sc0 + lane * (NB / 2));
 #pragma unroll
         for (uint32_t J = 0; J < 2; ++J)
 #pragma unroll
             for (uint32_t cc = 0; cc < NC; ++cc)
-                st.k[J][cc] = load16(kb + J * 16 * D + cc * 1024 + g4 * 256 + n * 16);
-        st.vs = load_scales<ScaleVec, DecodeTuning<D, QF32>::nt_scales>(geo.v_scales + sc0 + lane * (NB / 2));
 #pragma unroll
-        for (uint32_t mt = 0; mt < NM; ++mt)
-            st.v[mt] = load8(vb + (16 * mt + n) * 32 + g4 * 8);
+                for (uint32_t e = 0; e < KE; ++e)
+                    st.k[J][cc][e] = load16(kb + KE * (J * 16 * D + cc * 1024 + g4 * 256 + n * 16) + 16 * e);
+        if constexpr (!VF16)
+            st.vs = load_scales<ScaleVec, DecodeTuning<D, QF32>::nt_scales>(geo.v_scales + sc0 + lane * (NB / 2));
+#pragma unroll
+        for (uint32_t mt = 0; mt < NM; ++mt) {
+            if constexpr (VF16) st.v[mt] = load16(vb + 2 * ((16 * mt + n) * 32 + g4 * 8));
+            else st.v[mt] = load8(vb + (16 * mt + n) * 32 + g4 * 8);
+        }
         ld_tok += stride * kChunk;
         ld_tp += stride * kChunk;
     };
 
     // Ring of kRing step buffers; the first kRing-1 are loaded before L is known.
-    constexpr uint32_t kRing = DecodeTuning<D, QF32>::ring;
+    constexpr uint32_t kRing = (KF16 || VF16) ? 1u : DecodeTuning<D, QF32>::ring;
     Step S[kRing];
 #pragma unroll
     for (uint32_t r = 0; r + 1 < kRing; ++r)
@@ -478,7 +497,8 @@ decode_kernel(SplitArgs a) {
 #pragma unroll
             for (uint32_t J = 0; J < 2; ++J)
 #pragma unroll
-                for (uint32_t cc = 0; cc < NC; ++cc) x ^= st.k[J][cc].x ^ st.k[J][cc].y ^ st.k[J][cc].z ^ st.k[J][cc].w;
+                for (uint32_t cc = 0; cc < NC; ++cc)
+                    x ^= st.k[J][cc][0].x ^ st.k[J][cc][0].y ^ st.k[J][cc][0].z ^ st.k[J][cc][0].w;
 #pragma unroll
             for (uint32_t mt = 0; mt < NM; ++mt) x ^= st.v[mt].x ^ st.v[mt].y;
             l_run += static_cast<float>(x & 1u);
@@ -487,13 +507,35 @@ decode_kernel(SplitArgs a) {
         }
 #endif
         const bool tail = tok0 + kChunk > Lc;
-        *reinterpret_cast<ScaleVec*>(s_sc + lane * (NB / 2)) = st.ks;
-        ScaleVec vsv = st.vs;
-        if (tail && tok0 + lane / 2 >= Lc) vsv = ScaleVec{};
-        *reinterpret_cast<ScaleVec*>(s_sc + kChunk * NB + lane * (NB / 2)) = vsv;
+        if constexpr (!KF16) *reinterpret_cast<ScaleVec*>(s_sc + lane * (NB / 2)) = st.ks;
+        if constexpr (!VF16) {
+            ScaleVec vsv = st.vs;
+            if (tail && tok0 + lane / 2 >= Lc) vsv = ScaleVec{};
+            *reinterpret_cast<ScaleVec*>(s_sc + kChunk * NB + lane * (NB / 2)) = vsv;
+        }
 
         // ---- scores S^T[token][head], one MFMA per q8_0 block, block scale in fp32
         float s[2][4];
+        if constexpr (KF16) {
+            // fp16 keys: one accumulator chain over the blocks, no scale
+#pragma unroll
+            for (uint32_t J = 0; J < 2; ++J) {
+                float4v c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (uint32_t cc = 0; cc < NC; ++cc) {
+                    const half8 a0 = __builtin_bit_cast(half8, st.k[J][cc][0]);  // block 2cc
+                    const half8 a1 = __builtin_bit_cast(half8, st.k[J][cc][KF16 ? 1 : 0]);  // block 2cc+1
+                    c = mfma_16x16x32(a0, qf[2 * cc], c);
+                    c = mfma_16x16x32(a1, qf[2 * cc + 1], c);
+                    if (QF32) {
+                        c = mfma_16x16x32(a0, ql[QF32 ? 2 * cc : 0], c);
+                        c = mfma_16x16x32(a1, ql[QF32 ? 2 * cc + 1 : 0], c);
+                    }
+                }
+#pragma unroll
+                for (uint32_t i = 0; i < 4; ++i) s[J][i] = c[i] * a.scale_log2;
+            }
+        } else
 #pragma unroll
         for (uint32_t J = 0; J < 2; ++J) {
             uint4 ksw[NB / 2];  // scales of tokens 16J + 4*g4 + i, all blocks
@@ -504,7 +546,7 @@ decode_kernel(SplitArgs a) {
             float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (uint32_t cc = 0; cc < NC; ++cc) {
-                const uint4 w = st.k[J][cc];
+                const uint4 w = st.k[J][cc][0];
 #ifdef MIIKV_EXP_NO_KBIAS
                 const half8 a0 = codes8_to_half8(w.x, w.y);
                 const half8 a1 = codes8_to_half8(w.z, w.w);
@@ -574,6 +616,27 @@ decode_kernel(SplitArgs a) {
 
         // ---- O^T += V^T * (P^T scaled per block); V codes enter as (code + 1152), the
         // bias is removed at the end with the column sums accumulated in vbias.
+        if constexpr (VF16) {
+            // fp16 values: P^T unscaled; keys past the context are zeroed (the memory
+            // there may hold non-finite values, and p = 0 would not cancel them)
+#pragma unroll
+            for (uint32_t J = 0; J < 2; ++J) {
+                half4 pb;
+#pragma unroll
+                for (uint32_t i = 0; i < 4; ++i) pb[i] = static_cast<_Float16>(s[J][i]);
+#pragma unroll
+                for (uint32_t mt = 0; mt < NM; ++mt) {
+                    const uint4 w = reinterpret_cast<const uint4&>(st.v[mt]);
+                    half4 va = __builtin_bit_cast(half4, J == 0 ? make_uint2(w.x, w.y) : make_uint2(w.z, w.w));
+                    if (tail) {
+#pragma unroll
+                        for (uint32_t i = 0; i < 4; ++i)
+                            if (tok0 + 16 * J + 4 * g4 + i >= Lc) va[i] = static_cast<_Float16>(0.0f);
+                    }
+                    O[mt] = mfma_16x16x16(va, pb, O[mt]);
+                }
+            }
+        } else
 #pragma unroll
         for (uint32_t J = 0; J < 2; ++J) {
             uint4 vsw[NB / 2];
@@ -591,7 +654,8 @@ decode_kernel(SplitArgs a) {
 #pragma unroll
                 for (uint32_t sub = 0; sub < 2; ++sub) {
                     const uint32_t mt = 2 * blk + sub;
-                    const uint32_t word = J == 0 ? st.v[mt].x : st.v[mt].y;
+                    const uint2 vw = reinterpret_cast<const uint2&>(st.v[mt]);
+                    const uint32_t word = J == 0 ? vw.x : vw.y;
                     if constexpr (kVBias) O[mt] = mfma_16x16x16(codes4_to_half4_biased(word), pb, O[mt]);
                     else O[mt] = mfma_16x16x16(codes4_to_half4(word), pb, O[mt]);
                 }
@@ -667,9 +731,10 @@ decode_kernel(SplitArgs a) {
 
 // Workgroups of decode_kernel resident on the chip at its occupancy: 256 CUs x 4
 // SIMDs x waves per SIMD, 4 waves per workgroup.
-uint32_t resident_workgroups(uint32_t D, bool f32) {
-    const uint32_t wpe = D == 128 ? (f32 ? DecodeTuning<128, true>::waves_per_eu : DecodeTuning<128, false>::waves_per_eu)
-                                  : (f32 ? DecodeTuning<256, true>::waves_per_eu : DecodeTuning<256, false>::waves_per_eu);
+uint32_t resident_workgroups(uint32_t D, bool f32, uint32_t mode) {
+    uint32_t wpe = D == 128 ? (f32 ? DecodeTuning<128, true>::waves_per_eu : DecodeTuning<128, false>::waves_per_eu)
+                            : (f32 ? DecodeTuning<256, true>::waves_per_eu : DecodeTuning<256, false>::waves_per_eu);
+    if (D == 256 && mode == MIIKV_KV_Q8_FP16) wpe = 1;
     return 256 * 4 * wpe / kWavesPerWg;
 }
 
@@ -744,6 +809,34 @@ extern "C" miikv_status miikv_workspace_init(void* workspace, uint64_t bytes, vo
     return hip_status(hipGetLastError());
 }
 
+namespace {
+template <uint32_t D, bool F32, bool APP, bool KF, bool VF>
+void launch_decode_t(dim3 grid, size_t lds, hipStream_t s, const SplitArgs& a) {
+    hipLaunchKernelGGL((decode_kernel<D, F32, APP, KF, VF>), grid, dim3(64 * kWavesPerWg), lds, s, a);
+}
+// Runtime flags -> kernel instance.  The fused append exists for q8 planes only (the
+// caller has rejected it for the other modes).
+template <uint32_t D>
+void launch_decode(bool f32, bool app, bool kf, bool vf, dim3 grid, size_t lds, hipStream_t s, const SplitArgs& a) {
+    if (app) {
+        if (f32) launch_decode_t<D, true, true, false, false>(grid, lds, s, a);
+        else launch_decode_t<D, false, true, false, false>(grid, lds, s, a);
+        return;
+    }
+    if (f32) {
+        if (kf && vf) launch_decode_t<D, true, false, true, true>(grid, lds, s, a);
+        else if (kf) launch_decode_t<D, true, false, true, false>(grid, lds, s, a);
+        else if (vf) launch_decode_t<D, true, false, false, true>(grid, lds, s, a);
+        else launch_decode_t<D, true, false, false, false>(grid, lds, s, a);
+    } else {
+        if (kf && vf) launch_decode_t<D, false, false, true, true>(grid, lds, s, a);
+        else if (kf) launch_decode_t<D, false, false, true, false>(grid, lds, s, a);
+        else if (vf) launch_decode_t<D, false, false, false, true>(grid, lds, s, a);
+        else launch_decode_t<D, false, false, false, false>(grid, lds, s, a);
+    }
+}
+}  // namespace
+
 static miikv_status decode_impl(const miikv_view* view, const uint16_t* k_new, const uint16_t* v_new,
                                 const void* q, uint32_t q_dtype, uint32_t q_heads, float scale, uint32_t batch,
                                 const uint32_t* d_lengths, const miikv_decode_state* decode_state,
@@ -763,6 +856,8 @@ static miikv_status decode_impl(const miikv_view* view, const uint16_t* k_new, c
     if (d_lengths == nullptr && (decode_state == nullptr || batch != 1)) return MIIKV_EINVAL;
     if (max_context == 0 || max_context > view_seq_capacity(view)) return MIIKV_EINVAL;
     if (view->layout == MIIKV_LAYOUT_CONTIGUOUS && batch != 1) return MIIKV_EINVAL;
+    // the fused append stores q8 rows
+    if (k_new != nullptr && view->quant_mode != MIIKV_KV_Q8_Q8) return MIIKV_EUNSUPPORTED;
     const Plan p = make_plan(view, q_heads, batch, max_context);
     if (workspace == nullptr || workspace_bytes < p.counter_bytes + p.part_bytes) return MIIKV_EWORKSPACE;
     if (p.splits > 65535u || batch > 65535u || static_cast<uint64_t>(batch) * view->kv_heads > 0x7fffffffu)
@@ -806,27 +901,20 @@ static miikv_status decode_impl(const miikv_view* view, const uint16_t* k_new, c
                          (k_new != nullptr ? static_cast<uint64_t>(view->kv_heads) * batch : 0);
     if (wgs > 0x7fffffffu) return MIIKV_EINVAL;
     a.batch = batch;
-    a.slots = p.adaptive ? resident_workgroups(view->head_dim, q_dtype == MIIKV_DTYPE_F32) : 0u;
+    a.slots = p.adaptive ? resident_workgroups(view->head_dim, q_dtype == MIIKV_DTYPE_F32, view->quant_mode) : 0u;
     const dim3 grid(static_cast<uint32_t>(wgs));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool f32 = q_dtype == MIIKV_DTYPE_F32;
     // combine: one workgroup per (sequence, kv head, 32 output elements)
     const dim3 cgrid(batch * view->kv_heads, G * view->head_dim / 32);
     const bool app = k_new != nullptr;
+    const bool kf = mode_k_f16(view->quant_mode), vf = mode_v_f16(view->quant_mode);
     if (view->head_dim == 128) {
-        if (app) {
-            if (f32) hipLaunchKernelGGL((decode_kernel<128, true, true>), grid, dim3(64 * kWavesPerWg), lds, s, a);
-            else hipLaunchKernelGGL((decode_kernel<128, false, true>), grid, dim3(64 * kWavesPerWg), lds, s, a);
-        } else if (f32) hipLaunchKernelGGL((decode_kernel<128, true, false>), grid, dim3(64 * kWavesPerWg), lds, s, a);
-        else hipLaunchKernelGGL((decode_kernel<128, false, false>), grid, dim3(64 * kWavesPerWg), lds, s, a);
+        launch_decode<128>(f32, app, kf, vf, grid, lds, s, a);
         if (app) hipLaunchKernelGGL((combine_kernel<128, true>), cgrid, dim3(256), 0, s, a);
         else hipLaunchKernelGGL((combine_kernel<128, false>), cgrid, dim3(256), 0, s, a);
     } else {
-        if (app) {
-            if (f32) hipLaunchKernelGGL((decode_kernel<256, true, true>), grid, dim3(64 * kWavesPerWg), lds, s, a);
-            else hipLaunchKernelGGL((decode_kernel<256, false, true>), grid, dim3(64 * kWavesPerWg), lds, s, a);
-        } else if (f32) hipLaunchKernelGGL((decode_kernel<256, true, false>), grid, dim3(64 * kWavesPerWg), lds, s, a);
-        else hipLaunchKernelGGL((decode_kernel<256, false, false>), grid, dim3(64 * kWavesPerWg), lds, s, a);
+        launch_decode<256>(f32, app, kf, vf, grid, lds, s, a);
         if (app) hipLaunchKernelGGL((combine_kernel<256, true>), cgrid, dim3(256), 0, s, a);
         else hipLaunchKernelGGL((combine_kernel<256, false>), cgrid, dim3(256), 0, s, a);
     }

@@ -88,6 +88,9 @@ __global__ void __launch_bounds__(256) expand_kernel(ExpandArgs a) {
     const size_t cb = slab * static_cast<size_t>(geo.page_tokens) * D + static_cast<size_t>(tp0) * D;
     const int8_t* kb = geo.k_codes + cb;
     const int8_t* vb = geo.v_codes + cb;
+    // fp16 planes (the control path): the tiles are the stored fp16 rows themselves
+    const _Float16* kb16 = reinterpret_cast<const _Float16*>(geo.k_codes) + cb;
+    const _Float16* vb16 = reinterpret_cast<const _Float16*>(geo.v_codes) + cb;
     const uint16_t* ksc = geo.k_scales + sc0;
     const uint16_t* vsc = geo.v_scales + sc0;
     if constexpr (APPEND) {
@@ -171,7 +174,7 @@ __global__ void __launch_bounds__(256) expand_kernel(ExpandArgs a) {
             vsc = s_vsc;
         }
     }
-    if (tid < kSufStep * NB) {
+    if (tid < kSufStep * NB && !geo.v_f16) {
         const uint32_t key = tid / NB, blk = tid % NB;
         s_vs[blk * kSufStep + key] = tok0 + key < nkeys ? clamp_scale(vsc[tid]) : (_Float16)0.0f;
     }
@@ -186,6 +189,11 @@ __global__ void __launch_bounds__(256) expand_kernel(ExpandArgs a) {
         const uint32_t c = fl / 64, l = fl % 64, n = l % 32, hh = l / 32;
         const uint32_t off = (n / 16) * 16 * D + (c / 4) * 1024 + (2 * (c % 2) + hh) * 256 + (n % 16) * 16 +
                              ((c % 4) / 2) * 8;
+        if (geo.k_f16) {
+            const half8 x = *reinterpret_cast<const half8*>(kb16 + off);
+            *reinterpret_cast<half8*>(out + 8 * fl) = tok0 + n < nkeys ? x : half8{};
+            continue;
+        }
         const uint2 w = *reinterpret_cast<const uint2*>(kb + off);
         const _Float16 sc = tok0 + n < nkeys ? clamp_scale(ksc[n * NB + c / 2]) : (_Float16)0.0f;
         *reinterpret_cast<half8*>(out + 8 * fl) = codes8_to_half8(w.x, w.y) * (half8)sc;
@@ -199,6 +207,21 @@ __global__ void __launch_bounds__(256) expand_kernel(ExpandArgs a) {
         const uint32_t fl = tid + 256 * u;
         const uint32_t f = fl / 64, l = fl % 64, n = l % 32, hh = l / 32;
         const uint32_t mt = f / 2, kc = f % 2;
+        if (geo.v_f16) {
+            const _Float16* vd16 = vb16 + (32 * mt + n) * 32;
+            half4 a0 = *reinterpret_cast<const half4*>(vd16 + 8 * hh + 4 * kc);
+            half4 a1 = *reinterpret_cast<const half4*>(vd16 + 8 * (2 + hh) + 4 * kc);
+#pragma unroll
+            for (uint32_t i = 0; i < 4; ++i) {  // keys 16kc + 4hh + i and 16kc + 8 + 4hh + i
+                if (tok0 + 16 * kc + 4 * hh + i >= nkeys) a0[i] = (_Float16)0.0f;
+                if (tok0 + 16 * kc + 8 + 4 * hh + i >= nkeys) a1[i] = (_Float16)0.0f;
+            }
+            half8 r;
+            r.lo = a0;
+            r.hi = a1;
+            *reinterpret_cast<half8*>(out + 64 * 8 * NKF + 8 * fl) = r;
+            continue;
+        }
         const int8_t* vd = vb + (32 * mt + n) * 32;
         const uint32_t w0 = *reinterpret_cast<const uint32_t*>(vd + 8 * hh + 4 * kc);
         const uint32_t w1 = *reinterpret_cast<const uint32_t*>(vd + 8 * (2 + hh) + 4 * kc);
@@ -637,6 +660,7 @@ static miikv_status suffix_impl(const miikv_view* view, const uint16_t* k_new, c
     if ((gate == nullptr) != (gated_out == nullptr)) return MIIKV_EINVAL;
     if (view->layout == MIIKV_LAYOUT_CONTIGUOUS && seq != 0) return MIIKV_EINVAL;
     if (token_count == 0) return MIIKV_OK;
+    if (k_new != nullptr && view->quant_mode != MIIKV_KV_Q8_Q8) return MIIKV_EUNSUPPORTED;  // stores q8 rows
     const uint64_t cap = view_seq_capacity(view);
     if (prefill_state == nullptr && static_cast<uint64_t>(base_position) + token_count > cap) return MIIKV_EINVAL;
     const uint64_t rows = static_cast<uint64_t>(token_count) * G;

@@ -52,40 +52,49 @@ class KvCache:
     """
 
     def __init__(self, kv_heads: int, head_dim: int, page_tokens: int, num_pages: int,
-                 block_table: torch.Tensor | None = None, device="cuda"):
+                 block_table: torch.Tensor | None = None, device="cuda", quant_mode: int = _lib.KV_Q8_Q8):
         if page_tokens % 64 != 0:
             raise ValueError("page_tokens must be a multiple of 64")
+        if quant_mode not in (_lib.KV_FP16_FP16, _lib.KV_Q8_FP16, _lib.KV_FP16_Q8, _lib.KV_Q8_Q8):
+            raise ValueError("unknown quant_mode")
         self.kv_heads = kv_heads
         self.head_dim = head_dim
         self.page_tokens = page_tokens
         self.num_pages = num_pages
         self.paged = block_table is not None
         self.block_table = block_table
+        self.quant_mode = quant_mode
+        # K / V planes: q8 codes + one fp16 scale per 32 values (KvCacheQuantMode Q8), or
+        # fp16 rows without scales (the reference's FP16 modes, kv_cache.hpp:16-21)
+        self.k_f16 = quant_mode in (_lib.KV_FP16_FP16, _lib.KV_FP16_Q8)
+        self.v_f16 = quant_mode in (_lib.KV_FP16_FP16, _lib.KV_Q8_FP16)
         n = num_pages * kv_heads * page_tokens
-        self.k_codes = torch.zeros(n * head_dim, dtype=torch.int8, device=device)
-        self.v_codes = torch.zeros(n * head_dim, dtype=torch.int8, device=device)
-        self.k_scales = torch.zeros(n * (head_dim // QBLOCK), dtype=torch.int16, device=device)
-        self.v_scales = torch.zeros(n * (head_dim // QBLOCK), dtype=torch.int16, device=device)
+        nb = n * (head_dim // QBLOCK)
+        self.k_codes = torch.zeros(n * head_dim, dtype=torch.float16 if self.k_f16 else torch.int8, device=device)
+        self.v_codes = torch.zeros(n * head_dim, dtype=torch.float16 if self.v_f16 else torch.int8, device=device)
+        self.k_scales = None if self.k_f16 else torch.zeros(nb, dtype=torch.int16, device=device)
+        self.v_scales = None if self.v_f16 else torch.zeros(nb, dtype=torch.int16, device=device)
         self._view = MiikvView()
         self._refresh_view()
 
     @classmethod
-    def contiguous(cls, kv_heads: int, head_dim: int, capacity: int, device="cuda") -> "KvCache":
-        return cls(kv_heads, head_dim, capacity, 1, None, device)
+    def contiguous(cls, kv_heads: int, head_dim: int, capacity: int, device="cuda",
+                   quant_mode: int = _lib.KV_Q8_Q8) -> "KvCache":
+        return cls(kv_heads, head_dim, capacity, 1, None, device, quant_mode)
 
     @classmethod
     def paged_cache(cls, kv_heads: int, head_dim: int, num_pages: int, block_table: torch.Tensor,
-                    page_tokens: int = 256, device="cuda") -> "KvCache":
-        return cls(kv_heads, head_dim, page_tokens, num_pages, block_table, device)
+                    page_tokens: int = 256, device="cuda", quant_mode: int = _lib.KV_Q8_Q8) -> "KvCache":
+        return cls(kv_heads, head_dim, page_tokens, num_pages, block_table, device, quant_mode)
 
     def _refresh_view(self) -> None:
         v = self._view
         v.k_codes = self.k_codes.data_ptr()
-        v.k_scales = self.k_scales.data_ptr()
+        v.k_scales = None if self.k_scales is None else self.k_scales.data_ptr()
         v.v_codes = self.v_codes.data_ptr()
-        v.v_scales = self.v_scales.data_ptr()
+        v.v_scales = None if self.v_scales is None else self.v_scales.data_ptr()
         v.layout = _lib.LAYOUT_PAGED if self.paged else _lib.LAYOUT_CONTIGUOUS
-        v.quant_mode = _lib.KV_Q8_Q8
+        v.quant_mode = self.quant_mode
         v.kv_heads = self.kv_heads
         v.head_dim = self.head_dim
         v.page_tokens = self.page_tokens
@@ -120,12 +129,14 @@ class KvCache:
     def reset(self) -> None:
         """Zero every plane (src/prefill_v2/kv_cache.cpp:99-130)."""
         for t in (self.k_codes, self.v_codes, self.k_scales, self.v_scales):
-            t.zero_()
+            if t is not None:
+                t.zero_()
 
     def raw_tokens_bytes(self, tokens: int) -> int:
         """Bytes of the raw compact form of `tokens` tokens (kv_cache.cpp:214-225,
         with one fp16 scale per 32-value block)."""
-        return 2 * tokens * self.kv_heads * (self.head_dim + 2 * (self.head_dim // QBLOCK))
+        per = {False: self.head_dim + 2 * (self.head_dim // QBLOCK), True: 2 * self.head_dim}
+        return tokens * self.kv_heads * (per[self.k_f16] + per[self.v_f16])
 
     # ---- append ----------------------------------------------------------
     def append(self, k: torch.Tensor, v: torch.Tensor, base_position: int = 0, seq: int = 0,
@@ -194,14 +205,16 @@ class KvCache:
     # ---- canonical export / import ------------------------------------------
     def export_canonical(self, seq: int, t0: int, count: int, stream=None):
         """Return (k_codes, k_scales, v_codes, v_scales) canonical device tensors:
-        codes [kv_heads, count, head_dim] int8, scales [kv_heads, count, head_dim/32] int16."""
+        codes [kv_heads, count, head_dim] int8, scales [kv_heads, count, head_dim/32] int16;
+        an fp16 plane gives its rows [kv_heads, count, head_dim] fp16 and no scales (None)."""
         self._check_seq(seq)
         dev = self.k_codes.device
-        kc = torch.empty((self.kv_heads, count, self.head_dim), dtype=torch.int8, device=dev)
-        vc = torch.empty_like(kc)
-        ks = torch.empty((self.kv_heads, count, self.head_dim // QBLOCK), dtype=torch.int16,
-                         device=dev)
-        vs = torch.empty_like(ks)
+        shape = (self.kv_heads, count, self.head_dim)
+        sshape = (self.kv_heads, count, self.head_dim // QBLOCK)
+        kc = torch.empty(shape, dtype=torch.float16 if self.k_f16 else torch.int8, device=dev)
+        vc = torch.empty(shape, dtype=torch.float16 if self.v_f16 else torch.int8, device=dev)
+        ks = None if self.k_f16 else torch.empty(sshape, dtype=torch.int16, device=dev)
+        vs = None if self.v_f16 else torch.empty(sshape, dtype=torch.int16, device=dev)
         call("miikv_export_canonical", self.view, seq, t0, count, _ptr(kc), _ptr(ks), _ptr(vc),
              _ptr(vs), _stream(stream))
         return kc, ks, vc, vs
@@ -239,11 +252,20 @@ class KvCache:
         self._check_seq(seq)
         count = kc.shape[1]
         nb = self.head_dim // QBLOCK
-        for t, last, dt in ((kc, self.head_dim, torch.int8), (vc, self.head_dim, torch.int8),
-                            (ks, nb, torch.int16), (vs, nb, torch.int16)):
-            if tuple(t.shape) != (self.kv_heads, count, last) or t.dtype != dt or \
+        planes = [(kc, self.head_dim, torch.float16 if self.k_f16 else torch.int8),
+                  (vc, self.head_dim, torch.float16 if self.v_f16 else torch.int8)]
+        if not self.k_f16:
+            planes.append((ks, nb, torch.int16))
+        if not self.v_f16:
+            planes.append((vs, nb, torch.int16))
+        for t, last, dt in planes:
+            if t is None or tuple(t.shape) != (self.kv_heads, count, last) or t.dtype != dt or \
                     not t.is_contiguous():
                 raise ValueError("canonical planes have the wrong shape or dtype")
+        if self.k_f16:
+            ks = None
+        if self.v_f16:
+            vs = None
         call("miikv_import_canonical", self.view, seq, t0, count, _ptr(kc), _ptr(ks), _ptr(vc),
              _ptr(vs), _stream(stream))
 
@@ -255,10 +277,11 @@ class KvCache:
         parts = []
         for codes, scales in ((kc, ks), (vc, vs)):
             c = codes.cpu().numpy()
-            s = scales.cpu().numpy()
+            s = None if scales is None else scales.cpu().numpy()
             for h in range(self.kv_heads):
                 parts.append(c[h].tobytes())
-                parts.append(s[h].tobytes())
+                if s is not None:
+                    parts.append(s[h].tobytes())
         return b"".join(parts)
 
     def upload_raw(self, raw: bytes, tokens: int, seq: int = 0) -> None:
@@ -270,7 +293,14 @@ class KvCache:
         buf = np.frombuffer(raw, dtype=np.uint8)
         off = 0
         out = []
-        for _ in range(2):
+        for f16 in (self.k_f16, self.v_f16):
+            if f16:  # fp16 rows per kv head, no scales
+                c = np.empty((hk, tokens, d), np.float16)
+                for h in range(hk):
+                    c[h] = buf[off:off + tokens * d * 2].view(np.float16).reshape(tokens, d)
+                    off += tokens * d * 2
+                out += [torch.from_numpy(c).to(self.k_codes.device), None]
+                continue
             c = np.empty((hk, tokens, d), np.int8)
             s = np.empty((hk, tokens, nb), np.int16)
             for h in range(hk):

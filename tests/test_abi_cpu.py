@@ -64,7 +64,9 @@ def test_version_and_status_strings():
 
 
 @pytest.mark.parametrize("over,status", [
-    ({"head_dim": 64}, 2), ({"quant_mode": 0}, 2), ({"page_tokens": 100}, 1),
+    ({"head_dim": 64}, 2), ({"quant_mode": 7}, 1), ({"page_tokens": 100}, 1),
+    # fp16 planes carry no scales; a q8 plane needs its scales
+    ({"quant_mode": 0, "k_scales": None, "v_scales": None}, 0), ({"quant_mode": 1, "k_scales": None}, 1),
     ({"kv_heads": 0}, 1), ({"layout": 7}, 1), ({"num_pages": 2}, 1),
     ({"layout": 1, "num_pages": 4}, 1),  # paged without a block table
 ])
