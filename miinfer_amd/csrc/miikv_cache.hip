@@ -40,7 +40,7 @@ struct AppendIn {
     const void* k;
     const void* v;
     const float* k_norm_weight;  // fp32 input only; null: no prologue
-    float theta;
+    float rope_step;             // theta^(-2/64), computed once on the host
     float epsilon;
 };
 
@@ -55,18 +55,62 @@ __device__ __forceinline__ void load16_f32(const float* p, float (&x)[16]) {
     }
 }
 
-// K prologue on one lane's 16 dims d0 = 16*q16 ..: the row's sum of squares is
-// reduced over its D/16 lanes; RoPE pairs (i, i+32), i < 32, sit in lanes q16
-// and q16 ^ 2.  Pair i's angle is position * s^i with s = theta^(-2/64),
-// accumulated by repeated fp32 multiplication as in the reference
-// (gfx906/kernels/qwen3_primitives.hip:622-659, 7257-7281).
+// sin and cos of a RoPE angle (|a| < 2^17), the same float arithmetic in the CPU oracle
+// so the rotated keys are bit-identical there: a Cody-Waite reduction by pi/2 in three
+// parts (1.5703125 holds 8 bits, so k * P1 is exact for k < 2^16) with fused
+// multiply-adds, then the Taylor polynomials of sin and cos on [-pi/4, pi/4] (truncation
+// below 1e-11) in Horner form, and the quadrant.  Within two ulps of sin and cos.
+__device__ __forceinline__ void rope_sincos(float a, float* s, float* c) {
+#pragma clang fp contract(off)
+    const float k = rintf(a * 6.366197467e-01f);
+    float r = fmaf(-k, 1.5703125f, a);
+    r = fmaf(-k, 4.838267923e-04f, r);
+    r = fmaf(-k, 2.563282919e-12f, r);
+    const float r2 = r * r;
+    float ps = fmaf(r2, -2.505210794e-08f, 2.755731884e-06f);
+    ps = fmaf(r2, ps, -1.984127011e-04f);
+    ps = fmaf(r2, ps, 8.333333768e-03f);
+    ps = fmaf(r2, ps, -1.666666716e-01f);
+    const float sr = fmaf(r * r2, ps, r);
+    float pc = fmaf(r2, 2.087675588e-09f, -2.755731998e-07f);
+    pc = fmaf(r2, pc, 2.480158764e-05f);
+    pc = fmaf(r2, pc, -1.388888923e-03f);
+    pc = fmaf(r2, pc, 4.166666791e-02f);
+    pc = fmaf(r2, pc, -5.000000000e-01f);
+    const float cr = fmaf(r2, pc, 1.0f);
+    const int q = static_cast<int>(k) & 3;
+    *s = q == 0 ? sr : q == 1 ? cr : q == 2 ? -sr : -cr;
+    *c = q == 0 ? cr : q == 1 ? -sr : q == 2 ? -cr : sr;
+}
+
+// K prologue on one lane's 16 dims d0 = 16*q16 ..: RMSNorm * weight, then RoPE on
+// dims 0..63 (gfx906/kernels/qwen3_primitives.hip:7257-7281, 622-659).
+// The sum of squares follows the reference's 256-lane LDS tree exactly: element t
+// first meets t + D/2 (lanes q16 and q16 ^ groups/2), then t + D/4, ... down to the
+// lane's own 16 values, pairs 8, 4, 2, 1 apart.  r = 1 / sqrt(ss / D + eps) with the
+// correctly rounded square root and division (the reference's rsqrtf is the
+// hardware approximation, within one ulp of it), value * r * weight in that order.
+// RoPE pairs (i, i+32), i < 32, sit in lanes q16 and q16 ^ 2; pair i's angle is
+// position * step^i, accumulated by repeated fp32 multiplication as the reference
+// does, with step = theta^(-2/64) computed once on the host (one powf for every
+// kernel, so the angles are the ones a host computes), and rotated with rope_sincos
+// (the reference calls cosf and sinf).  No contraction into fused multiply-adds: every
+// product and sum rounds as written, as in the oracle.
 __device__ __forceinline__ void k_norm_rope16(float (&x)[16], const float* w, uint32_t q16, uint32_t groups,
-                                              uint32_t D, uint32_t position, float theta, float eps) {
-    float ss = 0.0f;
+                                              uint32_t D, uint32_t position, float step, float eps) {
+#pragma clang fp contract(off)
+    float sq[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) ss += x[i] * x[i];
-    for (uint32_t o = 1; o < groups; o <<= 1) ss += __shfl_xor(ss, o, 64);
-    const float r = rsqrtf(ss / static_cast<float>(D) + eps);
+    for (int i = 0; i < 16; ++i) sq[i] = x[i] * x[i];
+    for (uint32_t o = groups / 2; o > 0; o >>= 1) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sq[i] += __shfl_xor(sq[i], o, 64);
+    }
+#pragma unroll
+    for (int s2 = 8; s2 > 0; s2 >>= 1)
+#pragma unroll
+        for (int i = 0; i < s2; ++i) sq[i] += sq[i + s2];
+    const float r = 1.0f / sqrtf(sq[0] / static_cast<float>(D) + eps);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const float4 wv = *reinterpret_cast<const float4*>(w + 16 * q16 + 4 * i);
@@ -79,7 +123,6 @@ __device__ __forceinline__ void k_norm_rope16(float (&x)[16], const float* w, ui
 #pragma unroll
     for (int i = 0; i < 16; ++i) partner[i] = dpp_mov<0x4E>(x[i]);  // lane ^ 2
     if (q16 >= 4) return;
-    const float step = powf(theta, -2.0f / 64.0f);
     float angle = static_cast<float>(position);
     const uint32_t i0 = 16 * (q16 & 1);  // first pair index of this lane
     for (uint32_t i = 0; i < i0; ++i) angle *= step;
@@ -87,7 +130,7 @@ __device__ __forceinline__ void k_norm_rope16(float (&x)[16], const float* w, ui
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
         float sn, cs;
-        sincosf(angle, &sn, &cs);
+        rope_sincos(angle, &sn, &cs);
         if (low) x[j] = x[j] * cs - partner[j] * sn;
         else x[j] = partner[j] * sn + x[j] * cs;
         angle *= step;
@@ -145,7 +188,7 @@ __global__ void __launch_bounds__(256) append_kernel(
         load16_f32(static_cast<const float*>(in.k) + src, xk);
         load16_f32(static_cast<const float*>(in.v) + src, xv);
         if (in.k_norm_weight != nullptr)
-            k_norm_rope16(xk, in.k_norm_weight, q16, groups, D, pos, in.theta, in.epsilon);
+            k_norm_rope16(xk, in.k_norm_weight, q16, groups, D, pos, in.rope_step, in.epsilon);
     } else {
         load16_f16(static_cast<const uint16_t*>(in.k) + src, xk);
         load16_f16(static_cast<const uint16_t*>(in.v) + src, xv);
@@ -222,7 +265,7 @@ __global__ void __launch_bounds__(512) append_tile_kernel(Geo g, AppendIn in, ui
         load16_f32(static_cast<const float*>(in.k) + src, xk);
         load16_f32(static_cast<const float*>(in.v) + src, xv);
         if (in.k_norm_weight != nullptr)
-            k_norm_rope16(xk, in.k_norm_weight, q16, groups, D, pos, in.theta, in.epsilon);
+            k_norm_rope16(xk, in.k_norm_weight, q16, groups, D, pos, in.rope_step, in.epsilon);
     } else {
         load16_f16(static_cast<const uint16_t*>(in.k) + src, xk);
         load16_f16(static_cast<const uint16_t*>(in.v) + src, xv);
@@ -684,7 +727,7 @@ extern "C" miikv_status miikv_append_f32(const miikv_view* view, const float* k,
     in.k = k;
     in.v = v;
     in.k_norm_weight = k_norm_weight;
-    in.theta = theta;
+    in.rope_step = powf(theta, -2.0f / 64.0f);
     in.epsilon = epsilon;
     return launch_append<true>(view, in, token_count, base_position, seq, prefill_state, decode_state, nullptr,
                                stream);

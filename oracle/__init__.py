@@ -47,6 +47,8 @@ def _load() -> ctypes.CDLL:
     lib.miikv_oracle_q8_0_block.argtypes = [_f32p, _i8p, _u16p]
     lib.miikv_oracle_quantize_rows_f16.argtypes = [_u16p, ctypes.c_size_t, _u32, _i8p, _u16p]
     lib.miikv_oracle_quantize_rows_f32.argtypes = [_f32p, ctypes.c_size_t, _u32, _i8p, _u16p]
+    lib.miikv_oracle_rope_sincos.argtypes = [ctypes.c_float, ctypes.POINTER(ctypes.c_float),
+                                             ctypes.POINTER(ctypes.c_float)]
     lib.miikv_oracle_k_norm_rope.argtypes = [_f32p, _f32p, _u32, _u32, ctypes.c_float, ctypes.c_float, _f32p]
     lib.miikv_oracle_q8_1_block.argtypes = [_f32p, ctypes.POINTER(ctypes.c_uint8)]
     lib.miikv_oracle_dequantize_rows.argtypes = [_i8p, _u16p, ctypes.c_size_t, _u32, _f32p]
@@ -138,10 +140,19 @@ def quantize_rows_f32(rows: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     return codes, scales
 
 
+def rope_sincos(a: float):
+    """(sin, cos) of a float32 angle with the prologue's float arithmetic."""
+    s, c = ctypes.c_float(), ctypes.c_float()
+    lib().miikv_oracle_rope_sincos(a, ctypes.byref(s), ctypes.byref(c))
+    return s.value, c.value
+
+
 def k_norm_rope(x: np.ndarray, w: np.ndarray, position: int, theta: float, eps: float) -> np.ndarray:
     """One K row after the reference's RMSNorm * weight and RoPE on dims 0..63."""
     x = np.ascontiguousarray(x, np.float32)
     w = np.ascontiguousarray(w, np.float32)
+    if x.size not in (64, 128, 256, 512):
+        raise ValueError("head_dim must be a power of two in [64, 512] (the tree reduction)")
     out = np.zeros_like(x)
     lib().miikv_oracle_k_norm_rope(_p(x, _f32p), _p(w, _f32p), x.size, position, theta, eps, _p(out, _f32p))
     return out

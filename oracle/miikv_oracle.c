@@ -120,19 +120,53 @@ void miikv_oracle_quantize_rows_f32(const float* rows, size_t n_rows, uint32_t h
                                     codes + r * head_dim + (size_t)b * MIIKV_ORACLE_QBLOCK, scales + r * nblk + b);
 }
 
+/* sin and cos of a RoPE angle with the float arithmetic of the library's prologue
+ * (miinfer_amd/csrc/miikv_cache.hip rope_sincos): Cody-Waite reduction by pi/2 in three
+ * parts with fused multiply-adds, Taylor polynomials on [-pi/4, pi/4], quadrant.  The
+ * reference calls cosf / sinf (qwen3_primitives.hip:651-652); this pair is pinned
+ * against float64 sin / cos in the tests (within two ulps). */
+void miikv_oracle_rope_sincos(float a, float* s, float* c) {
+    const float k = rintf(a * 6.366197467e-01f);
+    float r = fmaf(-k, 1.5703125f, a);
+    r = fmaf(-k, 4.838267923e-04f, r);
+    r = fmaf(-k, 2.563282919e-12f, r);
+    const float r2 = r * r;
+    float ps = fmaf(r2, -2.505210794e-08f, 2.755731884e-06f);
+    ps = fmaf(r2, ps, -1.984127011e-04f);
+    ps = fmaf(r2, ps, 8.333333768e-03f);
+    ps = fmaf(r2, ps, -1.666666716e-01f);
+    const float sr = fmaf(r * r2, ps, r);
+    float pc = fmaf(r2, 2.087675588e-09f, -2.755731998e-07f);
+    pc = fmaf(r2, pc, 2.480158764e-05f);
+    pc = fmaf(r2, pc, -1.388888923e-03f);
+    pc = fmaf(r2, pc, 4.166666791e-02f);
+    pc = fmaf(r2, pc, -5.000000000e-01f);
+    const float cr = fmaf(r2, pc, 1.0f);
+    const int q = (int)k & 3;
+    *s = q == 0 ? sr : q == 1 ? cr : q == 2 ? -sr : -cr;
+    *c = q == 0 ? cr : q == 1 ? -sr : q == 2 ? -cr : sr;
+}
+
 /* gfx906/kernels/qwen3_primitives.hip:7257-7281 (RMSNorm * weight, RoPE on dims
  * 0..63) and :622-659 (compute_qwen35_rope_pair: every pair < 32 falls in a
  * rotated section, and the three section angles are the same position). */
 void miikv_oracle_k_norm_rope(const float* x, const float* w, uint32_t head_dim, uint32_t position, float theta,
                               float eps, float* out) {
-    float ss = 0.0f;
-    for (uint32_t d = 0; d < head_dim; ++d) ss += x[d] * x[d];
+    /* sum of squares in the reference's LDS tree order (qwen3_primitives.hip:7257-7263):
+     * p[t] = x[t]^2, then p[t] += p[t + stride] for stride = D/2, D/4, ..., 1 */
+    float p[512];
+    for (uint32_t d = 0; d < head_dim; ++d) p[d] = x[d] * x[d];
+    for (uint32_t stride = head_dim / 2; stride > 0; stride /= 2)
+        for (uint32_t t = 0; t < stride; ++t) p[t] += p[t + stride];
+    const float ss = p[0];
+    /* the reference takes rsqrtf (a hardware approximation within one ulp of this) */
     const float r = 1.0f / sqrtf(ss / (float)head_dim + eps);
     for (uint32_t d = 0; d < head_dim; ++d) out[d] = x[d] * r * w[d];
     const float step = powf(theta, -2.0f / 64.0f);
     float angle = (float)position;
     for (uint32_t i = 0; i < 32; ++i) {
-        const float c = cosf(angle), s = sinf(angle);
+        float s, c;
+        miikv_oracle_rope_sincos(angle, &s, &c);
         const float x0 = out[i], x1 = out[i + 32];
         out[i] = x0 * c - x1 * s;
         out[i + 32] = x0 * s + x1 * c;

@@ -51,6 +51,7 @@ void miikv_oracle_quantize_rows_f32(const float* rows, size_t n_rows, uint32_t h
  *   for i < 32: a = position * s^i with s = powf(theta, -2/64) accumulated by
  *   repeated fp32 multiplication; (y_i, y_{i+32}) <- (y_i cos a - y_{i+32} sin a,
  *   y_i sin a + y_{i+32} cos a).  Dims >= 64 are only normalised. */
+void miikv_oracle_rope_sincos(float a, float* s, float* c);
 void miikv_oracle_k_norm_rope(const float* x, const float* w, uint32_t head_dim, uint32_t position, float theta,
                               float eps, float* out);
 

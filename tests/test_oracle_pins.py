@@ -329,3 +329,52 @@ def test_q8_1_rounds_half_away_and_zero_block():
     assert list(q[:5]) == [127, 3, -3, 1, -2]
     z = oracle.q8_1_blocks(np.zeros(32, np.float32))[0]
     assert not z.any()  # d = 0, inverse 0, all codes 0, s = 0
+
+
+@pytest.mark.parametrize("d", [128, 256])
+def test_k_norm_sum_of_squares_follows_the_reference_tree(d):
+    """At position 0 the prologue is RMSNorm * weight; its sum of squares is reduced in
+    the reference's LDS tree order (p[t] += p[t + stride], stride = D/2 .. 1,
+    qwen3_primitives.hip:7257-7263), then value * (1 / sqrt(ss / D + eps)) * weight.
+    Restated here with numpy float32 vector ops; a sequential sum differs in the last
+    bits for some rows, which this catches."""
+    rng = np.random.default_rng(d)
+    seq_differs = 0
+    for _ in range(50):
+        x = (rng.standard_normal(d) * 3).astype(np.float32)
+        w = rng.uniform(0.5, 1.5, d).astype(np.float32)
+        p = x * x
+        s = d // 2
+        while s > 0:
+            p[:s] = p[:s] + p[s:2 * s]
+            s //= 2
+        r = np.float32(1.0) / np.sqrt(p[0] / np.float32(d) + np.float32(1e-6))
+        expect = (x * r) * w
+        got = oracle.k_norm_rope(x, w, 0, 1.0e6, 1.0e-6)
+        assert np.array_equal(got.view(np.uint32), expect.view(np.uint32))
+        seq = np.float32(0)
+        for v in x * x:
+            seq = np.float32(seq + v)
+        seq_differs += int(seq != p[0])
+    assert seq_differs > 0  # the order is observable at this size
+
+
+def test_rope_sincos_close_to_float64():
+    """The prologue's sin/cos pair against float64 sin and cos of the same float32 angle,
+    over the RoPE angle range (positions < 2^16 times step^i <= 1) and around multiples of
+    pi/2, where the reduction matters: within 2.5 float32 ulps where |value| >= 1/16 and
+    within 1e-7 absolute everywhere (libm's sinf/cosf are within half an ulp; a wrong
+    quadrant, sign, reduction constant or polynomial coefficient is off by far more)."""
+    rng = np.random.default_rng(7)
+    angles = np.concatenate([
+        rng.uniform(0, 65536, 4000), rng.uniform(0, 8, 2000),
+        (np.arange(1, 40000, 37) * (np.pi / 2))[:1000] + rng.uniform(-1e-3, 1e-3, 1000),
+        [0.0, 1e-8, 0.5, 1.0, 65535.0]]).astype(np.float32)
+    worst_ulps, worst_abs = 0.0, 0.0
+    for a in angles:
+        s, c = oracle.rope_sincos(float(a))
+        for got, exact in ((s, np.sin(np.float64(a))), (c, np.cos(np.float64(a)))):
+            if abs(exact) >= 1.0 / 16:
+                worst_ulps = max(worst_ulps, abs(got - exact) / float(np.spacing(np.float32(abs(exact)))))
+            worst_abs = max(worst_abs, abs(got - exact))
+    assert worst_ulps <= 2.5 and worst_abs <= 1e-7, (worst_ulps, worst_abs)
