@@ -279,13 +279,37 @@ __device__ void append_record(const SplitArgs& a, uint32_t b, uint32_t h, uint32
 // one-step ring (fp16 fragments take twice the registers).
 // Waves per SIMD of a decode_kernel instance: the tuned value, except q8 keys with fp16
 // values at D = 256, which need a wave's full register file (two waves spilled 122).
+// Lane n of a row of 16 takes the value of lane n + k (DPP row_shl); k <= 8.
+template <uint32_t K>
+__device__ __forceinline__ float dpp_row_shl(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x100 + K, 0xF, 0xF,
+                                                                 false));
+}
+__device__ __forceinline__ float row_shl_by(float x, uint32_t k) {
+    switch (k) {
+        case 1: return dpp_row_shl<1>(x);
+        case 2: return dpp_row_shl<2>(x);
+        case 3: return dpp_row_shl<3>(x);
+        case 4: return dpp_row_shl<4>(x);
+        case 5: return dpp_row_shl<5>(x);
+        case 6: return dpp_row_shl<6>(x);
+        case 7: return dpp_row_shl<7>(x);
+        default: return dpp_row_shl<8>(x);
+    }
+}
+
 template <uint32_t D, bool QF32, bool KF16, bool VF16>
 constexpr uint32_t decode_waves_per_eu() {
     return (D == 256 && VF16 && !KF16) ? 1u : DecodeTuning<D, QF32>::waves_per_eu;
 }
-template <uint32_t D, bool QF32, bool APPEND, bool KF16 = false, bool VF16 = false>
+// An fp32 query is split into fp16 hi + lo parts.  QPAIR (G <= 8): the lo parts ride in
+// the QK MFMA's unused columns G..2G-1 (B operand column G + g = lo of head g), so one
+// MFMA per block carries both and the two column sums meet with one row shift per
+// score; the fp16-query register budget and occupancy then hold.  Otherwise (G > 8) the
+// lo parts are a second fragment set and a second MFMA per block.
+template <uint32_t D, bool QF32, bool APPEND, bool KF16 = false, bool VF16 = false, bool QPAIR = false>
 __global__ void __launch_bounds__(64 * kWavesPerWg)
-__attribute__((amdgpu_waves_per_eu(decode_waves_per_eu<D, QF32, KF16, VF16>())))
+__attribute__((amdgpu_waves_per_eu(decode_waves_per_eu<D, QF32 && !QPAIR, KF16, VF16>())))
 decode_kernel(SplitArgs a) {
     constexpr uint32_t NB = D / 32;   // q8_0 blocks per row
     constexpr uint32_t NC = D / 64;   // 16-byte K loads per tile row group
@@ -293,7 +317,9 @@ decode_kernel(SplitArgs a) {
     using ScaleVec = typename std::conditional<NB == 4, uint32_t, uint2>::type;  // NB/2 fp16 scales
     // V codes enter the PV MFMA biased (one v_perm per two codes) and the bias is removed
     // with column sums, or exactly (perm + subtract): the fold costs NB accumulators.
-    constexpr bool kVBias = DecodeTuning<D, QF32>::vbias && !VF16;
+    constexpr bool kLo = QF32 && !QPAIR;  // separate lo fragments and MFMAs
+    static_assert(!QPAIR || QF32, "QPAIR splits an fp32 query");
+    constexpr bool kVBias = DecodeTuning<D, kLo>::vbias && !VF16;
     static_assert(!APPEND || (!KF16 && !VF16), "the fused append stores q8 rows");
     extern __shared__ float smem[];
 
@@ -375,7 +401,7 @@ decode_kernel(SplitArgs a) {
         // Scales first, each ahead of its codes: loads complete in issue order, so the
         // score MFMAs wait only for the K scales and codes while V is still in flight.
         if constexpr (!KF16)
-            st.ks = load_scales<ScaleVec, DecodeTuning<D, QF32>::nt_scales>(geo.k_scales + sc0 + lane * (NB / 2));
+            st.ks = load_scales<ScaleVec, DecodeTuning<D, kLo>::nt_scales>(geo.k_scales + sc0 + lane * (NB / 2));
 #pragma unroll
         for (uint32_t J = 0; J < 2; ++J)
 #pragma unroll
@@ -384,7 +410,7 @@ decode_kernel(SplitArgs a) {
                 for (uint32_t e = 0; e < KE; ++e)
                     st.k[J][cc][e] = load16(kb + KE * (J * 16 * D + cc * 1024 + g4 * 256 + n * 16) + 16 * e);
         if constexpr (!VF16)
-            st.vs = load_scales<ScaleVec, DecodeTuning<D, QF32>::nt_scales>(geo.v_scales + sc0 + lane * (NB / 2));
+            st.vs = load_scales<ScaleVec, DecodeTuning<D, kLo>::nt_scales>(geo.v_scales + sc0 + lane * (NB / 2));
 #pragma unroll
         for (uint32_t mt = 0; mt < NM; ++mt) {
             if constexpr (VF16) st.v[mt] = load16(vb + 2 * ((16 * mt + n) * 32 + g4 * 8));
@@ -395,7 +421,7 @@ decode_kernel(SplitArgs a) {
     };
 
     // Ring of kRing step buffers; the first kRing-1 are loaded before L is known.
-    constexpr uint32_t kRing = (KF16 || VF16) ? 1u : DecodeTuning<D, QF32>::ring;
+    constexpr uint32_t kRing = (KF16 || VF16) ? 1u : DecodeTuning<D, kLo>::ring;
     Step S[kRing];
 #pragma unroll
     for (uint32_t r = 0; r + 1 < kRing; ++r)
@@ -406,7 +432,8 @@ decode_kernel(SplitArgs a) {
     uint4 qraw[QF32 ? 1 : NB];
     float4 q32raw[QF32 ? NB : 1][2];
     {
-        const size_t qrow = (static_cast<size_t>(b) * a.q_heads + static_cast<size_t>(h) * G + min(n, G - 1)) * D;
+        const uint32_t qh = QPAIR && n >= G ? min(n - G, G - 1) : min(n, G - 1);
+        const size_t qrow = (static_cast<size_t>(b) * a.q_heads + static_cast<size_t>(h) * G + qh) * D;
 #pragma unroll
         for (uint32_t blk = 0; blk < NB; ++blk) {
             if constexpr (QF32) {
@@ -428,17 +455,27 @@ decode_kernel(SplitArgs a) {
     // (code + 1152) (see codes4_to_half_biased), so each block's dot carries an
     // extra 1152 * sum(q_blk); the accumulator starts at minus that amount.
     half8 qf[NB];
-    half8 ql[QF32 ? NB : 1];
+    half8 ql[kLo ? NB : 1];
     float kbias[NB];
     {
-        const size_t qrow = (static_cast<size_t>(b) * a.q_heads + static_cast<size_t>(h) * G + n) * D;
 #pragma unroll
         for (uint32_t blk = 0; blk < NB; ++blk) {
             half8 v = {};
             half8 lo = {};
             float qs = 0.0f;
-            if (n < G) {
-                if constexpr (QF32) {
+            if (n < (QPAIR ? 2 * G : G)) {
+                if constexpr (QPAIR) {
+                    // columns < G: hi parts; columns G..2G-1: lo parts of head n - G
+                    const float4 x0 = q32raw[blk][0];
+                    const float4 x1 = q32raw[blk][1];
+                    const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const _Float16 hi = static_cast<_Float16>(xs[i]);
+                        v[i] = n < G ? hi : static_cast<_Float16>(xs[i] - static_cast<float>(hi));
+                        qs += static_cast<float>(v[i]);
+                    }
+                } else if constexpr (QF32) {
                     const float4 x0 = q32raw[blk][0];
                     const float4 x1 = q32raw[blk][1];
                     const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
@@ -458,7 +495,7 @@ decode_kernel(SplitArgs a) {
             qs = rows_reduce(qs, AddOp{});
             kbias[blk] = kCodeBias * qs;
             qf[blk] = v;
-            if (QF32) ql[QF32 ? blk : 0] = lo;
+            if (kLo) ql[kLo ? blk : 0] = lo;
         }
     }
 
@@ -527,10 +564,14 @@ decode_kernel(SplitArgs a) {
                     const half8 a1 = __builtin_bit_cast(half8, st.k[J][cc][KF16 ? 1 : 0]);  // block 2cc+1
                     c = mfma_16x16x32(a0, qf[2 * cc], c);
                     c = mfma_16x16x32(a1, qf[2 * cc + 1], c);
-                    if (QF32) {
-                        c = mfma_16x16x32(a0, ql[QF32 ? 2 * cc : 0], c);
-                        c = mfma_16x16x32(a1, ql[QF32 ? 2 * cc + 1 : 0], c);
+                    if (kLo) {
+                        c = mfma_16x16x32(a0, ql[kLo ? 2 * cc : 0], c);
+                        c = mfma_16x16x32(a1, ql[kLo ? 2 * cc + 1 : 0], c);
                     }
+                }
+                if constexpr (QPAIR) {
+#pragma unroll
+                    for (uint32_t i = 0; i < 4; ++i) c[i] += row_shl_by(c[i], G);  // + lo column
                 }
 #pragma unroll
                 for (uint32_t i = 0; i < 4; ++i) s[J][i] = c[i] * a.scale_log2;
@@ -558,15 +599,19 @@ decode_kernel(SplitArgs a) {
 #endif
                 float4v c0 = mfma_16x16x32(a0, qf[2 * cc], float4v{b0, b0, b0, b0});
                 float4v c1 = mfma_16x16x32(a1, qf[2 * cc + 1], float4v{b1, b1, b1, b1});
-                if (QF32) {
-                    c0 = mfma_16x16x32(a0, ql[QF32 ? 2 * cc : 0], c0);
-                    c1 = mfma_16x16x32(a1, ql[QF32 ? 2 * cc + 1 : 0], c1);
+                if (kLo) {
+                    c0 = mfma_16x16x32(a0, ql[kLo ? 2 * cc : 0], c0);
+                    c1 = mfma_16x16x32(a1, ql[kLo ? 2 * cc + 1 : 0], c1);
                 }
 #pragma unroll
                 for (uint32_t i = 0; i < 4; ++i) {
                     acc[i] = fmaf(c0[i], f16_bits_to_f32(ks16[i * NB + 2 * cc]), acc[i]);
                     acc[i] = fmaf(c1[i], f16_bits_to_f32(ks16[i * NB + 2 * cc + 1]), acc[i]);
                 }
+            }
+            if constexpr (QPAIR) {
+#pragma unroll
+                for (uint32_t i = 0; i < 4; ++i) acc[i] += row_shl_by(acc[i], G);  // + lo column
             }
 #pragma unroll
             for (uint32_t i = 0; i < 4; ++i) {
@@ -731,6 +776,7 @@ decode_kernel(SplitArgs a) {
 
 // Workgroups of decode_kernel resident on the chip at its occupancy: 256 CUs x 4
 // SIMDs x waves per SIMD, 4 waves per workgroup.
+// f32: an fp32 query with separate lo fragments (more than 8 heads per kv head).
 uint32_t resident_workgroups(uint32_t D, bool f32, uint32_t mode) {
     uint32_t wpe = D == 128 ? (f32 ? DecodeTuning<128, true>::waves_per_eu : DecodeTuning<128, false>::waves_per_eu)
                             : (f32 ? DecodeTuning<256, true>::waves_per_eu : DecodeTuning<256, false>::waves_per_eu);
@@ -812,7 +858,11 @@ extern "C" miikv_status miikv_workspace_init(void* workspace, uint64_t bytes, vo
 namespace {
 template <uint32_t D, bool F32, bool APP, bool KF, bool VF>
 void launch_decode_t(dim3 grid, size_t lds, hipStream_t s, const SplitArgs& a) {
-    hipLaunchKernelGGL((decode_kernel<D, F32, APP, KF, VF>), grid, dim3(64 * kWavesPerWg), lds, s, a);
+    // an fp32 query of up to 8 heads per kv head pairs its lo parts into the spare columns
+    if (F32 && 2 * a.group <= 16)
+        hipLaunchKernelGGL((decode_kernel<D, F32, APP, KF, VF, F32>), grid, dim3(64 * kWavesPerWg), lds, s, a);
+    else
+        hipLaunchKernelGGL((decode_kernel<D, F32, APP, KF, VF, false>), grid, dim3(64 * kWavesPerWg), lds, s, a);
 }
 // Runtime flags -> kernel instance.  The fused append exists for q8 planes only (the
 // caller has rejected it for the other modes).
@@ -901,7 +951,7 @@ static miikv_status decode_impl(const miikv_view* view, const uint16_t* k_new, c
                          (k_new != nullptr ? static_cast<uint64_t>(view->kv_heads) * batch : 0);
     if (wgs > 0x7fffffffu) return MIIKV_EINVAL;
     a.batch = batch;
-    a.slots = p.adaptive ? resident_workgroups(view->head_dim, q_dtype == MIIKV_DTYPE_F32, view->quant_mode) : 0u;
+    a.slots = p.adaptive ? resident_workgroups(view->head_dim, q_dtype == MIIKV_DTYPE_F32 && 2 * G > 16, view->quant_mode) : 0u;
     const dim3 grid(static_cast<uint32_t>(wgs));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool f32 = q_dtype == MIIKV_DTYPE_F32;
