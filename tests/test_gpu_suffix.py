@@ -195,3 +195,40 @@ def test_suffix_fused_append_paged_prefill_state(gpu):
     for x, y, z in zip(after, _canon_all(plain, 0, prefix + t + 20), before):
         assert np.array_equal(x[:, :prefix + t], y[:, :prefix + t])
         assert np.array_equal(x[:, prefix + t:], z[:, prefix + t:])  # past the device count: untouched
+
+
+@pytest.mark.parametrize("split", [True, False])
+def test_suffix_blocks_near_the_fp16_maximum(gpu, split):
+    """Blocks whose absmax sits within 0.8% of the fp16 maximum have scales above
+    511.75; the suffix path clamps those scales so that its fp16 tiles stay finite
+    (128 * 511.75 = 65504).  Keys and values hold such blocks here: the outputs stay
+    finite and equal the oracle over the clamped scales (relative 1e-2), while the
+    unclamped oracle differs by the clamp's factor on the affected values."""
+    import miinfer_amd as m
+    rng = np.random.default_rng(77)
+    hq, hk, d, prefix, t = 24, 4, 256, 500, 40
+    cache = m.KvCache.contiguous(hk, d, 576)
+    k = randn_f16(rng, (prefix + t, hk, d))
+    v = randn_f16(rng, (prefix + t, hk, d))
+    big = np.float16(65504.0)
+    v[::7, :, 32:64] = v[::7, :, 32:64] * np.float16(0.5)   # a block of each 7th row ...
+    v[::7, :, 40] = big                                      # ... with absmax 65504: scale 515.5
+    k[::11, :, 0:32] = k[::11, :, 0:32] * np.float16(0.01)
+    k[::11, :, 3] = np.float16(-65504.0)                     # keys with a huge negative entry
+    cache.append(_dev(k, gpu), _dev(v, gpu))
+    kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+    vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+    q = randn_f16(rng, (t, hq, d)) * np.float16(0.01)
+    out, _ = m.suffix_attention(cache, _dev(q, gpu), prefix, split=split)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.all(np.isfinite(got))
+    f16 = lambda bits: bits.view(np.float16).astype(np.float32)
+    clamp = lambda s: np.minimum(f16(s), np.float32(511.75)).astype(np.float16).view(np.uint16)
+    assert (f16(vs) > 511.75).any() and (f16(ks) > 511.75).any()
+    expect = oracle.suffix_attention_q8(q.astype(np.float32), kc, clamp(ks), vc, clamp(vs), prefix, hq,
+                                        1 / math.sqrt(d))
+    rel = np.linalg.norm(got - expect) / np.linalg.norm(expect)
+    assert rel <= 1e-2, rel
+    unclamped = oracle.suffix_attention_q8(q.astype(np.float32), kc, ks, vc, vs, prefix, hq, 1 / math.sqrt(d))
+    assert np.abs(unclamped - expect).max() > 1.0  # the clamp is visible at this size
