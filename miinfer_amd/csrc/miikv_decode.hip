@@ -725,12 +725,14 @@ decode_kernel(SplitArgs a) {
         for (uint32_t mt = 0; mt < NM; ++mt) O[mt] -= kCodeBias * vbias[mt / 2];
     }
 
-    // ---- wave-level sums, then cross-wave combine in LDS.
+    // ---- wave-level sums, then the cross-wave merge in LDS: each wave leaves its
+    // state there (float4 per lane, a layout whose stores hit distinct banks), one
+    // barrier, then every thread merges float4 slices of the record in wave order and
+    // stores them (no second barrier: each thread derives the merge weights itself).
     l_run = rows_reduce(l_run, AddOp{});
     float* s_m = smem;                          // [waves][16]
     float* s_l = smem + 16 * kWavesPerWg;       // [waves][16]
-    float* s_O = smem + 32 * kWavesPerWg;       // [waves][G][D]
-    __shared__ float s_M[16];
+    float4* s_O = reinterpret_cast<float4*>(smem + 32 * kWavesPerWg);  // [waves][NM][4 g4][G]
     if (g4 == 0) {
         s_m[wave * 16 + n] = m_run;
         s_l[wave * 16 + n] = l_run;
@@ -738,37 +740,42 @@ decode_kernel(SplitArgs a) {
     if (n < G) {
 #pragma unroll
         for (uint32_t mt = 0; mt < NM; ++mt)
-#pragma unroll
-            for (uint32_t i = 0; i < 4; ++i) s_O[(wave * G + n) * D + 16 * mt + 4 * g4 + i] = O[mt][i];
+            s_O[((wave * NM + mt) * 4 + g4) * G + n] = make_float4(O[mt][0], O[mt][1], O[mt][2], O[mt][3]);
     }
     __syncthreads();
 
     // Partial record of one split: [O: G*D][m: G][l: G] padded to a multiple of 4 floats,
     // so every record starts 16-byte aligned.
     const uint32_t rec = record_floats(G, D);
-    float* part = a.part + ((static_cast<size_t>(b) * geo.kv_heads + h) * (a.max_splits + 1)) * rec;
-    float* mine = part + static_cast<size_t>(split) * rec;
-    if (tid < G) {
+    float* mine = a.part + ((static_cast<size_t>(b) * geo.kv_heads + h) * (a.max_splits + 1) + split) * rec;
+    for (uint32_t c4 = tid; c4 < G * D / 4; c4 += blockDim.x) {
+        const uint32_t hn = (4 * c4) / D, dim = (4 * c4) % D;
+        const uint32_t mt = dim / 16, gq = (dim % 16) / 4;
+        float mw[kWavesPerWg];
         float M = -INFINITY;
-        for (uint32_t w = 0; w < kWavesPerWg; ++w) M = fmaxf(M, s_m[w * 16 + tid]);
+#pragma unroll
+        for (uint32_t w = 0; w < kWavesPerWg; ++w) {
+            mw[w] = s_m[w * 16 + hn];
+            M = fmaxf(M, mw[w]);
+        }
+        float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         float Ls = 0.0f;
+#pragma unroll
         for (uint32_t w = 0; w < kWavesPerWg; ++w) {
-            const float mw = s_m[w * 16 + tid];
-            if (mw != -INFINITY) Ls += s_l[w * 16 + tid] * exp2_safe(mw - M);
+            if (mw[w] == -INFINITY) continue;
+            const float f = exp2_safe(mw[w] - M);
+            const float4 v = s_O[((w * NM + mt) * 4 + gq) * G + hn];
+            o.x += v.x * f;
+            o.y += v.y * f;
+            o.z += v.z * f;
+            o.w += v.w * f;
+            Ls += s_l[w * 16 + hn] * f;
         }
-        s_M[tid] = M;
-        mine[G * D + tid] = M;
-        mine[G * D + G + tid] = Ls;
-    }
-    __syncthreads();
-    for (uint32_t idx = tid; idx < G * D; idx += blockDim.x) {
-        const uint32_t hn = idx / D;
-        float o = 0.0f;
-        for (uint32_t w = 0; w < kWavesPerWg; ++w) {
-            const float mw = s_m[w * 16 + hn];
-            if (mw != -INFINITY) o += s_O[w * G * D + idx] * exp2_safe(mw - s_M[hn]);
+        *reinterpret_cast<float4*>(mine + 4 * c4) = o;
+        if (dim == 0) {
+            mine[G * D + hn] = M;
+            mine[G * D + G + hn] = Ls;
         }
-        mine[idx] = o;
     }
 }
 
