@@ -33,7 +33,8 @@
 // Measurement switches (never defined by the product build; each gives wrong
 // results by design and exists to time one part of the kernel in isolation):
 // MIIKV_EXP_NO_LOOP (no step: the fixed cost of a launch), MIIKV_EXP_NO_COMPUTE
-// (loads only), MIIKV_EXP_NO_KBIAS (no code bias), MIIKV_EXP_EXP2F (library exp2).
+// (loads only), MIIKV_EXP_NO_KBIAS (no code bias), MIIKV_EXP_EXP2F (library exp2),
+// MIIKV_EXP_NO_COMBINE (D = 128: no combine launch).
 #include "miikv_common.hpp"
 #include "miikv_split.hpp"
 
@@ -968,6 +969,9 @@ static miikv_status decode_impl(const miikv_view* view, const uint16_t* k_new, c
     const bool kf = mode_k_f16(view->quant_mode), vf = mode_v_f16(view->quant_mode);
     if (view->head_dim == 128) {
         launch_decode<128>(f32, app, kf, vf, grid, lds, s, a);
+#ifdef MIIKV_EXP_NO_COMBINE
+        return hip_status(hipGetLastError());
+#endif
         if (app) hipLaunchKernelGGL((combine_kernel<128, true>), cgrid, dim3(256), 0, s, a);
         else hipLaunchKernelGGL((combine_kernel<128, false>), cgrid, dim3(256), 0, s, a);
     } else {
