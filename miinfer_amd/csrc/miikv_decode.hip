@@ -866,8 +866,10 @@ extern "C" miikv_status miikv_workspace_init(void* workspace, uint64_t bytes, vo
 namespace {
 template <uint32_t D, bool F32, bool APP, bool KF, bool VF>
 void launch_decode_t(dim3 grid, size_t lds, hipStream_t s, const SplitArgs& a) {
-    // an fp32 query of up to 8 heads per kv head pairs its lo parts into the spare columns
-    if (F32 && 2 * a.group <= 16)
+    // An fp32 query of up to 8 heads per kv head pairs its lo parts into the spare columns
+    // at D = 256, where the second fragment set costs occupancy; at D = 128 the second
+    // set fits and the pairing's per-score row shift (a switch on G) measured slower.
+    if (F32 && D == 256 && 2 * a.group <= 16)
         hipLaunchKernelGGL((decode_kernel<D, F32, APP, KF, VF, F32>), grid, dim3(64 * kWavesPerWg), lds, s, a);
     else
         hipLaunchKernelGGL((decode_kernel<D, F32, APP, KF, VF, false>), grid, dim3(64 * kWavesPerWg), lds, s, a);
@@ -959,7 +961,7 @@ static miikv_status decode_impl(const miikv_view* view, const uint16_t* k_new, c
                          (k_new != nullptr ? static_cast<uint64_t>(view->kv_heads) * batch : 0);
     if (wgs > 0x7fffffffu) return MIIKV_EINVAL;
     a.batch = batch;
-    a.slots = p.adaptive ? resident_workgroups(view->head_dim, q_dtype == MIIKV_DTYPE_F32 && 2 * G > 16, view->quant_mode) : 0u;
+    a.slots = p.adaptive ? resident_workgroups(view->head_dim, q_dtype == MIIKV_DTYPE_F32 && (view->head_dim == 128 || 2 * G > 16), view->quant_mode) : 0u;
     const dim3 grid(static_cast<uint32_t>(wgs));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool f32 = q_dtype == MIIKV_DTYPE_F32;
