@@ -430,11 +430,13 @@ def _graph_median(fn, steps_per_graph: int, replays: int = 30, warm: int = 5):
 
 
 def decode_variants(dev, ctx: int = 32768, nl: int = 8) -> dict:
-    """Two more config 2 lines at 32k, same rotation and protocol as the headline:
+    """More config 2 lines at 32k, same rotation and protocol as the headline:
     * reference_signature: the drop-in call sequence of the reference's decode step
       (attention_layer.cpp:599-632): miikv_append_f32 with the fused K RMSNorm + RoPE
       prologue on fp32 rows at the decode-state position, then miikv_decode_attn_q8_1 with
       an fp32 query, gate, gated output and the Q8_1 epilogue;
+    * reference_signature_fused: the same arguments through miikv_decode_append_attn_f32
+      (one launch pair);
     * fp16_control: attention over an FP16_FP16 cache (the reference's production default,
       qwen3_primitives.hip:2198-2293), attention only, 2x the KV bytes of q8_0."""
     import ctypes
@@ -480,6 +482,20 @@ def decode_variants(dev, ctx: int = 32768, nl: int = 8) -> dict:
     out["reference_signature"] = {
         "calls": "miikv_append_f32 (K RMSNorm + RoPE prologue, fp32 rows, decode state) + "
                  "miikv_decode_attn_q8_1 (fp32 query, gate, gated output, Q8_1 blocks)",
+        "us_median": round(med, 3), "us_p10": round(p10, 3), "us_p90": round(p90, 3),
+        "GBs_median": round(nbytes / (med * 1e-6) / 1e9, 1)}
+
+    def ref_fused(i, s):
+        c = caches[i % nl]
+        assert L.miikv_decode_append_attn_f32(c.view, P(k32.data_ptr()), P(v32.data_ptr()), P(w.data_ptr()),
+                                              ctypes.c_float(1.0e6), ctypes.c_float(1e-6), P(q32.data_ptr()),
+                                              _lib.DTYPE_F32, HQ, ctypes.c_float(1 / math.sqrt(D)), 1, None,
+                                              P(ds.data_ptr()), ctx, None, P(gate.data_ptr()), P(gated.data_ptr()),
+                                              P(q81.data_ptr()), P(ws.buf.data_ptr()), ws.bytes,
+                                              P(s.cuda_stream)) == 0
+    med, p10, p90 = _graph_median(ref_fused, 8 * nl)
+    out["reference_signature_fused"] = {
+        "calls": "miikv_decode_append_attn_f32 (the same arguments in one launch pair)",
         "us_median": round(med, 3), "us_p10": round(p10, 3), "us_p90": round(p90, 3),
         "GBs_median": round(nbytes / (med * 1e-6) / 1e9, 1)}
     del caches

@@ -237,6 +237,23 @@ miikv_status miikv_decode_append_attn(const miikv_view* view, const uint16_t* k_
                                       const float* gate, float* gated_out, void* gated_q8_1, void* workspace,
                                       uint64_t workspace_bytes, void* stream);
 
+/* The reference's decode step in one launch pair with its own store arguments:
+ * k_new / v_new are fp32 rows [batch][kv_heads][head_dim] as the reference store
+ * kernel takes them; with k_norm_weight set, K first gets the reference's prologue
+ * (RMSNorm * weight with epsilon, RoPE on dims 0..63 with theta at the row's
+ * position L-1) before the q8 rule.  Replaces
+ * launch_qwen35_decoupled_k_norm_rope_kv_store_batch_quant followed by
+ * launch_qwen35_tiled_online_attention_quant_dynamic (attention_layer.cpp:599-632;
+ * include/miinfer/qwen3_gpu_primitives.hpp:695-741).  Cache bytes equal
+ * miikv_append_f32 with the same arguments; outputs as miikv_decode_append_attn. */
+miikv_status miikv_decode_append_attn_f32(const miikv_view* view, const float* k_new, const float* v_new,
+                                          const float* k_norm_weight, float theta, float epsilon, const void* q,
+                                          uint32_t q_dtype, uint32_t q_heads, float scale, uint32_t batch,
+                                          const uint32_t* d_lengths, const miikv_decode_state* decode_state,
+                                          uint32_t max_context, float* out, const float* gate, float* gated_out,
+                                          void* gated_q8_1, void* workspace, uint64_t workspace_bytes,
+                                          void* stream);
+
 /* miikv_decode_append_attn without the workspace arguments, for callers that
  * cannot allocate (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc).  No counterpart in the reference.  The split records go

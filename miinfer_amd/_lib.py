@@ -78,6 +78,9 @@ SIGNATURES = {
                                                  _U32, _P, _P, _P, _P, _P, _U64, _P]),
     "miikv_export_canonical": (ctypes.c_int, [_VP, _U32, _U32, _U32, _P, _P, _P, _P, _P]),
     "miikv_import_canonical": (ctypes.c_int, [_VP, _U32, _U32, _U32, _P, _P, _P, _P, _P]),
+    "miikv_decode_append_attn_f32": (ctypes.c_int, [_VP, _P, _P, _P, ctypes.c_float, ctypes.c_float, _P, _U32, _U32,
+                                                     ctypes.c_float, _U32, _P, _P, _U32, _P, _P, _P, _P, _P, _U64,
+                                                     _P]),
     "miikv_decode_scratch_max_bytes": (ctypes.c_uint64, []),
     "miikv_decode_append_attn_noalloc": (ctypes.c_int, [_VP, _P, _P, _P, _U32, _U32, ctypes.c_float, _U32, _P,
                                                          _P, _U32, _P, _P, _P, _P, _P]),

@@ -192,6 +192,67 @@ __device__ bool locate_item(const SplitArgs& a, uint32_t cpw, uint32_t id, uint3
     return true;
 }
 
+// sin and cos of a RoPE angle: the arithmetic of miikv_cache.hip's rope_sincos (and of
+// the CPU oracle), so the fused store rotates keys to the same bits as miikv_append_f32.
+__device__ __forceinline__ void rope_sincos_d(float a, float* s, float* c) {
+#pragma clang fp contract(off)
+    const float k = rintf(a * 6.366197467e-01f);
+    float r = fmaf(-k, 1.5703125f, a);
+    r = fmaf(-k, 4.838267923e-04f, r);
+    r = fmaf(-k, 2.563282919e-12f, r);
+    const float r2 = r * r;
+    float ps = fmaf(r2, -2.505210794e-08f, 2.755731884e-06f);
+    ps = fmaf(r2, ps, -1.984127011e-04f);
+    ps = fmaf(r2, ps, 8.333333768e-03f);
+    ps = fmaf(r2, ps, -1.666666716e-01f);
+    const float sr = fmaf(r * r2, ps, r);
+    float pc = fmaf(r2, 2.087675588e-09f, -2.755731998e-07f);
+    pc = fmaf(r2, pc, 2.480158764e-05f);
+    pc = fmaf(r2, pc, -1.388888923e-03f);
+    pc = fmaf(r2, pc, 4.166666791e-02f);
+    pc = fmaf(r2, pc, -5.000000000e-01f);
+    const float cr = fmaf(r2, pc, 1.0f);
+    const int q = static_cast<int>(k) & 3;
+    *s = q == 0 ? sr : q == 1 ? cr : q == 2 ? -sr : -cr;
+    *c = q == 0 ? cr : q == 1 ? -sr : q == 2 ? -cr : sr;
+}
+
+// The reference's K prologue for one row held one value per thread (thread t < D owns
+// dim t), in its own shape (qwen35_decoupled_k_norm_rope_kv_store_batch_quant_kernel,
+// gfx906/kernels/qwen3_primitives.hip:7257-7281): sum of squares by the LDS tree
+// p[t] += p[t + stride], stride = D/2 .. 1; value * (1 / sqrt(ss / D + eps)) * weight;
+// pairs (t, t + 32), t < 32, rotated by position * step^t.  Same arithmetic as
+// miikv_append_f32's prologue, so the stored codes are the same.  Called by all 256
+// threads (barriers inside).
+template <uint32_t D>
+__device__ void k_prologue(float& kx, float w, uint32_t tid, uint32_t position, float step, float eps) {
+#pragma clang fp contract(off)
+    __shared__ float s_p[256];
+    __shared__ float s_rot[64];
+    s_p[tid] = tid < D ? kx * kx : 0.0f;
+    __syncthreads();
+    for (uint32_t stride = D / 2; stride > 0; stride >>= 1) {
+        if (tid < stride) s_p[tid] += s_p[tid + stride];
+        __syncthreads();
+    }
+    const float r = 1.0f / sqrtf(s_p[0] / static_cast<float>(D) + eps);
+    kx = kx * r * w;
+    if (tid < 64) s_rot[tid] = kx;
+    __syncthreads();
+    if (tid < 32) {
+        float angle = static_cast<float>(position);
+        for (uint32_t i = 0; i < tid; ++i) angle *= step;
+        float sn, cs;
+        rope_sincos_d(angle, &sn, &cs);
+        const float x0 = s_rot[tid], x1 = s_rot[tid + 32];
+        kx = x0 * cs - x1 * sn;
+        s_rot[tid + 32] = x0 * sn + x1 * cs;
+    }
+    __syncthreads();
+    if (tid >= 32 && tid < 64) kx = s_rot[tid];
+    __syncthreads();  // s_p / s_rot are reused by the caller's next use
+}
+
 // Fused append for (sequence b, kv head h), by one 256-thread workgroup: quantise
 // the new fp16 K/V rows with the append rule (thread t < D owns dim t; block absmax
 // over 32 lanes), store them at position L-1, score the K row against the G query
@@ -209,7 +270,10 @@ __device__ void append_record(const SplitArgs& a, uint32_t b, uint32_t h, uint32
     // Threads past D (whole waves: D is a multiple of 64) load dim D-1 and discard it.
     const uint32_t t = min(tid, D - 1);
     const size_t row = (static_cast<size_t>(b) * a.g.kv_heads + h) * D + t;
-    const uint16_t kraw = a.k_new[row], vraw = a.v_new[row];
+    const bool rows32 = a.k_new32 != nullptr;
+    float kx = rows32 ? a.k_new32[row] : f16_bits_to_f32(a.k_new[row]);
+    const float vx = rows32 ? a.v_new32[row] : f16_bits_to_f32(a.v_new[row]);
+    const float kw = a.k_norm_weight != nullptr ? a.k_norm_weight[t] : 0.0f;
     // Wave w scores heads w, w+4, ... with dims lane + 64j; an fp16 query is read as
     // the 32-bit word holding the value (one load form for both query types).
     uint32_t qw[4][DJ];
@@ -223,7 +287,7 @@ __device__ void append_record(const SplitArgs& a, uint32_t b, uint32_t h, uint32
     }
     const uint32_t L = split_length(a, b);
     if (L == 0) return;  // no token (the combine writes zeros)
-    const float kx = f16_bits_to_f32(kraw), vx = f16_bits_to_f32(vraw);
+    if (a.k_norm_weight != nullptr) k_prologue<D>(kx, kw, tid, L - 1, a.rope_step, a.epsilon);
     const float ka = group_reduce<32>(fabsf(kx), MaxOp{});
     const float va = group_reduce<32>(fabsf(vx), MaxOp{});
     const float ksc = ka > 0.0f ? ka / 127.0f : 1.0f, vsc = va > 0.0f ? va / 127.0f : 1.0f;
@@ -897,7 +961,20 @@ void launch_decode(bool f32, bool app, bool kf, bool vf, dim3 grid, size_t lds, 
 }
 }  // namespace
 
-static miikv_status decode_impl(const miikv_view* view, const uint16_t* k_new, const uint16_t* v_new,
+// The new token's rows of a fused append + decode: fp16 rows, or fp32 rows with the
+// reference's K prologue (k_norm_weight set) or without it.
+struct NewRows {
+    const uint16_t* k16 = nullptr;
+    const uint16_t* v16 = nullptr;
+    const float* k32 = nullptr;
+    const float* v32 = nullptr;
+    const float* k_norm_weight = nullptr;
+    float theta = 0.0f;
+    float epsilon = 0.0f;
+    bool any() const { return k16 != nullptr || k32 != nullptr; }
+};
+
+static miikv_status decode_impl(const miikv_view* view, const NewRows& rows,
                                 const void* q, uint32_t q_dtype, uint32_t q_heads, float scale, uint32_t batch,
                                 const uint32_t* d_lengths, const miikv_decode_state* decode_state,
                                 uint32_t max_context, float* out, const float* gate, float* gated_out,
@@ -917,7 +994,9 @@ static miikv_status decode_impl(const miikv_view* view, const uint16_t* k_new, c
     if (max_context == 0 || max_context > view_seq_capacity(view)) return MIIKV_EINVAL;
     if (view->layout == MIIKV_LAYOUT_CONTIGUOUS && batch != 1) return MIIKV_EINVAL;
     // the fused append stores q8 rows
-    if (k_new != nullptr && view->quant_mode != MIIKV_KV_Q8_Q8) return MIIKV_EUNSUPPORTED;
+    if (rows.any() && view->quant_mode != MIIKV_KV_Q8_Q8) return MIIKV_EUNSUPPORTED;
+    if (rows.k_norm_weight != nullptr && (!std::isfinite(rows.theta) || !std::isfinite(rows.epsilon)))
+        return MIIKV_EINVAL;
     const Plan p = make_plan(view, q_heads, batch, max_context);
     if (workspace == nullptr || workspace_bytes < p.counter_bytes + p.part_bytes) return MIIKV_EWORKSPACE;
     if (p.splits > 65535u || batch > 65535u || static_cast<uint64_t>(batch) * view->kv_heads > 0x7fffffffu)
@@ -948,8 +1027,13 @@ static miikv_status decode_impl(const miikv_view* view, const uint16_t* k_new, c
     a.gate = gate;
     a.gated_out = gated_out;
     a.gated_q8_1 = static_cast<uint8_t*>(gated_q8_1);
-    a.k_new = k_new;
-    a.v_new = v_new;
+    a.k_new = rows.k16;
+    a.v_new = rows.v16;
+    a.k_new32 = rows.k32;
+    a.v_new32 = rows.v32;
+    a.k_norm_weight = rows.k_norm_weight;
+    a.rope_step = rows.k_norm_weight != nullptr ? powf(rows.theta, -2.0f / 64.0f) : 0.0f;
+    a.epsilon = rows.epsilon;
     a.q_f32 = q_dtype == MIIKV_DTYPE_F32;
 
     const size_t lds = (32 * kWavesPerWg + kWavesPerWg * G * view->head_dim) * sizeof(float) +
@@ -958,7 +1042,7 @@ static miikv_status decode_impl(const miikv_view* view, const uint16_t* k_new, c
     // One workgroup per possible (sequence, kv head, split) work item, plus one per
     // (sequence, kv head) for the new token of the fused append.
     const uint64_t wgs = static_cast<uint64_t>(p.splits) * view->kv_heads * batch +
-                         (k_new != nullptr ? static_cast<uint64_t>(view->kv_heads) * batch : 0);
+                         (rows.any() ? static_cast<uint64_t>(view->kv_heads) * batch : 0);
     if (wgs > 0x7fffffffu) return MIIKV_EINVAL;
     a.batch = batch;
     a.slots = p.adaptive ? resident_workgroups(view->head_dim, q_dtype == MIIKV_DTYPE_F32 && (view->head_dim == 128 || 2 * G > 16), view->quant_mode) : 0u;
@@ -967,7 +1051,7 @@ static miikv_status decode_impl(const miikv_view* view, const uint16_t* k_new, c
     const bool f32 = q_dtype == MIIKV_DTYPE_F32;
     // combine: one workgroup per (sequence, kv head, 32 output elements)
     const dim3 cgrid(batch * view->kv_heads, G * view->head_dim / 32);
-    const bool app = k_new != nullptr;
+    const bool app = rows.any();
     const bool kf = mode_k_f16(view->quant_mode), vf = mode_v_f16(view->quant_mode);
     if (view->head_dim == 128) {
         launch_decode<128>(f32, app, kf, vf, grid, lds, s, a);
@@ -990,7 +1074,7 @@ extern "C" miikv_status miikv_decode_attn_q8_1(const miikv_view* view, const voi
                                                uint32_t max_context, float* out, const float* gate,
                                                float* gated_out, void* gated_q8_1, void* workspace,
                                                uint64_t workspace_bytes, void* stream) {
-    return decode_impl(view, nullptr, nullptr, q, q_dtype, q_heads, scale, batch, d_lengths, decode_state, max_context,
+    return decode_impl(view, NewRows{}, q, q_dtype, q_heads, scale, batch, d_lengths, decode_state, max_context,
                        out, gate, gated_out, gated_q8_1, workspace, workspace_bytes, stream);
 }
 
@@ -999,7 +1083,7 @@ extern "C" miikv_status miikv_decode_attn(const miikv_view* view, const void* q,
                                           const miikv_decode_state* decode_state, uint32_t max_context, float* out,
                                           const float* gate, float* gated_out, void* workspace,
                                           uint64_t workspace_bytes, void* stream) {
-    return decode_impl(view, nullptr, nullptr, q, q_dtype, q_heads, scale, batch, d_lengths, decode_state, max_context,
+    return decode_impl(view, NewRows{}, q, q_dtype, q_heads, scale, batch, d_lengths, decode_state, max_context,
                        out, gate, gated_out, nullptr, workspace, workspace_bytes, stream);
 }
 
@@ -1011,10 +1095,33 @@ extern "C" miikv_status miikv_decode_append_attn(const miikv_view* view, const u
                                                  float* gated_out, void* gated_q8_1, void* workspace,
                                                  uint64_t workspace_bytes, void* stream) {
     if (k_new == nullptr || v_new == nullptr) return MIIKV_EINVAL;
-    return decode_impl(view, k_new, v_new, q, q_dtype, q_heads, scale, batch, d_lengths, decode_state, max_context,
+    NewRows rows;
+    rows.k16 = k_new;
+    rows.v16 = v_new;
+    return decode_impl(view, rows, q, q_dtype, q_heads, scale, batch, d_lengths, decode_state, max_context,
                        out, gate, gated_out, gated_q8_1, workspace, workspace_bytes, stream);
 }
 
+
+extern "C" miikv_status miikv_decode_append_attn_f32(const miikv_view* view, const float* k_new, const float* v_new,
+                                                     const float* k_norm_weight, float theta, float epsilon,
+                                                     const void* q, uint32_t q_dtype, uint32_t q_heads, float scale,
+                                                     uint32_t batch, const uint32_t* d_lengths,
+                                                     const miikv_decode_state* decode_state, uint32_t max_context,
+                                                     float* out, const float* gate, float* gated_out,
+                                                     void* gated_q8_1, void* workspace, uint64_t workspace_bytes,
+                                                     void* stream) {
+    if (k_new == nullptr || v_new == nullptr) return MIIKV_EINVAL;
+    if (k_norm_weight != nullptr && view != nullptr && view->head_dim < 64) return MIIKV_EINVAL;
+    NewRows rows;
+    rows.k32 = k_new;
+    rows.v32 = v_new;
+    rows.k_norm_weight = k_norm_weight;
+    rows.theta = theta;
+    rows.epsilon = epsilon;
+    return decode_impl(view, rows, q, q_dtype, q_heads, scale, batch, d_lengths, decode_state, max_context, out,
+                       gate, gated_out, gated_q8_1, workspace, workspace_bytes, stream);
+}
 
 // ---- decode without a caller workspace ---------------------------------------
 // The split records live in a file-scope device array instead of a caller
@@ -1064,6 +1171,9 @@ extern "C" miikv_status miikv_decode_append_attn_noalloc(const miikv_view* view,
     void* ptr = nullptr;
     const int st = scratch_for_current_device(&ptr);
     if (st != MIIKV_OK) return st;
-    return decode_impl(view, k_new, v_new, q, q_dtype, q_heads, scale, batch, d_lengths, decode_state, max_context,
+    NewRows rows;
+    rows.k16 = k_new;
+    rows.v16 = v_new;
+    return decode_impl(view, rows, q, q_dtype, q_heads, scale, batch, d_lengths, decode_state, max_context,
                        out, gate, gated_out, gated_q8_1, ptr, kScratchBytes, stream);
 }

@@ -39,6 +39,13 @@ struct SplitArgs {
     uint8_t* gated_q8_1;  // nullable: Q8_1 blocks [batch][q_heads][D/32] of gated_out
     const uint16_t* k_new;  // fused append: fp16 rows [batch][kv_heads][D] stored at position L-1
     const uint16_t* v_new;
+    // fused append of fp32 rows instead (k_new / v_new then null), with the reference's
+    // K prologue when k_norm_weight is set (RMSNorm * weight, RoPE on dims 0..63)
+    const float* k_new32;
+    const float* v_new32;
+    const float* k_norm_weight;
+    float rope_step;        // theta^(-2/64), from the host
+    float epsilon;
     uint32_t q_f32;         // q dtype (scoring the appended token)
 };
 

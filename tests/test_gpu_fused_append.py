@@ -190,3 +190,59 @@ def test_decode_c2_16k_plan(gpu, fused, length):
         assert np.array_equal(got[3][:, -1].view(np.uint16), vs[:, -1])
     expect = oracle.attention_q8(q[0].astype(np.float32), kc, ks, vc, vs, length, hq, 1 / math.sqrt(d))
     assert_attention_close(out.cpu().numpy()[0], expect, f"L={length} fused={fused}")
+
+
+@pytest.mark.parametrize("hq,hk,d,length,theta", [(32, 8, 128, 32768, 1.0e6), (24, 4, 256, 1000, 1.0e7),
+                                                  (24, 4, 256, 1, 1.0e7), (32, 8, 128, 33, 1.0e4)])
+def test_decode_append_attn_f32_reference_step(gpu, hq, hk, d, length, theta):
+    """miikv_decode_append_attn_f32: the reference's store arguments (fp32 rows, K-norm
+    weight, theta, eps) fused into the decode launch pair.  The new row's bytes equal
+    miikv_append_f32 with the same arguments (and so the oracle's prologue + q8 rule), and
+    attention (fp32 query, gate, Q8_1 epilogue) matches the oracle."""
+    import ctypes
+
+    import miinfer_amd as m
+    from miinfer_amd import _lib
+    rng = np.random.default_rng(length + d)
+    cap = max(64, (length + 63) // 64 * 64)
+    fused = m.KvCache.contiguous(hk, d, cap)
+    plain = m.KvCache.contiguous(hk, d, cap)
+    k = randn_f16(rng, (length, hk, d))
+    v = randn_f16(rng, (length, hk, d))
+    for c in (fused, plain):
+        if length > 1:
+            for t0 in range(0, length - 1, 8192):
+                n = min(8192, length - 1 - t0)
+                c.append(_dev(k[t0:t0 + n], gpu), _dev(v[t0:t0 + n], gpu), base_position=t0)
+    k32 = (rng.standard_normal((1, hk, d)) * 3).astype(np.float32)
+    v32 = rng.standard_normal((1, hk, d)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    eps = 1.0e-6
+    plain.append_f32(_dev(k32, gpu), _dev(v32, gpu), base_position=length - 1, k_norm_weight=_dev(w, gpu),
+                     theta=theta, epsilon=eps)
+    q = rng.standard_normal((1, hq, d)).astype(np.float32)
+    gate = rng.standard_normal((1, hq, d)).astype(np.float32)
+    ds = m.make_decode_state(length - 1, device=gpu)
+    ws = m.DecodeWorkspace(fused, hq, 1, cap)
+    out = torch.empty((1, hq, d), device=gpu)
+    gated = torch.empty((1, hq, d), device=gpu)
+    q81 = torch.zeros(hq * d // 32 * 36, dtype=torch.uint8, device=gpu)
+    P = ctypes.c_void_p
+    dk, dv, dw, dq, dg = (_dev(x, gpu) for x in (k32, v32, w, q, gate))
+    st = _lib.lib().miikv_decode_append_attn_f32(
+        fused.view, P(dk.data_ptr()), P(dv.data_ptr()), P(dw.data_ptr()), ctypes.c_float(theta),
+        ctypes.c_float(eps), P(dq.data_ptr()), _lib.DTYPE_F32, hq, ctypes.c_float(1 / math.sqrt(d)), 1, None,
+        P(ds.data_ptr()), cap, P(out.data_ptr()), P(dg.data_ptr()), P(gated.data_ptr()), P(q81.data_ptr()),
+        P(ws.buf.data_ptr()), ws.bytes, P(torch.cuda.current_stream().cuda_stream))
+    assert st == 0, st
+    torch.cuda.synchronize()
+    a, b = _canon(fused, 0, length), _canon(plain, 0, length)
+    for x, y in zip(a, b):
+        assert np.array_equal(x, y)
+    kn = oracle.k_norm_rope(k32[0, :, :].reshape(hk, d)[0], w, length - 1, theta, eps)  # one head spot check
+    kc1, _ = oracle.quantize_rows_f32(kn[None, None])
+    assert np.array_equal(a[0][0, length - 1], kc1[0, 0])
+    kc, ks, vc, vs = b
+    expect = oracle.attention_q8(q[0], kc, ks.view(np.uint16), vc, vs.view(np.uint16), length, hq, 1 / math.sqrt(d))
+    assert_attention_close(out.cpu().numpy()[0], expect, f"L={length}")
+    assert_attention_close(gated.cpu().numpy()[0], expect / (1 + np.exp(-gate[0])), "gated")
