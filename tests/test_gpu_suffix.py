@@ -232,3 +232,35 @@ def test_suffix_blocks_near_the_fp16_maximum(gpu, split):
     assert rel <= 1e-2, rel
     unclamped = oracle.suffix_attention_q8(q.astype(np.float32), kc, ks, vc, vs, prefix, hq, 1 / math.sqrt(d))
     assert np.abs(unclamped - expect).max() > 1.0  # the clamp is visible at this size
+
+
+@pytest.mark.parametrize("split", [True, False])
+def test_suffix_scores_climbing_far_past_the_first_step(gpu, split):
+    """Keys deep in the context whose scores exceed every earlier score by ~100 (log2
+    units) for some rows: the softmax must re-reference those rows (a fixed reference
+    taken from the first keys would overflow fp16 probabilities)."""
+    import miinfer_amd as m
+    rng = np.random.default_rng(91)
+    hq, hk, d, prefix, t = 24, 4, 256, 3000, 40
+    cap = ((prefix + t + 63) // 64) * 64
+    k = randn_f16(rng, (prefix + t, hk, d))
+    v = randn_f16(rng, (prefix + t, hk, d))
+    q = randn_f16(rng, (t, hq, d))
+    # key 1700 of kv head 0 and key 2900 of kv head 3 align with two query rows
+    k[1700, 0] = (q[t - 1, 0].astype(np.float32) * 6).astype(np.float16)
+    k[2900, 3] = (q[5, 20].astype(np.float32) * 6).astype(np.float16)
+    cache = m.KvCache.contiguous(hk, d, cap)
+    cache.append(_dev(k, gpu), _dev(v, gpu))
+    kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+    vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+    out, _ = m.suffix_attention(cache, _dev(q, gpu), prefix, split=split)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    expect = oracle.suffix_attention_q8(q.astype(np.float32), kc, ks, vc, vs, prefix, hq, 1 / math.sqrt(d))
+    assert np.all(np.isfinite(got))
+    # The aligned rows output (nearly) one value row, |x| up to ~4 rather than the
+    # ~0.05 of an average over thousands of rows, so the bound is relative there:
+    # fp16 tiles and fp16 split records each hold ~2^-11 of |x|.
+    err = np.abs(got - expect)
+    assert np.all(err <= 2e-3 + 2e-3 * np.abs(expect)), float((err - 2e-3 * np.abs(expect)).max())
+    assert np.linalg.norm(got - expect) / np.linalg.norm(expect) <= 1e-2
