@@ -284,6 +284,11 @@ miikv_status miikv_decode_append_attn_noalloc(const miikv_view* view, const uint
  *        out * sigmoid(gate).  At least one output is required.
  * If prefill_state is non-NULL, base_position and token_count come from it on
  * the device (token_count is then a host upper bound).
+ * A short suffix (token_count <= 10 for caches of at most 16384 positions, <= 6
+ * above) runs as a batch of decodes over the sequence, each token streaming its
+ * context once; longer ones run on MFMA over fp16 tiles expanded into the
+ * workspace.  miikv_suffix_workspace_bytes() covers both; a smaller workspace
+ * that holds the tiles runs the MFMA path with one split.
  * Replaces launch_qwen35_splitk_suffix_attention_quant
  * (include/miinfer/qwen3_gpu_primitives.hpp:670-693; kernels
  * gfx906/kernels/qwen3_primitives.hip:6789-7207, 6637-6725). */
@@ -299,7 +304,8 @@ miikv_status miikv_suffix_attn(const miikv_view* view, const void* q, uint32_t q
  * (k_new, v_new device [token_count][kv_heads][head_dim]) with the append rule,
  * stores them at positions base_position + t (or the prefill state's), and
  * attends as miikv_suffix_attn, in one pass over the context instead of the
- * reference's store launch followed by attention (attention_layer.cpp:297-343).
+ * reference's store launch followed by attention (attention_layer.cpp:297-343);
+ * a short suffix (see miikv_suffix_attn) is stored first, then attended.
  * Cache bytes and results equal miikv_append_f16 followed by miikv_suffix_attn. */
 miikv_status miikv_suffix_append_attn(const miikv_view* view, const uint16_t* k_new, const uint16_t* v_new,
                                       const void* q, uint32_t q_dtype, uint32_t q_heads, float scale,

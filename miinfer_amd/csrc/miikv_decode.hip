@@ -974,11 +974,22 @@ struct NewRows {
     bool any() const { return k16 != nullptr || k32 != nullptr; }
 };
 
+// Row sets that all read one sequence (a short suffix run as a batch of decodes):
+// row set b has context length (len_ptr ? *len_ptr : 0) + len_add + b, and row sets
+// at or past *count_ptr (when set) are skipped.
+struct RowSets {
+    const uint32_t* len_ptr;
+    uint32_t len_add;
+    const uint32_t* count_ptr;
+    uint32_t seq;
+};
+
 static miikv_status decode_impl(const miikv_view* view, const NewRows& rows,
                                 const void* q, uint32_t q_dtype, uint32_t q_heads, float scale, uint32_t batch,
                                 const uint32_t* d_lengths, const miikv_decode_state* decode_state,
                                 uint32_t max_context, float* out, const float* gate, float* gated_out,
-                                void* gated_q8_1, void* workspace, uint64_t workspace_bytes, void* stream) {
+                                void* gated_q8_1, void* workspace, uint64_t workspace_bytes, void* stream,
+                                const RowSets* rs = nullptr) {
     const int st = validate_view(view);
     if (st != MIIKV_OK) return st;
     if (q == nullptr || batch == 0 || q_heads == 0 || q_heads % view->kv_heads != 0 || !std::isfinite(scale))
@@ -990,9 +1001,9 @@ static miikv_status decode_impl(const miikv_view* view, const NewRows& rows,
         return MIIKV_EINVAL;
     if (gate == nullptr && (gated_out != nullptr || gated_q8_1 != nullptr)) return MIIKV_EINVAL;
     if (gate != nullptr && gated_out == nullptr && gated_q8_1 == nullptr) return MIIKV_EINVAL;
-    if (d_lengths == nullptr && (decode_state == nullptr || batch != 1)) return MIIKV_EINVAL;
+    if (rs == nullptr && d_lengths == nullptr && (decode_state == nullptr || batch != 1)) return MIIKV_EINVAL;
     if (max_context == 0 || max_context > view_seq_capacity(view)) return MIIKV_EINVAL;
-    if (view->layout == MIIKV_LAYOUT_CONTIGUOUS && batch != 1) return MIIKV_EINVAL;
+    if (rs == nullptr && view->layout == MIIKV_LAYOUT_CONTIGUOUS && batch != 1) return MIIKV_EINVAL;
     // the fused append stores q8 rows
     if (rows.any() && view->quant_mode != MIIKV_KV_Q8_Q8) return MIIKV_EUNSUPPORTED;
     if (rows.k_norm_weight != nullptr && (!std::isfinite(rows.theta) || !std::isfinite(rows.epsilon)))
@@ -1008,7 +1019,19 @@ static miikv_status decode_impl(const miikv_view* view, const NewRows& rows,
     a.q_heads = q_heads;
     a.group = G;
     a.scale_log2 = scale * kLog2e;
-    if (d_lengths != nullptr) {
+    a.len_bstep = 0;
+    a.count_ptr = nullptr;
+    if (rs != nullptr) {
+        a.len_ptr = rs->len_ptr;
+        a.len_stride = 0;
+        a.len_add = rs->len_add;
+        a.len_bstep = 1;
+        a.count_ptr = rs->count_ptr;
+        if (view->layout == MIIKV_LAYOUT_PAGED) {  // every row set reads table row seq
+            a.g.table = view->block_table + static_cast<size_t>(rs->seq) * view->table_stride;
+            a.g.table_stride = 0;
+        }
+    } else if (d_lengths != nullptr) {
         a.len_ptr = d_lengths;
         a.len_stride = 1;
         a.len_add = 0;
@@ -1017,8 +1040,6 @@ static miikv_status decode_impl(const miikv_view* view, const NewRows& rows,
         a.len_stride = 0;
         a.len_add = 1;
     }
-    a.len_bstep = 0;
-    a.count_ptr = nullptr;
     a.max_context = max_context;
     a.cpw = p.cpw;
     a.max_splits = p.splits;
@@ -1067,6 +1088,30 @@ static miikv_status decode_impl(const miikv_view* view, const NewRows& rows,
     }
     return hip_status(hipGetLastError());
 }
+
+namespace miikv {
+// Suffix attention of a short suffix as a batch of decodes over one sequence: token t
+// is row set t with context P + t + 1 (the cache already holds the suffix's rows).
+// Each row set streams its context once, so this pays for few tokens only; it
+// serves miikv_suffix_attn below a token-count threshold (miikv_suffix.hip).
+uint64_t suffix_by_decode_bytes(const miikv_view* view, uint32_t q_heads, uint32_t token_count, uint32_t bound) {
+    const Plan p = make_plan(view, q_heads, token_count, bound);
+    return p.counter_bytes + p.part_bytes;
+}
+
+miikv_status suffix_by_decode(const miikv_view* view, const void* q, uint32_t q_dtype, uint32_t q_heads, float scale,
+                              uint32_t token_count, uint32_t base_position, uint32_t seq,
+                              const miikv_prefill_state* prefill_state, uint32_t bound, float* out, const float* gate,
+                              float* gated_out, void* workspace, uint64_t workspace_bytes, void* stream) {
+    RowSets rs;
+    rs.len_ptr = prefill_state ? &prefill_state->base_position : nullptr;
+    rs.len_add = prefill_state ? 1u : base_position + 1u;
+    rs.count_ptr = prefill_state ? &prefill_state->token_count : nullptr;
+    rs.seq = seq;
+    return decode_impl(view, NewRows{}, q, q_dtype, q_heads, scale, token_count, nullptr, nullptr, bound, out, gate,
+                       gated_out, nullptr, workspace, workspace_bytes, stream, &rs);
+}
+}  // namespace miikv
 
 extern "C" miikv_status miikv_decode_attn_q8_1(const miikv_view* view, const void* q, uint32_t q_dtype,
                                                uint32_t q_heads, float scale, uint32_t batch,

@@ -593,6 +593,20 @@ using namespace miikv;
 
 namespace {
 
+// Short suffixes run as a batch of decodes over the one sequence (miikv_decode.hip):
+// each token streams its context once, where the MFMA path expands the context and
+// runs 32-key steps whose cost does not shrink with the token count.  Measured on
+// 24q/4kv/D256 (µs, MFMA path / decodes): context 8192 T=1 39.1/12.5, T=8
+// 40.2/30.5, T=12 41.4/36.7, T=16 42.7/46.7; context 32768 T=1 78.0/21.6, T=6
+// 80.3/54.9, T=8 80.7/77.8.  The threshold follows the cache capacity, so that it
+// is known when the workspace is sized.  MIIKV_SUFFIX_DECODE_MAX_T overrides it.
+bool suffix_runs_as_decode(const miikv_view* v, uint32_t q_heads, uint32_t token_count) {
+    static const char* env = std::getenv("MIIKV_SUFFIX_DECODE_MAX_T");
+    const uint32_t max_t = env ? static_cast<uint32_t>(std::strtoul(env, nullptr, 10))
+                               : (view_seq_capacity(v) <= 16384 ? kSuffixDecodeMaxTShort : kSuffixDecodeMaxT);
+    return token_count <= max_t && q_heads / v->kv_heads <= 16;
+}
+
 struct SuffixPlan {
     uint32_t splits;
     uint32_t split_keys;
@@ -643,7 +657,14 @@ SuffixPlan make_suffix_plan(const miikv_view* v, uint32_t q_heads, uint32_t toke
 extern "C" uint64_t miikv_suffix_workspace_bytes(const miikv_view* view, uint32_t q_heads, uint32_t token_count) {
     if (validate_view(view) != MIIKV_OK || q_heads == 0 || q_heads % view->kv_heads != 0 || token_count == 0)
         return 0;
-    return make_suffix_plan(view, q_heads, token_count, view_seq_capacity(view), true).total();
+    // room for either path: a short suffix runs as decodes when the workspace holds
+    // their records, else on the MFMA path
+    uint64_t dec = 0;
+    if (suffix_runs_as_decode(view, q_heads, token_count)) {
+        const uint64_t cap = std::min<uint64_t>(view_seq_capacity(view), 0xffffffffu);
+        dec = suffix_by_decode_bytes(view, q_heads, token_count, static_cast<uint32_t>(cap));
+    }
+    return std::max(dec, make_suffix_plan(view, q_heads, token_count, view_seq_capacity(view), true).total());
 }
 
 static miikv_status suffix_impl(const miikv_view* view, const uint16_t* k_new, const uint16_t* v_new, const void* q,
@@ -672,6 +693,19 @@ static miikv_status suffix_impl(const miikv_view* view, const uint16_t* k_new, c
     // one holding just the tiles runs a single split.
     const uint64_t bound = prefill_state ? cap : static_cast<uint64_t>(base_position) + token_count;
     if (workspace == nullptr) return MIIKV_EWORKSPACE;
+    const uint32_t bound32 = static_cast<uint32_t>(std::min<uint64_t>(bound, 0xffffffffu));
+    // (a workspace sized for the MFMA path alone runs that path)
+    if (suffix_runs_as_decode(view, q_heads, token_count) &&
+        workspace_bytes >= suffix_by_decode_bytes(view, q_heads, token_count, bound32)) {
+        // the suffix's own rows first; every token then reads its context from the cache
+        if (k_new != nullptr) {
+            const miikv_status ast = miikv_append_f16(view, k_new, v_new, token_count, base_position, seq,
+                                                      prefill_state, nullptr, stream);
+            if (ast != MIIKV_OK) return ast;
+        }
+        return suffix_by_decode(view, q, q_dtype, q_heads, scale, token_count, base_position, seq, prefill_state,
+                                bound32, out, gate, gated_out, workspace, workspace_bytes, stream);
+    }
     SuffixPlan plan = make_suffix_plan(view, q_heads, token_count, bound, true);
     if (workspace_bytes < plan.total()) {
         plan = make_suffix_plan(view, q_heads, token_count, bound, false);

@@ -17,6 +17,15 @@ constexpr float kSlackS = 6.0f;        // lazy-rescale threshold (log2 units): p
 // (two per SIMD at <= 256 VGPRs) and its LDS tile buffers (4 x 32 KiB at D = 256).
 constexpr uint32_t kSufSlots = 256 * (8 / kSufWaves);
 constexpr uint32_t kSufMaxSplits = 64;
+// Suffixes of at most this many tokens run as a batch of decodes (miikv_decode.hip):
+// caches of more than 16384 positions, and of at most that many.
+constexpr uint32_t kSuffixDecodeMaxT = 6;
+constexpr uint32_t kSuffixDecodeMaxTShort = 10;
+uint64_t suffix_by_decode_bytes(const miikv_view* view, uint32_t q_heads, uint32_t token_count, uint32_t bound);
+miikv_status suffix_by_decode(const miikv_view* view, const void* q, uint32_t q_dtype, uint32_t q_heads, float scale,
+                              uint32_t token_count, uint32_t base_position, uint32_t seq,
+                              const miikv_prefill_state* prefill_state, uint32_t bound, float* out, const float* gate,
+                              float* gated_out, void* workspace, uint64_t workspace_bytes, void* stream);
 
 // fp16 halves of one expanded step: K fragments [D/16][64 lanes][8], then
 // V fragments [D/32][2 key halves][64 lanes][8].

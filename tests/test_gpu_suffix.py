@@ -70,12 +70,14 @@ def test_suffix_config4_full_size_sampled_tokens(gpu, split):
         assert_attention_close(out[tok], expect, f"token {tok}")
 
 
+# (t, extra): 100 tokens run on the MFMA path, 3 as a batch of decodes
+@pytest.mark.parametrize("t,extra", [(100, 20), (3, 2)])
 @pytest.mark.parametrize("split", [True, False])
-def test_suffix_prefill_state_and_paged(gpu, split):
+def test_suffix_prefill_state_and_paged(gpu, split, t, extra):
     import miinfer_amd as m
     rng = np.random.default_rng(8)
     hq, hk, d, pt = 24, 4, 256, 256
-    prefix, t = 700, 100
+    prefix = 700
     npages = (prefix + t + pt - 1) // pt
     table = _dev(rng.permutation(npages + 2)[:npages].astype(np.int32).reshape(1, npages), gpu)
     cache = m.KvCache.paged_cache(hk, d, npages + 2, table, page_tokens=pt)
@@ -84,9 +86,9 @@ def test_suffix_prefill_state_and_paged(gpu, split):
     cache.append(_dev(k, gpu), _dev(v, gpu), base_position=0)
     kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
     vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
-    q = randn_f16(rng, (t + 20, hq, d))  # host bound 120 rows, device says 100
+    q = randn_f16(rng, (t + extra, hq, d))  # host bound t + extra rows, device says t
     ps = m.make_prefill_state(prefix, t, device=gpu)
-    out = torch.full((t + 20, hq, d), 5.0, device=gpu)
+    out = torch.full((t + extra, hq, d), 5.0, device=gpu)
     m.suffix_attention(cache, _dev(q, gpu), 0, prefill_state=ps, out=out, split=split)
     torch.cuda.synchronize()
     got = out.cpu().numpy()
@@ -164,35 +166,37 @@ def test_suffix_fused_append_matches_append_then_attend(gpu, hq, hk, d, prefix, 
     assert_attention_close(a.cpu().numpy(), expect, "fused suffix")
 
 
-def test_suffix_fused_append_paged_prefill_state(gpu):
+@pytest.mark.parametrize("t,extra", [(100, 20), (4, 3)])
+def test_suffix_fused_append_paged_prefill_state(gpu, t, extra):
     """Paged cache, positions from a device prefill state (host bound larger than the
-    device token count): rows past the device count are neither stored nor attended."""
+    device token count): rows past the device count are neither stored nor attended.
+    4 + 3 tokens run as a batch of decodes after a plain append."""
     import miinfer_amd as m
     rng = np.random.default_rng(21)
     hq, hk, d, pt = 24, 4, 256, 256
-    prefix, t = 700, 100
-    npages = (prefix + t + 20 + pt - 1) // pt
+    prefix = 700
+    npages = (prefix + t + extra + pt - 1) // pt
     table = _dev(rng.permutation(npages + 2)[:npages].astype(np.int32).reshape(1, npages), gpu)
-    k = randn_f16(rng, (prefix + t + 20, hk, d))
-    v = randn_f16(rng, (prefix + t + 20, hk, d))
+    k = randn_f16(rng, (prefix + t + extra, hk, d))
+    v = randn_f16(rng, (prefix + t + extra, hk, d))
     fused = m.KvCache.paged_cache(hk, d, npages + 2, table, page_tokens=pt)
     plain = m.KvCache.paged_cache(hk, d, npages + 2, table, page_tokens=pt)
     for c in (fused, plain):
         c.append(_dev(k[:prefix], gpu), _dev(v[:prefix], gpu), base_position=0)
     plain.append(_dev(k[prefix:prefix + t], gpu), _dev(v[prefix:prefix + t], gpu), base_position=prefix)
-    before = _canon_all(fused, 0, prefix + t + 20)
-    q = _dev(randn_f16(rng, (t + 20, hq, d)), gpu)
+    before = _canon_all(fused, 0, prefix + t + extra)
+    q = _dev(randn_f16(rng, (t + extra, hq, d)), gpu)
     ps = m.make_prefill_state(prefix, t, device=gpu)
-    a = torch.full((t + 20, hq, d), 5.0, device=gpu)
-    b = torch.full((t + 20, hq, d), 5.0, device=gpu)
+    a = torch.full((t + extra, hq, d), 5.0, device=gpu)
+    b = torch.full((t + extra, hq, d), 5.0, device=gpu)
     m.suffix_attention(fused, q, 0, prefill_state=ps, out=a, k_new=_dev(k[prefix:], gpu),
                        v_new=_dev(v[prefix:], gpu))
     m.suffix_attention(plain, q, 0, prefill_state=ps, out=b)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
     assert bool((a[t:] == 5.0).all())
-    after = _canon_all(fused, 0, prefix + t + 20)
-    for x, y, z in zip(after, _canon_all(plain, 0, prefix + t + 20), before):
+    after = _canon_all(fused, 0, prefix + t + extra)
+    for x, y, z in zip(after, _canon_all(plain, 0, prefix + t + extra), before):
         assert np.array_equal(x[:, :prefix + t], y[:, :prefix + t])
         assert np.array_equal(x[:, prefix + t:], z[:, prefix + t:])  # past the device count: untouched
 
@@ -264,3 +268,34 @@ def test_suffix_scores_climbing_far_past_the_first_step(gpu, split):
     err = np.abs(got - expect)
     assert np.all(err <= 2e-3 + 2e-3 * np.abs(expect)), float((err - 2e-3 * np.abs(expect)).max())
     assert np.linalg.norm(got - expect) / np.linalg.norm(expect) <= 1e-2
+
+
+
+@pytest.mark.parametrize("t", [1, 5, 9])
+def test_suffix_short_on_a_second_sequence(gpu, t):
+    """Short suffixes run as a batch of decodes: token t reads sequence `seq`'s block
+    table row with context P + t + 1.  Two sequences share the page pool; the suffix
+    of sequence 1 must read its own pages only."""
+    import miinfer_amd as m
+    rng = np.random.default_rng(31 + t)
+    hq, hk, d, pt = 24, 4, 256, 256
+    prefix = 1500
+    per = (prefix + t + pt - 1) // pt
+    perm = rng.permutation(2 * per + 3)[:2 * per].astype(np.int32)
+    table = _dev(perm.reshape(2, per), gpu)
+    cache = m.KvCache.paged_cache(hk, d, 2 * per + 3, table, page_tokens=pt)
+    other = randn_f16(rng, (prefix + t, hk, d))
+    cache.append(_dev(other, gpu), _dev(other, gpu), base_position=0, seq=0)
+    k = randn_f16(rng, (prefix + t, hk, d))
+    v = randn_f16(rng, (prefix + t, hk, d))
+    cache.append(_dev(k, gpu), _dev(v, gpu), base_position=0, seq=1)
+    kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+    vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+    q = randn_f16(rng, (t, hq, d))
+    gate = rng.standard_normal((t, hq, d)).astype(np.float32)
+    out, gated = m.suffix_attention(cache, _dev(q, gpu), prefix, seq=1, gate=_dev(gate, gpu),
+                                    out=torch.empty((t, hq, d), device=gpu))
+    torch.cuda.synchronize()
+    expect = oracle.suffix_attention_q8(q.astype(np.float32), kc, ks, vc, vs, prefix, hq, 1 / math.sqrt(d))
+    assert_attention_close(out.cpu().numpy(), expect, "seq 1")
+    assert_attention_close(gated.cpu().numpy(), expect / (1 + np.exp(-gate)), "seq 1 gated")
