@@ -3,6 +3,7 @@
 // fingerprint / match logic of ReusableContext.  Pure C++ (no device calls);
 // the device work these plans describe runs through miikv_copy_pages,
 // miikv_copy_segments and miikv_clone_state.
+#include <algorithm>
 #include <cstdint>
 #include <cstring>
 #include <new>
@@ -114,16 +115,31 @@ extern "C" miikv_status miikv_pool_fork_n(miikv_pool* p, const int32_t* parent_r
         return MIIKV_EINVAL;
     *n_copies = 0;
     *n_done = 0;
-    for (uint32_t i = 0; i < n; ++i) {
-        uint32_t c = 0;
-        const miikv_status st =
-            miikv_pool_fork(p, parent_row, row_stride, length, page_tokens, child_rows + static_cast<size_t>(i) * row_stride,
-                            copy_src ? copy_src + *n_copies : nullptr, copy_dst ? copy_dst + *n_copies : nullptr, &c);
-        if (st != MIIKV_OK) return st;
-        *n_copies += c;
-        *n_done = i + 1;
+    if (n == 0) return MIIKV_OK;
+    const uint32_t np = pages_for(length, page_tokens);
+    if (np > 0 && parent_row == nullptr) return MIIKV_EINVAL;
+    for (uint32_t i = 0; i < np; ++i)
+        if (!valid_page(p, parent_row[i]) || p->refs[static_cast<size_t>(parent_row[i])] == 0) return MIIKV_EINVAL;
+    const bool partial = (length % page_tokens) != 0;
+    if (partial && (copy_src == nullptr || copy_dst == nullptr)) return MIIKV_EINVAL;
+    // The forks that fit: each partial fork takes one fresh page.
+    const uint32_t k = partial ? static_cast<uint32_t>(std::min<size_t>(n, p->free_list.size())) : n;
+    // The full pages are shared by every child: one reference-count pass for all k.
+    const uint32_t shared = partial ? np - 1 : np;
+    for (uint32_t i = 0; i < shared; ++i) p->refs[static_cast<size_t>(parent_row[i])] += k;
+    for (uint32_t c = 0; c < k; ++c) {
+        int32_t* row = child_rows + static_cast<size_t>(c) * row_stride;
+        if (shared > 0) std::memcpy(row, parent_row, shared * sizeof(int32_t));
+        if (partial) {
+            const int32_t fresh = miikv_pool_alloc(p);  // cannot fail: k <= free pages
+            row[np - 1] = fresh;
+            copy_src[c] = parent_row[np - 1];
+            copy_dst[c] = fresh;
+        }
     }
-    return MIIKV_OK;
+    *n_copies = partial ? k : 0;
+    *n_done = k;
+    return k == n ? MIIKV_OK : MIIKV_EINVAL;
 }
 
 extern "C" miikv_status miikv_pool_prepare_append(miikv_pool* p, int32_t* row, uint32_t row_capacity,

@@ -41,7 +41,7 @@ class PagePool:
 
     def __del__(self):
         h = getattr(self, "_h", None)
-        if h:
+        if h and lib is not None:  # module globals may already be gone at interpreter exit
             lib().miikv_pool_destroy(h)
             self._h = None
 

@@ -148,6 +148,37 @@ def test_fork_many_matches_repeated_fork():
     assert [a.refcount(p) for p in range(40)] == [b.refcount(p) for p in range(40)]
     with pytest.raises(MemoryError):
         PagePool(5).fork_many(np.array([0, 1, 2, 3], np.int32), length, pt, 3)
+    # whole pages only: no copies, every page shared n + 1 ways
+    c = PagePool(8)
+    rc = np.array([c.alloc() for _ in range(3)], np.int32)
+    rows, copies = c.fork_many(rc, 3 * pt, pt, 6)
+    assert copies == [] and np.array_equal(rows, np.tile(rc, (6, 1)))
+    assert [c.refcount(int(p)) for p in rc] == [7, 7, 7] and c.free_pages == 5
+
+
+def test_fork_many_exhaustion_keeps_the_completed_forks():
+    """Partial-page forks need one fresh page each: with 2 free pages, 2 of 5 forks
+    complete (rows, copies, reference counts as 2 single forks) and the call fails."""
+    from miinfer_amd.reuse import PagePool
+    from miinfer_amd import lib
+    import ctypes
+    pt, length = 256, 256 * 2 + 7
+    a, b = PagePool(5), PagePool(5)
+    ra = np.array([a.alloc() for _ in range(3)], np.int32)
+    rb = np.array([b.alloc() for _ in range(3)], np.int32)
+    rows = np.full((5, 3), -1, np.int32)
+    src, dst = np.zeros(5, np.int32), np.zeros(5, np.int32)
+    nc, done = ctypes.c_uint32(0), ctypes.c_uint32(0)
+    p32 = lambda x: x.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+    st = lib().miikv_pool_fork_n(a._h, p32(ra), length, pt, 5, p32(rows), 3, p32(src), p32(dst),
+                                 ctypes.byref(nc), ctypes.byref(done))
+    assert st != 0 and done.value == 2 and nc.value == 2
+    single = [b.fork(rb, length, pt) for _ in range(2)]
+    assert np.array_equal(rows[:2], np.stack([r for r, _ in single]))
+    assert list(zip(src[:2].tolist(), dst[:2].tolist())) == [c for _, cs in single for c in cs]
+    assert np.all(rows[2:] == -1)
+    assert [a.refcount(p) for p in range(5)] == [b.refcount(p) for p in range(5)]
+    assert a.free_pages == b.free_pages == 0
 
 
 def test_pool_fork_rejects_short_rows():
