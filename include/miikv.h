@@ -284,10 +284,10 @@ miikv_status miikv_decode_append_attn_noalloc(const miikv_view* view, const uint
  *        out * sigmoid(gate).  At least one output is required.
  * If prefill_state is non-NULL, base_position and token_count come from it on
  * the device (token_count is then a host upper bound).
- * A short suffix (token_count <= 10 for caches of at most 16384 positions, <= 6
- * above) runs as a batch of decodes over the sequence, each token streaming its
- * context once; longer ones run on MFMA over fp16 tiles expanded into the
- * workspace.  miikv_suffix_workspace_bytes() covers both; a smaller workspace
+ * A short suffix runs as a batch of decodes over the sequence (up to 16 / (q_heads
+ * / kv_heads) tokens share one pass over the context; at most 12 such passes for
+ * caches of at most 16384 positions, 6 above); longer ones run on MFMA over fp16
+ * tiles expanded into the workspace.  miikv_suffix_workspace_bytes() covers both; a smaller workspace
  * that holds the tiles runs the MFMA path with one split.
  * Replaces launch_qwen35_splitk_suffix_attention_quant
  * (include/miinfer/qwen3_gpu_primitives.hpp:670-693; kernels

@@ -498,7 +498,11 @@ decode_kernel(SplitArgs a) {
     float4 q32raw[QF32 ? NB : 1][2];
     {
         const uint32_t qh = QPAIR && n >= G ? min(n - G, G - 1) : min(n, G - 1);
-        const size_t qrow = (static_cast<size_t>(b) * a.q_heads + static_cast<size_t>(h) * G + qh) * D;
+        // packed tokens (a short suffix): column qh is token pack*b + qh / Gt, head qh % Gt
+        const uint32_t Gt = a.pack == 1 ? G : G / a.pack;
+        const uint32_t tp = a.pack == 1 ? 0u : qh / Gt;
+        const size_t qrow = ((static_cast<size_t>(b) * a.pack + tp) * a.q_heads + static_cast<size_t>(h) * Gt +
+                             (qh - tp * Gt)) * D;
 #pragma unroll
         for (uint32_t blk = 0; blk < NB; ++blk) {
             if constexpr (QF32) {
@@ -579,6 +583,10 @@ decode_kernel(SplitArgs a) {
     // by append_record: masked) has its own record.
     const uint32_t Lc = APPEND ? L - 1 : L;
     const uint32_t nsteps = (Lc + kChunk - 1) / kChunk;
+    // Packed tokens: column n's context is shorter by the packed tokens after its own
+    // (Lc_col); steps past Lc_lo, the shortest, mask per column.
+    const uint32_t Lc_lo = Lc - (a.pack - 1);
+    const uint32_t Lc_col = a.pack == 1 ? Lc : Lc - (a.pack - 1 - min(n, G - 1) / (G / a.pack));
 #ifdef MIIKV_EXP_NO_LOOP
     const uint32_t n_steps = 0;
 #else
@@ -608,7 +616,7 @@ decode_kernel(SplitArgs a) {
             return;
         }
 #endif
-        const bool tail = tok0 + kChunk > Lc;
+        const bool tail = tok0 + kChunk > Lc_lo;
         if constexpr (!KF16) *reinterpret_cast<ScaleVec*>(s_sc + lane * (NB / 2)) = st.ks;
         if constexpr (!VF16) {
             ScaleVec vsv = st.vs;
@@ -689,7 +697,7 @@ decode_kernel(SplitArgs a) {
             for (uint32_t J = 0; J < 2; ++J)
 #pragma unroll
                 for (uint32_t i = 0; i < 4; ++i)
-                    if (tok0 + 16 * J + 4 * g4 + i >= Lc) s[J][i] = -INFINITY;
+                    if (tok0 + 16 * J + 4 * g4 + i >= Lc_col) s[J][i] = -INFINITY;
         }
 
         // ---- online softmax with a lazy running max: the accumulators are rescaled only
@@ -715,11 +723,13 @@ decode_kernel(SplitArgs a) {
             }
         }
         float psum = 0.0f;
+        // a packed column may have no key yet (m_run = -inf): its p stay 0
+        const float m_use = m_run == -INFINITY ? 0.0f : m_run;
 #pragma unroll
         for (uint32_t J = 0; J < 2; ++J)
 #pragma unroll
             for (uint32_t i = 0; i < 4; ++i) {
-                s[J][i] = fast_exp2(s[J][i] - m_run);
+                s[J][i] = fast_exp2(s[J][i] - m_use);
                 psum += s[J][i];
             }
         l_run += psum;
@@ -982,6 +992,7 @@ struct RowSets {
     uint32_t len_add;
     const uint32_t* count_ptr;
     uint32_t seq;
+    uint32_t pack;  // tokens per row set (divides batch; no count_ptr when > 1)
 };
 
 static miikv_status decode_impl(const miikv_view* view, const NewRows& rows,
@@ -994,7 +1005,11 @@ static miikv_status decode_impl(const miikv_view* view, const NewRows& rows,
     if (st != MIIKV_OK) return st;
     if (q == nullptr || batch == 0 || q_heads == 0 || q_heads % view->kv_heads != 0 || !std::isfinite(scale))
         return MIIKV_EINVAL;
-    const uint32_t G = q_heads / view->kv_heads;
+    // packed tokens: batch / pack row sets of pack * G columns
+    const uint32_t pack = rs != nullptr ? rs->pack : 1u;
+    if (pack == 0 || batch % pack != 0 || (pack > 1 && rs->count_ptr != nullptr)) return MIIKV_EINVAL;
+    batch /= pack;
+    const uint32_t G = q_heads / view->kv_heads * pack;
     if (G > 16) return MIIKV_EUNSUPPORTED;
     if (q_dtype != MIIKV_DTYPE_F16 && q_dtype != MIIKV_DTYPE_F32) return MIIKV_EINVAL;
     if (out == nullptr && !(gate != nullptr && (gated_out != nullptr || gated_q8_1 != nullptr)))
@@ -1008,7 +1023,7 @@ static miikv_status decode_impl(const miikv_view* view, const NewRows& rows,
     if (rows.any() && view->quant_mode != MIIKV_KV_Q8_Q8) return MIIKV_EUNSUPPORTED;
     if (rows.k_norm_weight != nullptr && (!std::isfinite(rows.theta) || !std::isfinite(rows.epsilon)))
         return MIIKV_EINVAL;
-    const Plan p = make_plan(view, q_heads, batch, max_context);
+    const Plan p = make_plan(view, q_heads * pack, batch, max_context);
     if (workspace == nullptr || workspace_bytes < p.counter_bytes + p.part_bytes) return MIIKV_EWORKSPACE;
     if (p.splits > 65535u || batch > 65535u || static_cast<uint64_t>(batch) * view->kv_heads > 0x7fffffffu)
         return MIIKV_EINVAL;
@@ -1018,14 +1033,15 @@ static miikv_status decode_impl(const miikv_view* view, const NewRows& rows,
     a.q = q;
     a.q_heads = q_heads;
     a.group = G;
+    a.pack = pack;
     a.scale_log2 = scale * kLog2e;
     a.len_bstep = 0;
     a.count_ptr = nullptr;
-    if (rs != nullptr) {
+    if (rs != nullptr) {  // row set b: len_add + b * pack (its last token's context)
         a.len_ptr = rs->len_ptr;
         a.len_stride = 0;
-        a.len_add = rs->len_add;
-        a.len_bstep = 1;
+        a.len_add = rs->len_add + (pack - 1);
+        a.len_bstep = pack;
         a.count_ptr = rs->count_ptr;
         if (view->layout == MIIKV_LAYOUT_PAGED) {  // every row set reads table row seq
             a.g.table = view->block_table + static_cast<size_t>(rs->seq) * view->table_stride;
@@ -1094,9 +1110,22 @@ namespace miikv {
 // is row set t with context P + t + 1 (the cache already holds the suffix's rows).
 // Each row set streams its context once, so this pays for few tokens only; it
 // serves miikv_suffix_attn below a token-count threshold (miikv_suffix.hip).
+// Tokens per row set: the largest divisor of token_count whose columns (tokens x
+// query heads per kv head) fit the 16 of the MFMA; with a device token count, 1.
+uint32_t suffix_pack(const miikv_view* view, uint32_t q_heads, uint32_t token_count, bool device_count) {
+    const uint32_t G = q_heads / view->kv_heads;
+    if (device_count || G == 0 || G > 16) return 1;
+    for (uint32_t p = std::min<uint32_t>(16 / G, token_count); p > 1; --p)
+        if (token_count % p == 0) return p;
+    return 1;
+}
+
 uint64_t suffix_by_decode_bytes(const miikv_view* view, uint32_t q_heads, uint32_t token_count, uint32_t bound) {
-    const Plan p = make_plan(view, q_heads, token_count, bound);
-    return p.counter_bytes + p.part_bytes;
+    // the larger of the packed (host token count) and unpacked (device count) plans
+    const uint32_t pk = suffix_pack(view, q_heads, token_count, false);
+    const Plan p1 = make_plan(view, q_heads, token_count, bound);
+    const Plan pp = make_plan(view, q_heads * pk, token_count / pk, bound);
+    return std::max(p1.counter_bytes + p1.part_bytes, pp.counter_bytes + pp.part_bytes);
 }
 
 miikv_status suffix_by_decode(const miikv_view* view, const void* q, uint32_t q_dtype, uint32_t q_heads, float scale,
@@ -1108,6 +1137,8 @@ miikv_status suffix_by_decode(const miikv_view* view, const void* q, uint32_t q_
     rs.len_add = prefill_state ? 1u : base_position + 1u;
     rs.count_ptr = prefill_state ? &prefill_state->token_count : nullptr;
     rs.seq = seq;
+    static const bool no_pack = std::getenv("MIIKV_SUFFIX_NO_PACK") != nullptr;  // measurement
+    rs.pack = no_pack ? 1u : suffix_pack(view, q_heads, token_count, prefill_state != nullptr);
     return decode_impl(view, NewRows{}, q, q_dtype, q_heads, scale, token_count, nullptr, nullptr, bound, out, gate,
                        gated_out, nullptr, workspace, workspace_bytes, stream, &rs);
 }

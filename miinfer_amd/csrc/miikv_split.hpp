@@ -15,7 +15,12 @@ struct SplitArgs {
     Geo g;
     const void* q;
     uint32_t q_heads;
-    uint32_t group;  // query heads per kv head (<= 16)
+    uint32_t group;  // columns per (row set, kv head), <= 16: pack tokens x query heads per kv head
+    // Tokens per row set (1: decode).  A short suffix packs `pack` consecutive tokens of
+    // one sequence into a row set: column c is token pack*b + c / (group / pack), query
+    // head h * (group / pack) + c % (group / pack), with context split_length() - (pack -
+    // 1 - c / (group / pack)).
+    uint32_t pack;
     float scale_log2;
     // Context length of row-set b: (len_ptr ? len_ptr[b * len_stride] : 0) + len_add
     // + b * len_bstep (decode: per-sequence lengths; suffix: base + t + 1).
@@ -135,7 +140,11 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
     const uint32_t q = tid & 7, rg = tid >> 3;
     const uint32_t e = blockIdx.y * 32 + 4 * q;  // < GD: the grid covers GD / 32 blocks
     const uint32_t hn = (blockIdx.y * 32) / D;
-    const size_t out_row0 = (static_cast<size_t>(b) * a.q_heads + static_cast<size_t>(h) * G) * D;
+    // output row of column hn (packed tokens: token pack*b + hn / Gt, head h*Gt + hn % Gt),
+    // indexed below with the column's offset e - hn * D folded back in
+    const uint32_t Gt = G / a.pack, tp = hn / Gt;
+    const size_t out_row0 = ((static_cast<size_t>(b) * a.pack + tp) * a.q_heads + static_cast<size_t>(h) * Gt +
+                             (hn - tp * Gt)) * D - static_cast<size_t>(hn) * D;
     const uint32_t rec = record_floats(G, D);
     const uint32_t slots = a.max_splits + 1;
     const float* part = a.part + (static_cast<size_t>(bh) * slots) * rec;

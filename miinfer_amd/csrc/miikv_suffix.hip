@@ -594,17 +594,24 @@ using namespace miikv;
 namespace {
 
 // Short suffixes run as a batch of decodes over the one sequence (miikv_decode.hip):
-// each token streams its context once, where the MFMA path expands the context and
-// runs 32-key steps whose cost does not shrink with the token count.  Measured on
-// 24q/4kv/D256 (µs, MFMA path / decodes): context 8192 T=1 39.1/12.5, T=8
-// 40.2/30.5, T=12 41.4/36.7, T=16 42.7/46.7; context 32768 T=1 78.0/21.6, T=6
-// 80.3/54.9, T=8 80.7/77.8.  The threshold follows the cache capacity, so that it
-// is known when the workspace is sized.  MIIKV_SUFFIX_DECODE_MAX_T overrides it.
-bool suffix_runs_as_decode(const miikv_view* v, uint32_t q_heads, uint32_t token_count) {
+// each decode row set streams the context once for the tokens packed into it (as many
+// as fit the MFMA's 16 columns with their query heads), where the MFMA path expands
+// the context and runs 32-key steps whose cost barely depends on the token count.
+// Measured (graph replays, µs, MFMA path / decodes), 24q/4kv/D256 (2 tokens per row
+// set): context 8192 T=1 39.1/12.6, T=4 40.4/21.3, T=8 40.4/25.6, T=16 42.8/36.1;
+// context 32768 T=1 78.0/21.8, T=4 79.7/34.1, T=8 80.9/54.8, T=12 82.9/60.1, T=16
+// 84.9/82.1.  32q/8kv/D128 (4 per row set): context 32768 T=4 76.0/21.5, T=8
+// 76.3/34.2, T=16 76.8/47.0.  Without packing (a device token count), 24q/4kv/D256:
+// context 8192 T=12 41.4/36.7, T=16 42.7/46.7; context 32768 T=6 80.3/54.9, T=8
+// 80.7/77.8.  So: at most 6 row sets above a 16384-position capacity, 12 at or
+// below it.  MIIKV_SUFFIX_DECODE_MAX_T (a token count) overrides the rule.
+bool suffix_runs_as_decode(const miikv_view* v, uint32_t q_heads, uint32_t token_count, bool device_count) {
+    if (q_heads / v->kv_heads > 16) return false;
     static const char* env = std::getenv("MIIKV_SUFFIX_DECODE_MAX_T");
-    const uint32_t max_t = env ? static_cast<uint32_t>(std::strtoul(env, nullptr, 10))
-                               : (view_seq_capacity(v) <= 16384 ? kSuffixDecodeMaxTShort : kSuffixDecodeMaxT);
-    return token_count <= max_t && q_heads / v->kv_heads <= 16;
+    if (env) return token_count <= static_cast<uint32_t>(std::strtoul(env, nullptr, 10));
+    if (token_count > kSuffixDecodeMaxT) return false;
+    const uint32_t rows = token_count / suffix_pack(v, q_heads, token_count, device_count);
+    return rows <= (view_seq_capacity(v) <= 16384 ? kSuffixDecodeMaxRowsShort : kSuffixDecodeMaxRows);
 }
 
 struct SuffixPlan {
@@ -660,7 +667,8 @@ extern "C" uint64_t miikv_suffix_workspace_bytes(const miikv_view* view, uint32_
     // room for either path: a short suffix runs as decodes when the workspace holds
     // their records, else on the MFMA path
     uint64_t dec = 0;
-    if (suffix_runs_as_decode(view, q_heads, token_count)) {
+    if (suffix_runs_as_decode(view, q_heads, token_count, false) ||
+        suffix_runs_as_decode(view, q_heads, token_count, true)) {
         const uint64_t cap = std::min<uint64_t>(view_seq_capacity(view), 0xffffffffu);
         dec = suffix_by_decode_bytes(view, q_heads, token_count, static_cast<uint32_t>(cap));
     }
@@ -695,7 +703,7 @@ static miikv_status suffix_impl(const miikv_view* view, const uint16_t* k_new, c
     if (workspace == nullptr) return MIIKV_EWORKSPACE;
     const uint32_t bound32 = static_cast<uint32_t>(std::min<uint64_t>(bound, 0xffffffffu));
     // (a workspace sized for the MFMA path alone runs that path)
-    if (suffix_runs_as_decode(view, q_heads, token_count) &&
+    if (suffix_runs_as_decode(view, q_heads, token_count, prefill_state != nullptr) &&
         workspace_bytes >= suffix_by_decode_bytes(view, q_heads, token_count, bound32)) {
         // the suffix's own rows first; every token then reads its context from the cache
         if (k_new != nullptr) {

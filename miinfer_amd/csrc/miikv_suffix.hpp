@@ -17,10 +17,13 @@ constexpr float kSlackS = 6.0f;        // lazy-rescale threshold (log2 units): p
 // (two per SIMD at <= 256 VGPRs) and its LDS tile buffers (4 x 32 KiB at D = 256).
 constexpr uint32_t kSufSlots = 256 * (8 / kSufWaves);
 constexpr uint32_t kSufMaxSplits = 64;
-// Suffixes of at most this many tokens run as a batch of decodes (miikv_decode.hip):
-// caches of more than 16384 positions, and of at most that many.
-constexpr uint32_t kSuffixDecodeMaxT = 6;
-constexpr uint32_t kSuffixDecodeMaxTShort = 10;
+// Suffixes of at most this many decode row sets (tokens / tokens packed per row set)
+// run as a batch of decodes (miikv_decode.hip): caches of more than 16384 positions,
+// and of at most that many.
+constexpr uint32_t kSuffixDecodeMaxRows = 6;
+constexpr uint32_t kSuffixDecodeMaxRowsShort = 12;
+constexpr uint32_t kSuffixDecodeMaxT = 64;
+uint32_t suffix_pack(const miikv_view* view, uint32_t q_heads, uint32_t token_count, bool device_count);
 uint64_t suffix_by_decode_bytes(const miikv_view* view, uint32_t q_heads, uint32_t token_count, uint32_t bound);
 miikv_status suffix_by_decode(const miikv_view* view, const void* q, uint32_t q_dtype, uint32_t q_heads, float scale,
                               uint32_t token_count, uint32_t base_position, uint32_t seq,

@@ -238,21 +238,22 @@ def test_suffix_blocks_near_the_fp16_maximum(gpu, split):
     assert np.abs(unclamped - expect).max() > 1.0  # the clamp is visible at this size
 
 
+@pytest.mark.parametrize("t", [40, 4])  # the MFMA path; packed decodes
 @pytest.mark.parametrize("split", [True, False])
-def test_suffix_scores_climbing_far_past_the_first_step(gpu, split):
+def test_suffix_scores_climbing_far_past_the_first_step(gpu, split, t):
     """Keys deep in the context whose scores exceed every earlier score by ~100 (log2
     units) for some rows: the softmax must re-reference those rows (a fixed reference
     taken from the first keys would overflow fp16 probabilities)."""
     import miinfer_amd as m
     rng = np.random.default_rng(91)
-    hq, hk, d, prefix, t = 24, 4, 256, 3000, 40
+    hq, hk, d, prefix = 24, 4, 256, 3000
     cap = ((prefix + t + 63) // 64) * 64
     k = randn_f16(rng, (prefix + t, hk, d))
     v = randn_f16(rng, (prefix + t, hk, d))
     q = randn_f16(rng, (t, hq, d))
     # key 1700 of kv head 0 and key 2900 of kv head 3 align with two query rows
     k[1700, 0] = (q[t - 1, 0].astype(np.float32) * 6).astype(np.float16)
-    k[2900, 3] = (q[5, 20].astype(np.float32) * 6).astype(np.float16)
+    k[2900, 3] = (q[min(5, t - 1), 20].astype(np.float32) * 6).astype(np.float16)
     cache = m.KvCache.contiguous(hk, d, cap)
     cache.append(_dev(k, gpu), _dev(v, gpu))
     kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
@@ -299,3 +300,26 @@ def test_suffix_short_on_a_second_sequence(gpu, t):
     expect = oracle.suffix_attention_q8(q.astype(np.float32), kc, ks, vc, vs, prefix, hq, 1 / math.sqrt(d))
     assert_attention_close(out.cpu().numpy(), expect, "seq 1")
     assert_attention_close(gated.cpu().numpy(), expect / (1 + np.exp(-gate)), "seq 1 gated")
+
+
+# (hq, hk, d, prefix, t): tokens packed per decode row set = largest divisor of t with
+# t_pack * (hq / hk) <= 16: 32q/8kv t=4 -> 4, t=6 -> 3 (two row sets), t=2 -> 2;
+# 24q/4kv t=2 -> 2, t=4 -> 2; 16q/16kv t=10 -> 10; 24q/4kv t=5 -> 1.
+@pytest.mark.parametrize("hq,hk,d,prefix,t", [(32, 8, 128, 3000, 4), (32, 8, 128, 700, 6), (32, 8, 128, 4100, 2),
+                                              (24, 4, 256, 2000, 2), (24, 4, 256, 1234, 4), (16, 16, 128, 999, 10),
+                                              (24, 4, 256, 640, 5)])
+def test_suffix_short_packed_tokens(gpu, hq, hk, d, prefix, t):
+    """Short suffixes pack several tokens into one decode row set (one context stream
+    serves them all); each packed column masks the keys past its own token."""
+    import miinfer_amd as m
+    rng = np.random.default_rng(prefix + t)
+    cap = ((prefix + t + 63) // 64) * 64
+    cache, ref = _setup(gpu, rng, hq, hk, d, prefix, t, cap)
+    q = randn_f16(rng, (t, hq, d))
+    gate = rng.standard_normal((t, hq, d)).astype(np.float32)
+    out, gated = m.suffix_attention(cache, _dev(q, gpu), prefix, gate=_dev(gate, gpu),
+                                    out=torch.empty((t, hq, d), device=gpu))
+    torch.cuda.synchronize()
+    expect = oracle.suffix_attention_q8(q.astype(np.float32), *ref, prefix, hq, 1 / math.sqrt(d))
+    assert_attention_close(out.cpu().numpy(), expect, "packed")
+    assert_attention_close(gated.cpu().numpy(), expect / (1 + np.exp(-gate)), "packed gated")
