@@ -247,6 +247,22 @@ def bench_c4(dev, args) -> int:
         assert L.miikv_append_f16(cache.view, P(kp.data_ptr()), P(vp.data_ptr()), prefix, 0, 0,
                                   None, None, P(s.cuda_stream)) == 0
     us_bulk, _ = _time_graph(bulk, nrep, 5, inner=20)
+
+    # Short suffixes over the same prefix (speculative-verify sizes), through the same
+    # entry point: they run as a batch of decodes, several tokens per context pass.
+    short = {}
+    for ts in (1, 2, 4, 8):
+        ws_s = torch.empty(m.suffix_workspace_bytes(cache, hq, ts), dtype=torch.uint8, device=dev)
+        qs = q[:ts].contiguous()
+        outs = out[:ts]
+
+        def attn_short(s, ts=ts, ws_s=ws_s, qs=qs, outs=outs):
+            assert L.miikv_suffix_attn(cache.view, P(qs.data_ptr()), _lib.DTYPE_F16, hq,
+                                       ctypes.c_float(1 / math.sqrt(d)), ts, prefix, 0, None,
+                                       P(outs.data_ptr()), None, None, P(ws_s.data_ptr()),
+                                       ws_s.numel(), P(s.cuda_stream)) == 0
+        short[f"T{ts}_us"] = round(sorted(_time_graph(attn_short, max(4, nrep // 24), 3, inner=8)[0]
+                                          for _ in range(3))[1], 2)
     pairs = sum(prefix + i + 1 for i in range(t))
     flops = 4 * hq * d * pairs
     print(json.dumps({
@@ -265,6 +281,8 @@ def bench_c4(dev, args) -> int:
                    "GBs": round(t * append_bytes(hkv, d) / (us_app * 1e-6) / 1e9, 1)},
         "append_bulk": {"us": round(us_bulk, 2), "tokens": prefix,
                         "GBs": round(prefix * append_bytes(hkv, d) / (us_bulk * 1e-6) / 1e9, 1)},
+        "short_suffix": dict(short, note="miikv_suffix_attn with T tokens over the same 8192-token prefix "
+                                         "(a batch of decodes, 2 tokens per context pass)"),
     }), flush=True)
     return 0
 

@@ -74,12 +74,13 @@ def test_decode_step_graph_replays(gpu, fused):
     assert list(tokens_out.cpu().numpy()[:steps]) == toks
 
 
+@pytest.mark.parametrize("t", [64, 4])  # the MFMA path; a batch of decodes
 @pytest.mark.parametrize("fused", [False, True])
-def test_suffix_step_graph_replays(gpu, fused):
+def test_suffix_step_graph_replays(gpu, fused, t):
     """fused: the captured step is miikv_suffix_append_attn."""
     import miinfer_amd as m
     rng = np.random.default_rng(42)
-    hq, hk, d, cap, t = 24, 4, 256, 2048, 64
+    hq, hk, d, cap = 24, 4, 256, 2048
     cache = m.KvCache.contiguous(hk, d, cap)
     total = 3 * t + 700
     k_all = randn_f16(rng, (total, hk, d))
