@@ -219,38 +219,43 @@ __device__ __forceinline__ void rope_sincos_d(float a, float* s, float* c) {
 
 // The reference's K prologue for one row held one value per thread (thread t < D owns
 // dim t), in its own shape (qwen35_decoupled_k_norm_rope_kv_store_batch_quant_kernel,
-// gfx906/kernels/qwen3_primitives.hip:7257-7281): sum of squares by the LDS tree
+// gfx906/kernels/qwen3_primitives.hip:7257-7281): sum of squares by the tree
 // p[t] += p[t + stride], stride = D/2 .. 1; value * (1 / sqrt(ss / D + eps)) * weight;
-// pairs (t, t + 32), t < 32, rotated by position * step^t.  Same arithmetic as
-// miikv_append_f32's prologue, so the stored codes are the same.  Called by all 256
-// threads (barriers inside).
+// pairs (t, t + 32), t < 32, rotated by position * step^t.  Same additions in the same
+// order as miikv_append_f32's prologue, so the stored codes are the same.  Here the
+// levels that cross waves (strides >= 64) are formed by every wave from one LDS
+// exchange, the levels within a wave with shuffles, and each rotation pair (32 lanes
+// apart in wave 0) with one swap, so the whole prologue costs one barrier.  Called by
+// all 256 threads.
 template <uint32_t D>
 __device__ void k_prologue(float& kx, float w, uint32_t tid, uint32_t position, float step, float eps) {
 #pragma clang fp contract(off)
+    static_assert(D == 128 || D == 256, "the tree's cross-wave levels are written for D = 128 and 256");
     __shared__ float s_p[256];
-    __shared__ float s_rot[64];
+    const uint32_t lane = tid & 63;
     s_p[tid] = tid < D ? kx * kx : 0.0f;
     __syncthreads();
-    for (uint32_t stride = D / 2; stride > 0; stride >>= 1) {
-        if (tid < stride) s_p[tid] += s_p[tid + stride];
-        __syncthreads();
+    float p;  // p[lane] after the levels of stride >= 64 (the same value in every wave)
+    if constexpr (D == 256) {
+        const float a0 = s_p[lane] + s_p[lane + 128], a1 = s_p[lane + 64] + s_p[lane + 192];
+        p = a0 + a1;
+    } else {
+        p = s_p[lane] + s_p[lane + 64];
     }
-    const float r = 1.0f / sqrtf(s_p[0] / static_cast<float>(D) + eps);
+#pragma unroll
+    for (uint32_t stride = 32; stride > 0; stride >>= 1) p = p + __shfl_down(p, stride, 64);
+    const float ss = __shfl(p, 0, 64);
+    const float r = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
     kx = kx * r * w;
-    if (tid < 64) s_rot[tid] = kx;
-    __syncthreads();
-    if (tid < 32) {
+    if (tid < 64) {
         float angle = static_cast<float>(position);
-        for (uint32_t i = 0; i < tid; ++i) angle *= step;
+        for (uint32_t i = 0; i < (tid & 31); ++i) angle *= step;
         float sn, cs;
         rope_sincos_d(angle, &sn, &cs);
-        const float x0 = s_rot[tid], x1 = s_rot[tid + 32];
-        kx = x0 * cs - x1 * sn;
-        s_rot[tid + 32] = x0 * sn + x1 * cs;
+        const float other = __shfl_xor(kx, 32, 64);
+        kx = tid < 32 ? kx * cs - other * sn : other * sn + kx * cs;
     }
-    __syncthreads();
-    if (tid >= 32 && tid < 64) kx = s_rot[tid];
-    __syncthreads();  // s_p / s_rot are reused by the caller's next use
+    __syncthreads();  // s_p is reused by the next call
 }
 
 // Fused append for (sequence b, kv head h), by one 256-thread workgroup: quantise
