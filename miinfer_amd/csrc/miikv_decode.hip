@@ -989,6 +989,12 @@ struct NewRows {
     bool any() const { return k16 != nullptr || k32 != nullptr; }
 };
 
+// Dynamic LDS of decode_kernel with G columns: each wave's (m, l) and O^T for the
+// cross-wave merge, and its scale staging.
+static size_t decode_lds_bytes(uint32_t G, uint32_t D) {
+    return (32 * kWavesPerWg + kWavesPerWg * G * D) * sizeof(float) + kWavesPerWg * 2 * kChunk * (D / 32) * sizeof(uint16_t);
+}
+
 // Row sets that all read one sequence (a short suffix run as a batch of decodes):
 // row set b has context length (len_ptr ? *len_ptr : 0) + len_add + b, and row sets
 // at or past *count_ptr (when set) are skipped.
@@ -1078,8 +1084,7 @@ static miikv_status decode_impl(const miikv_view* view, const NewRows& rows,
     a.epsilon = rows.epsilon;
     a.q_f32 = q_dtype == MIIKV_DTYPE_F32;
 
-    const size_t lds = (32 * kWavesPerWg + kWavesPerWg * G * view->head_dim) * sizeof(float) +
-                       kWavesPerWg * 2 * kChunk * (view->head_dim / 32) * sizeof(uint16_t);
+    const size_t lds = decode_lds_bytes(G, view->head_dim);
     if (lds > 64 * 1024) return MIIKV_EUNSUPPORTED;
     // One workgroup per possible (sequence, kv head, split) work item, plus one per
     // (sequence, kv head) for the new token of the fused append.
@@ -1116,12 +1121,15 @@ namespace miikv {
 // Each row set streams its context once, so this pays for few tokens only; it
 // serves miikv_suffix_attn below a token-count threshold (miikv_suffix.hip).
 // Tokens per row set: the largest divisor of token_count whose columns (tokens x
-// query heads per kv head) fit the 16 of the MFMA; with a device token count, 1.
+// query heads per kv head) fit the 16 of the MFMA and the kernel's LDS; with a device
+// token count, 1.
+bool decode_columns_fit(uint32_t G, uint32_t D) { return G <= 16 && decode_lds_bytes(G, D) <= 64 * 1024; }
+
 uint32_t suffix_pack(const miikv_view* view, uint32_t q_heads, uint32_t token_count, bool device_count) {
     const uint32_t G = q_heads / view->kv_heads;
     if (device_count || G == 0 || G > 16) return 1;
     for (uint32_t p = std::min<uint32_t>(16 / G, token_count); p > 1; --p)
-        if (token_count % p == 0) return p;
+        if (token_count % p == 0 && decode_lds_bytes(p * G, view->head_dim) <= 64 * 1024) return p;
     return 1;
 }
 

@@ -606,7 +606,7 @@ namespace {
 // 80.7/77.8.  So: at most 6 row sets above a 16384-position capacity, 12 at or
 // below it.  MIIKV_SUFFIX_DECODE_MAX_T (a token count) overrides the rule.
 bool suffix_runs_as_decode(const miikv_view* v, uint32_t q_heads, uint32_t token_count, bool device_count) {
-    if (q_heads / v->kv_heads > 16) return false;
+    if (!decode_columns_fit(q_heads / v->kv_heads, v->head_dim)) return false;
     static const char* env = std::getenv("MIIKV_SUFFIX_DECODE_MAX_T");
     if (env) return token_count <= static_cast<uint32_t>(std::strtoul(env, nullptr, 10));
     if (token_count > kSuffixDecodeMaxT) return false;

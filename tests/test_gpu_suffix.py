@@ -323,3 +323,19 @@ def test_suffix_short_packed_tokens(gpu, hq, hk, d, prefix, t):
     expect = oracle.suffix_attention_q8(q.astype(np.float32), *ref, prefix, hq, 1 / math.sqrt(d))
     assert_attention_close(out.cpu().numpy(), expect, "packed")
     assert_attention_close(gated.cpu().numpy(), expect / (1 + np.exp(-gate)), "packed gated")
+
+
+# fp32 queries: 16q/4kv/D256 with 2 tokens per row set takes the paired-column
+# variant (hi parts in columns 0..7, lo parts in 8..15); 32q/8kv/D128 t=4 the
+# second fragment set.
+@pytest.mark.parametrize("hq,hk,d,prefix,t", [(16, 4, 256, 1500, 2), (16, 4, 256, 900, 4), (32, 8, 128, 2000, 4)])
+def test_suffix_short_packed_tokens_fp32_query(gpu, hq, hk, d, prefix, t):
+    import miinfer_amd as m
+    rng = np.random.default_rng(prefix + 7 * t)
+    cap = ((prefix + t + 63) // 64) * 64
+    cache, ref = _setup(gpu, rng, hq, hk, d, prefix, t, cap)
+    q = rng.standard_normal((t, hq, d)).astype(np.float32)
+    out, _ = m.suffix_attention(cache, _dev(q, gpu), prefix, out=torch.empty((t, hq, d), device=gpu))
+    torch.cuda.synchronize()
+    expect = oracle.suffix_attention_q8(q, *ref, prefix, hq, 1 / math.sqrt(d))
+    assert_attention_close(out.cpu().numpy(), expect, "packed fp32 query")
