@@ -663,8 +663,9 @@ static miikv_status launch_append(const miikv_view* view, const AppendIn& in, ui
     // Positions known on the host: [head partial group][whole groups][tail partial group].
     // (The grouped store assembles q8 codes and scales; caches with an fp16 plane take
     // the per-row kernel.)
+    static const bool rows_only = std::getenv("MIIKV_APPEND_ROWS_ONLY") != nullptr;  // measurement
     if (ps == nullptr && ds == nullptr && positions == nullptr && rows_tokens >= kTileAppendMin &&
-        view->quant_mode == MIIKV_KV_Q8_Q8 && std::getenv("MIIKV_APPEND_ROWS_ONLY") == nullptr) {
+        view->quant_mode == MIIKV_KV_Q8_Q8 && !rows_only) {
         const uint32_t D = view->head_dim;
         const uint32_t head = (32 - base % 32) % 32;
         const uint32_t whole = (rows_tokens - head) / 32;
