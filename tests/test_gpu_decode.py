@@ -322,3 +322,19 @@ def test_side_stream_temporaries(gpu):
         expect = oracle.attention_q8(q[s].cpu().numpy().astype(np.float32), kc, ks, vc, vs, 700, hq,
                                      1 / math.sqrt(d))
         assert_attention_close(out_ref[s].cpu().numpy(), expect, f"row {s}")
+
+
+@pytest.mark.parametrize("length", [131072, 100003])
+def test_decode_128k_context(gpu, length):
+    """Config 2 shape at a 131072-token capacity (16 steps per wave, 64 splits of 2048
+    keys): the largest context tested; 100003 ends mid-split and mid-step."""
+    import miinfer_amd as m
+    hq, hk, d, cap = 32, 8, 128, 131072
+    rng = np.random.default_rng(length)
+    cache, ref = _filled_contiguous(gpu, rng, hk, d, cap, length)
+    q = randn_f16(rng, (1, hq, d))
+    lens = _dev(np.array([length], np.int32), gpu)
+    out, _ = m.decode_attention(cache, _dev(q, gpu), lengths=lens, max_context=cap)
+    torch.cuda.synchronize()
+    expect = oracle.attention_q8(q[0].astype(np.float32), *ref, length, hq, 1 / math.sqrt(d))
+    assert_attention_close(out[0].cpu().numpy(), expect, f"L={length}")

@@ -339,3 +339,20 @@ def test_suffix_short_packed_tokens_fp32_query(gpu, hq, hk, d, prefix, t):
     torch.cuda.synchronize()
     expect = oracle.suffix_attention_q8(q, *ref, prefix, hq, 1 / math.sqrt(d))
     assert_attention_close(out.cpu().numpy(), expect, "packed fp32 query")
+
+
+@pytest.mark.parametrize("split", [True, False])
+def test_suffix_64k_prefix_sampled_tokens(gpu, split):
+    """A 64-token suffix over a 65536-token prefix (the prefix length of the reference's
+    published suffix runs), 24q/4kv/D256, on the MFMA path; sampled tokens."""
+    import miinfer_amd as m
+    hq, hk, d, prefix, t = 24, 4, 256, 65536, 64
+    rng = np.random.default_rng(65)
+    cache, ref = _setup(gpu, rng, hq, hk, d, prefix, t, prefix + t)
+    q = randn_f16(rng, (t, hq, d))
+    out, _ = m.suffix_attention(cache, _dev(q, gpu), prefix, split=split)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    for tok in (0, 31, 63):
+        expect = oracle.attention_q8(q[tok].astype(np.float32), *ref, prefix + tok + 1, hq, 1 / math.sqrt(d))
+        assert_attention_close(out[tok], expect, f"token {tok}")
