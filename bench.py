@@ -186,6 +186,56 @@ def bench_c3(dev, args) -> int:
     return 0
 
 
+# The reference's published Q8 suffix ladder (S = 512, 16 GQA layers, 24q/4kv/D256,
+# q8 K and V; MI50, experiments/EXP-V2-0019-quantized-kv-cache.md:53-55), ms per 16 layers.
+REFERENCE_SUFFIX_LADDER_MI50_MS = {4096: 662.96, 32768: 4971.17, 65536: 10506.89}
+
+
+def suffix_ladder(dev) -> dict:
+    """The reference's suffix ladder workload on this GPU: a 512-token suffix attending
+    over P cached tokens plus itself, 16 layers (16 distinct caches, one graph replay
+    runs each once), attention only (the suffix rows are already stored).  Reported
+    beside the reference's MI50 figures: other hardware, not a like-for-like baseline."""
+    import ctypes
+
+    import torch
+
+    import miinfer_amd as m
+    from miinfer_amd import _lib
+    hq, hkv, d, t, layers = 24, 4, 256, 512, 16
+    L = _lib.lib()
+    P = ctypes.c_void_p
+    res = {}
+    for prefix, ref_ms in REFERENCE_SUFFIX_LADDER_MI50_MS.items():
+        torch.manual_seed(prefix)
+        caches = []
+        for _ in range(layers):
+            c = m.KvCache.contiguous(hkv, d, prefix + t, device=dev)
+            for t0 in range(0, prefix + t, 8192):
+                n = min(8192, prefix + t - t0)
+                c.append(torch.randn((n, hkv, d), device=dev).half(), torch.randn((n, hkv, d), device=dev).half(),
+                         base_position=t0)
+            caches.append(c)
+        q = torch.randn((t, hq, d), device=dev).half()
+        out = torch.empty((t, hq, d), device=dev)
+        ws_bytes = m.suffix_workspace_bytes(caches[0], hq, t)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+
+        def attn(i, s):
+            assert L.miikv_suffix_attn(caches[i % layers].view, P(q.data_ptr()), _lib.DTYPE_F16, hq,
+                                       ctypes.c_float(1 / math.sqrt(d)), t, prefix, 0, None, P(out.data_ptr()),
+                                       None, None, P(ws.data_ptr()), ws_bytes, P(s.cuda_stream)) == 0
+        med, p10, p90 = _graph_median(attn, layers, replays=10, warm=2)
+        res[str(prefix)] = {"ms_16_layers": round(med * layers / 1e3, 3), "p10_ms": round(p10 * layers / 1e3, 3),
+                            "p90_ms": round(p90 * layers / 1e3, 3), "reference_mi50_ms": ref_ms,
+                            "ratio": round(ref_ms / (med * layers / 1e3), 1)}
+        del caches, ws
+        torch.cuda.empty_cache()
+    res["note"] = ("S=512 suffix over P cached tokens, 24q/4kv/D256 q8_0, 16 layers (distinct caches), attention "
+                   "only; reference: MI50, EXP-V2-0019-quantized-kv-cache.md:53-55 (other hardware)")
+    return res
+
+
 def bench_c4(dev, args) -> int:
     """Config 4: 512-token suffix (24q/4kv/D256) over an 8192-token q8_0 prefix: append the
     512 new K/V rows, then causal suffix attention.  MFMA roofline over the visible pairs."""
@@ -263,6 +313,7 @@ def bench_c4(dev, args) -> int:
                                        ws_s.numel(), P(s.cuda_stream)) == 0
         short[f"T{ts}_us"] = round(sorted(_time_graph(attn_short, max(4, nrep // 24), 3, inner=8)[0]
                                           for _ in range(3))[1], 2)
+    ladder = suffix_ladder(dev) if not getattr(args, "no_sweep", False) else None
     pairs = sum(prefix + i + 1 for i in range(t))
     flops = 4 * hq * d * pairs
     print(json.dumps({
@@ -283,6 +334,7 @@ def bench_c4(dev, args) -> int:
                         "GBs": round(prefix * append_bytes(hkv, d) / (us_bulk * 1e-6) / 1e9, 1)},
         "short_suffix": dict(short, note="miikv_suffix_attn with T tokens over the same 8192-token prefix "
                                          "(a batch of decodes, 2 tokens per context pass)"),
+        "reference_ladder": ladder,
     }), flush=True)
     return 0
 
