@@ -596,7 +596,62 @@ def decode_variants(dev, ctx: int = 32768, nl: int = 8) -> dict:
         "GBs_median": round(fbytes / (med * 1e-6) / 1e9, 1), "kv_bytes_per_launch": fbytes}
     del caches
     torch.cuda.empty_cache()
+    out["reference_decode_ladder"] = reference_decode_ladder(dev)
     return out
+
+
+# The reference's published split-K decode attention (fp16 K/V, one layer, 24q/4kv/D256;
+# MI50, experiments/EXP-0203-wave64-barrier-free-splitk-attention.md:42-46), ms.
+REFERENCE_DECODE_FP16_MI50_MS = {4096: 0.393, 16384: 0.762, 32768: 1.032, 65536: 1.893}
+
+
+def reference_decode_ladder(dev, nl: int = 8) -> dict:
+    """Decode attention at the reference's decode-ladder shape (24q/4kv/D256, batch 1,
+    one query token) and contexts, fp16 K/V (its kernel's format) and q8_0, cold (nl
+    rotated layer caches), attention only; beside the reference's MI50 figures (other
+    hardware, not a like-for-like baseline)."""
+    import ctypes
+
+    import torch
+
+    import miinfer_amd as m
+    from miinfer_amd import _lib
+    hq, hkv, d = 24, 4, 256
+    L = _lib.lib()
+    P = ctypes.c_void_p
+    res = {}
+    for ctx, ref_ms in REFERENCE_DECODE_FP16_MI50_MS.items():
+        row = {"reference_mi50_fp16_ms": ref_ms}
+        for name, mode in (("fp16", _lib.KV_FP16_FP16), ("q8_0", _lib.KV_Q8_Q8)):
+            torch.manual_seed(ctx)
+            caches = []
+            for _ in range(nl):
+                c = m.KvCache.contiguous(hkv, d, ctx, device=dev, quant_mode=mode)
+                for t0 in range(0, ctx, 8192):
+                    n = min(8192, ctx - t0)
+                    c.append(torch.randn((n, hkv, d), device=dev).half(), torch.randn((n, hkv, d), device=dev).half(),
+                             base_position=t0)
+                caches.append(c)
+            q = torch.randn((1, hq, d), device=dev).half()
+            o = torch.empty((1, hq, d), device=dev)
+            lens = torch.tensor([ctx], dtype=torch.int32, device=dev)
+            ws = m.DecodeWorkspace(caches[0], hq, 1, ctx)
+
+            def step(i, s, caches=caches, q=q, o=o, lens=lens, ws=ws):
+                assert L.miikv_decode_attn(caches[i % nl].view, P(q.data_ptr()), _lib.DTYPE_F16, hq,
+                                           ctypes.c_float(1 / math.sqrt(d)), 1, P(lens.data_ptr()), None, ctx,
+                                           P(o.data_ptr()), None, None, P(ws.buf.data_ptr()), ws.bytes,
+                                           P(s.cuda_stream)) == 0
+            med, p10, p90 = _graph_median(step, 4 * nl, replays=20, warm=3)
+            kv_bytes = ctx * 2 * hkv * (2 * d if mode == _lib.KV_FP16_FP16 else d + 2 * (d // 32))
+            row[name + "_us"] = round(med, 2)
+            row[name + "_GBs"] = round(kv_bytes / (med * 1e-6) / 1e9, 1)
+            del caches, ws
+            torch.cuda.empty_cache()
+        res[str(ctx)] = row
+    res["note"] = ("decode attention, 24q/4kv/D256, batch 1, cold over rotated layer caches; reference: fp16 "
+                   "K/V on MI50, EXP-0203-wave64-barrier-free-splitk-attention.md:42-46 (other hardware)")
+    return res
 
 
 def decode_at(dev, ctx: int, nl: int, replays: int = 30) -> dict:

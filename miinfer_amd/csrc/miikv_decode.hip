@@ -883,7 +883,12 @@ Plan make_plan(const miikv_view* v, uint32_t q_heads, uint32_t batch, uint32_t m
     Plan p;
     const uint64_t chunks = (static_cast<uint64_t>(max_context) + kChunk - 1) / kChunk;
     const uint64_t waves = chunks * v->kv_heads * batch;
-    uint64_t cpw = (waves + kTargetWaves - 1) / kTargetWaves;
+    // D = 256, one sequence: a wave holds one step in flight (its step buffer is
+    // twice D = 128's), and one workgroup per CU with twice the steps per wave
+    // measured faster than two (24q/4kv batch 1, µs: 16k 17.9 -> 16.7, 32k 24.1 ->
+    // 23.0; 4k and 64k unchanged).  Batches keep the full target (config 3 is tuned so).
+    const uint64_t target = (v->head_dim == 256 && batch == 1) ? kTargetWaves / 2 : kTargetWaves;
+    uint64_t cpw = (waves + target - 1) / target;
     // MIIKV_DECODE_STEPS_PER_WAVE fixes the 32-token steps per wave (split size =
     // 4 waves x steps x 32 tokens), a tuning override in the spirit of the
     // reference's MIINFER_ATTENTION_SPLITS (qwen3_primitives.hip:5229-5245).

@@ -338,3 +338,19 @@ def test_decode_128k_context(gpu, length):
     torch.cuda.synchronize()
     expect = oracle.attention_q8(q[0].astype(np.float32), *ref, length, hq, 1 / math.sqrt(d))
     assert_attention_close(out[0].cpu().numpy(), expect, f"L={length}")
+
+
+@pytest.mark.parametrize("length,cap", [(16384, 16384), (32768, 32768), (20001, 32768), (5000, 65536)])
+def test_decode_d256_single_sequence_plans(gpu, length, cap):
+    """24q/4kv/D256, one sequence: the plans of 2, 4 and 8 steps per wave (one workgroup
+    per CU), full and partial contexts."""
+    import miinfer_amd as m
+    hq, hk, d = 24, 4, 256
+    rng = np.random.default_rng(length + cap)
+    cache, ref = _filled_contiguous(gpu, rng, hk, d, cap, length)
+    q = randn_f16(rng, (1, hq, d))
+    lens = _dev(np.array([length], np.int32), gpu)
+    out, _ = m.decode_attention(cache, _dev(q, gpu), lengths=lens, max_context=cap)
+    torch.cuda.synchronize()
+    expect = oracle.attention_q8(q[0].astype(np.float32), *ref, length, hq, 1 / math.sqrt(d))
+    assert_attention_close(out[0].cpu().numpy(), expect, f"L={length} cap={cap}")
