@@ -116,3 +116,48 @@ def test_load_rejects_mismatch_before_device_writes(tmp_path, case):
     r = L.lib().miikv_session_load(p.encode(), model, quant, views, n_layers, 0, segs, sizes, 2,
                                    toks.ctypes.data_as(ctypes.c_void_p), 16, ctypes.byref(plen), None)
     assert r == 0 and plen.value == 0
+
+
+# Header fields the loader checks against the caller (offset, size), and the token
+# payload; a change to any byte of them must be rejected before device memory is used.
+_CHECKED = [(0, 4), (4, 4), (104, 4), (108, 8), (116, 4), (120, 8), (128, 4), (132, 1), (133, 8), (141, 8)]
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_load_rejects_random_corruption(tmp_path, seed):
+    """Random byte changes in the checked header fields, the model / quantization
+    strings and the tokens of a valid file: inspect / load reject every one before
+    touching device memory (the device pointers here are fake), and never crash."""
+    from miinfer_amd import _lib as L
+    rng = np.random.default_rng(seed)
+    P, hk, d = 3, 2, 64
+    layer_bytes = 2 * P * hk * (d + 2 * d // 32)
+    p = str(tmp_path / "s.miinfer")
+    _write(p, tokens=[1, 2, 3], gdn=b"\0" * 16, kv=b"\0" * (2 * layer_bytes), layers=(1, 2))
+    good = open(p, "rb").read()
+    v = L.MiikvView()
+    v.k_codes = v.v_codes = 0x1000
+    v.k_scales = v.v_scales = 0x2000
+    v.layout = L.LAYOUT_CONTIGUOUS
+    v.quant_mode = L.KV_Q8_Q8
+    v.kv_heads, v.head_dim, v.page_tokens, v.num_pages = hk, d, 64, 1
+    views = (L.MiikvView * 2)(v, v)
+    segs = (ctypes.c_void_p * 2)(0x5000, 0x6000)
+    sizes = (ctypes.c_uint64 * 2)(8, 8)
+    regions = _CHECKED + [(8, len("Qwen3.8-27B")), (72, len("Q4_K_M")), (157, 12)]
+    for _ in range(200):
+        off, size = regions[int(rng.integers(len(regions)))]
+        data = bytearray(good)
+        for _ in range(int(rng.integers(1, 3))):
+            i = off + int(rng.integers(size))
+            data[i] = (data[i] + int(rng.integers(1, 256))) % 256
+        if bytes(data) == good:
+            continue  # the changes cancelled: a valid file would go on to the (fake) device pointers
+        with open(p, "wb") as f:
+            f.write(bytes(data))
+        toks = np.zeros(16, np.uint32)
+        plen = ctypes.c_uint32(0)
+        r = L.lib().miikv_session_load(p.encode(), b"Qwen3.8-27B", b"Q4_K_M", views, 2, 0, segs, sizes, 2,
+                                       toks.ctypes.data_as(ctypes.c_void_p), 16, ctypes.byref(plen), None)
+        assert r == 0 and plen.value == 0, (off, size)
+        assert not np.any(toks)
