@@ -236,6 +236,55 @@ def suffix_ladder(dev) -> dict:
     return res
 
 
+def chunked_prefill(dev, prefix: int = 65536, t: int = 512, layers: int = 4) -> dict:
+    """The last 512-token chunk of a chunked prefill at `prefix` cached tokens (24q/4kv/
+    D256, q8_0), per layer (`layers` rotated caches, each with its own workspace):
+    a fresh call expands the whole context into fp16 tiles, a call with
+    MIIKV_SUFFIX_TILES_CURRENT only its own steps (the earlier chunks, run the same way
+    while the caches were filled, left theirs in the workspace)."""
+    import ctypes
+
+    import torch
+
+    import miinfer_amd as m
+    from miinfer_amd import _lib
+    hq, hkv, d = 24, 4, 256
+    L = _lib.lib()
+    P = ctypes.c_void_p
+    torch.manual_seed(11)
+    caches, wss = [], []
+    q = torch.randn((t, hq, d), device=dev).half()
+    out = torch.empty((t, hq, d), device=dev)
+    for _ in range(layers):
+        c = m.KvCache.contiguous(hkv, d, prefix + t, device=dev)
+        ws = torch.empty(m.suffix_workspace_bytes(c, hq, t), dtype=torch.uint8, device=dev)
+        for base in range(0, prefix + t, t):  # the prefill, chunk by chunk, tiles kept current
+            c.append(torch.randn((t, hkv, d), device=dev).half(), torch.randn((t, hkv, d), device=dev).half(),
+                     base_position=base)
+            assert L.miikv_suffix_attn_ex(c.view, None, None, P(q.data_ptr()), _lib.DTYPE_F16, hq,
+                                          ctypes.c_float(1 / math.sqrt(d)), t, base, 0, None,
+                                          _lib.SUFFIX_TILES_CURRENT, P(out.data_ptr()), None, None,
+                                          P(ws.data_ptr()), ws.numel(), None) == 0
+        caches.append(c)
+        wss.append(ws)
+    torch.cuda.synchronize()
+    res = {}
+    for name, flags in (("fresh_us", 0), ("current_tiles_us", _lib.SUFFIX_TILES_CURRENT)):
+        def step(i, s, flags=flags):
+            assert L.miikv_suffix_attn_ex(caches[i % layers].view, None, None, P(q.data_ptr()), _lib.DTYPE_F16,
+                                          hq, ctypes.c_float(1 / math.sqrt(d)), t, prefix, 0, None, flags,
+                                          P(out.data_ptr()), None, None, P(wss[i % layers].data_ptr()),
+                                          wss[i % layers].numel(), P(s.cuda_stream)) == 0
+        med, p10, p90 = _graph_median(step, layers, replays=10, warm=2)
+        res[name] = round(med, 1)
+    res["note"] = (f"the chunk of {t} tokens at P = {prefix}, 24q/4kv/D256 q8_0, per layer over {layers} rotated "
+                   "caches and workspaces; fresh: miikv_suffix_attn (expands every key), current_tiles: "
+                   "miikv_suffix_attn_ex with MIIKV_SUFFIX_TILES_CURRENT (expands the chunk's own steps)")
+    del caches, wss
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_c4(dev, args) -> int:
     """Config 4: 512-token suffix (24q/4kv/D256) over an 8192-token q8_0 prefix: append the
     512 new K/V rows, then causal suffix attention.  MFMA roofline over the visible pairs."""
@@ -314,6 +363,7 @@ def bench_c4(dev, args) -> int:
         short[f"T{ts}_us"] = round(sorted(_time_graph(attn_short, max(4, nrep // 24), 3, inner=8)[0]
                                           for _ in range(3))[1], 2)
     ladder = suffix_ladder(dev) if not getattr(args, "no_sweep", False) else None
+    chunked = chunked_prefill(dev) if not getattr(args, "no_sweep", False) else None
     pairs = sum(prefix + i + 1 for i in range(t))
     flops = 4 * hq * d * pairs
     print(json.dumps({
@@ -335,6 +385,7 @@ def bench_c4(dev, args) -> int:
         "short_suffix": dict(short, note="miikv_suffix_attn with T tokens over the same 8192-token prefix "
                                          "(a batch of decodes, 2 tokens per context pass)"),
         "reference_ladder": ladder,
+        "chunked_prefill": chunked,
     }), flush=True)
     return 0
 

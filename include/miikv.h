@@ -314,6 +314,27 @@ miikv_status miikv_suffix_append_attn(const miikv_view* view, const uint16_t* k_
                                       const float* gate, float* gated_out, void* workspace,
                                       uint64_t workspace_bytes, void* stream);
 
+/* Suffix attention with flags; k_new / v_new optional (both set: as
+ * miikv_suffix_append_attn, both NULL: as miikv_suffix_attn).
+ * MIIKV_SUFFIX_TILES_CURRENT (chunked prefill, the reference's 512-token tiles over
+ * a growing prefix, attention_layer.cpp:297-343): the workspace keeps the fp16
+ * tiles of this sequence's context between calls, at a fixed per-head stride of
+ * the cache capacity, and the caller asserts that the tiles of every key below the
+ * base position (the prefill state's, when given) were expanded by earlier calls
+ * with this flag, this workspace and this sequence, and that those cache rows are
+ * unchanged since.  Each call then expands only the steps from the one holding the
+ * base position on (instead of the whole context) and leaves its own steps current
+ * for the next call, also when a short suffix runs as decodes.  One workspace per
+ * (layer, sequence); a workspace of miikv_suffix_workspace_bytes() bytes suffices.
+ * The first call of a sequence (base position 0) needs no earlier call. */
+#define MIIKV_SUFFIX_TILES_CURRENT 1u
+miikv_status miikv_suffix_attn_ex(const miikv_view* view, const uint16_t* k_new, const uint16_t* v_new,
+                                  const void* q, uint32_t q_dtype, uint32_t q_heads, float scale,
+                                  uint32_t token_count, uint32_t base_position, uint32_t seq,
+                                  const miikv_prefill_state* prefill_state, uint32_t flags, float* out,
+                                  const float* gate, float* gated_out, void* workspace,
+                                  uint64_t workspace_bytes, void* stream);
+
 /* ---- export / import ----------------------------------------------------- */
 
 /* Copy tokens [t0, t0+count) of sequence `seq` out of the tiled cache into

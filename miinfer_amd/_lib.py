@@ -25,6 +25,7 @@ KV_FP16_FP16 = 0
 KV_Q8_FP16 = 1
 KV_FP16_Q8 = 2
 KV_Q8_Q8 = 3
+SUFFIX_TILES_CURRENT = 1  # MIIKV_SUFFIX_TILES_CURRENT
 
 DTYPE_F16 = 0
 DTYPE_F32 = 1
@@ -133,6 +134,8 @@ SIGNATURES = {
                                           _P, _P, _P, _P, _U64, _P]),
     "miikv_suffix_append_attn": (ctypes.c_int, [_VP, _P, _P, _P, _U32, _U32, ctypes.c_float, _U32, _U32, _U32,
                                                  _P, _P, _P, _P, _P, _U64, _P]),
+    "miikv_suffix_attn_ex": (ctypes.c_int, [_VP, _P, _P, _P, _U32, _U32, ctypes.c_float, _U32, _U32, _U32,
+                                             _P, _U32, _P, _P, _P, _P, _U64, _P]),
 }
 
 _lib = None

@@ -76,12 +76,13 @@ __global__ void __launch_bounds__(256) expand_kernel(ExpandArgs a) {
     const Geo& geo = a.g;
     // Last step first: with the fused append the suffix's steps, which carry the
     // longer quantise-and-store chain, are dispatched ahead of the rest.
-    const uint32_t step = gridDim.x - 1 - blockIdx.x;
+    const uint32_t step = a.step0 + (gridDim.x - 1 - blockIdx.x);
     const uint32_t h = blockIdx.y;
     const uint32_t tid = threadIdx.x;
     const uint32_t nkeys = context_keys(a.key_count, a.ps);
     const uint32_t tok0 = step * kSufStep;
     if (tok0 >= nkeys) return;
+    if (a.current && a.ps != nullptr && step < a.ps->base_position / kSufStep) return;  // already expanded
     const size_t slab = slab_of(geo, a.seq, tok0, h);
     const uint32_t tp0 = tok0 % geo.page_tokens;
     const size_t sc0 = (slab * geo.page_tokens + tp0) * NB;
@@ -628,12 +629,15 @@ struct SuffixPlan {
 // 256 keys per split).  Monotone in key_bound, so a plan made with the cache
 // capacity covers any smaller context.
 SuffixPlan make_suffix_plan(const miikv_view* v, uint32_t q_heads, uint32_t tokens, uint64_t key_bound,
-                            bool allow_split) {
+                            bool allow_split, uint64_t stride_bound = 0) {
     SuffixPlan p{1, 0, 0, 0, 0};
     const uint32_t G = q_heads / v->kv_heads;
-    p.steps = static_cast<uint32_t>((key_bound + kSufStep - 1) / kSufStep);
+    // the tile area holds stride_bound keys per kv head (the capacity for incremental
+    // tiles, whose layout must not move between calls), the splits cover key_bound
+    p.steps = static_cast<uint32_t>((std::max(key_bound, stride_bound) + kSufStep - 1) / kSufStep);
     p.tile_bytes = static_cast<uint64_t>(v->kv_heads) * p.steps * tile_halves(v->head_dim) * 2;
-    p.split_keys = static_cast<uint32_t>(std::min<uint64_t>(static_cast<uint64_t>(p.steps) * kSufStep, 0xffffff00u));
+    const uint64_t key_steps = (key_bound + kSufStep - 1) / kSufStep;
+    p.split_keys = static_cast<uint32_t>(std::min<uint64_t>(key_steps * kSufStep, 0xffffff00u));
     if (!allow_split) return p;
     const uint64_t wgs = (static_cast<uint64_t>(tokens) * G + kSufRows - 1) / kSufRows * v->kv_heads;
     // Splits: as many as keep every workgroup resident in one round (the
@@ -664,21 +668,22 @@ SuffixPlan make_suffix_plan(const miikv_view* v, uint32_t q_heads, uint32_t toke
 extern "C" uint64_t miikv_suffix_workspace_bytes(const miikv_view* view, uint32_t q_heads, uint32_t token_count) {
     if (validate_view(view) != MIIKV_OK || q_heads == 0 || q_heads % view->kv_heads != 0 || token_count == 0)
         return 0;
-    // room for either path: a short suffix runs as decodes when the workspace holds
-    // their records, else on the MFMA path
+    // Room for either path and for incremental tiles: the tiles of every key of the
+    // capacity, then the larger of the split records and a short suffix's decode
+    // records (a short suffix keeping the tiles current needs both).
+    const uint64_t cap = view_seq_capacity(view);
     uint64_t dec = 0;
     if (suffix_runs_as_decode(view, q_heads, token_count, false) ||
-        suffix_runs_as_decode(view, q_heads, token_count, true)) {
-        const uint64_t cap = std::min<uint64_t>(view_seq_capacity(view), 0xffffffffu);
-        dec = suffix_by_decode_bytes(view, q_heads, token_count, static_cast<uint32_t>(cap));
-    }
-    return std::max(dec, make_suffix_plan(view, q_heads, token_count, view_seq_capacity(view), true).total());
+        suffix_runs_as_decode(view, q_heads, token_count, true))
+        dec = suffix_by_decode_bytes(view, q_heads, token_count, static_cast<uint32_t>(std::min<uint64_t>(cap, 0xffffffffu)));
+    const SuffixPlan p = make_suffix_plan(view, q_heads, token_count, cap, true);
+    return p.tile_bytes + std::max(dec, p.part_bytes);
 }
 
 static miikv_status suffix_impl(const miikv_view* view, const uint16_t* k_new, const uint16_t* v_new, const void* q,
                                 uint32_t q_dtype, uint32_t q_heads, float scale, uint32_t token_count,
                                 uint32_t base_position, uint32_t seq, const miikv_prefill_state* prefill_state,
-                                float* out, const float* gate, float* gated_out, void* workspace,
+                                uint32_t flags, float* out, const float* gate, float* gated_out, void* workspace,
                                 uint64_t workspace_bytes, void* stream) {
     const int st = validate_view(view);
     if (st != MIIKV_OK) return st;
@@ -688,6 +693,8 @@ static miikv_status suffix_impl(const miikv_view* view, const uint16_t* k_new, c
     if (out == nullptr && !(gate != nullptr && gated_out != nullptr)) return MIIKV_EINVAL;
     if ((gate == nullptr) != (gated_out == nullptr)) return MIIKV_EINVAL;
     if (view->layout == MIIKV_LAYOUT_CONTIGUOUS && seq != 0) return MIIKV_EINVAL;
+    if ((flags & ~MIIKV_SUFFIX_TILES_CURRENT) != 0) return MIIKV_EINVAL;
+    const bool current = (flags & MIIKV_SUFFIX_TILES_CURRENT) != 0;
     if (token_count == 0) return MIIKV_OK;
     if (k_new != nullptr && view->quant_mode != MIIKV_KV_Q8_Q8) return MIIKV_EUNSUPPORTED;  // stores q8 rows
     const uint64_t cap = view_seq_capacity(view);
@@ -702,49 +709,66 @@ static miikv_status suffix_impl(const miikv_view* view, const uint16_t* k_new, c
     const uint64_t bound = prefill_state ? cap : static_cast<uint64_t>(base_position) + token_count;
     if (workspace == nullptr) return MIIKV_EWORKSPACE;
     const uint32_t bound32 = static_cast<uint32_t>(std::min<uint64_t>(bound, 0xffffffffu));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    _Float16* tiles = static_cast<_Float16*>(workspace);
+    // Incremental tiles: the tile area holds every key of the capacity at a fixed
+    // stride; steps below the base position are current, the rest are expanded here.
+    const uint64_t stride_bound = current ? cap : 0;
+    const uint32_t host_step0 = current && prefill_state == nullptr ? base_position / kSufStep : 0u;
+    auto expand = [&](const SuffixPlan& plan, bool append) {
+        ExpandArgs e;
+        e.g = make_geo(*view);
+        e.seq = seq;
+        e.key_count = bound32;
+        e.ps = prefill_state;
+        e.steps = plan.steps;
+        e.tiles = tiles;
+        e.k_new = append ? k_new : nullptr;
+        e.v_new = append ? v_new : nullptr;
+        e.token_count = token_count;
+        e.base_position = base_position;
+        e.step0 = host_step0;
+        e.current = current ? 1u : 0u;
+        const uint32_t key_steps = static_cast<uint32_t>((bound + kSufStep - 1) / kSufStep);
+        const dim3 egrid(key_steps - host_step0, view->kv_heads);
+        if (append) {
+            if (view->head_dim == 128) hipLaunchKernelGGL((expand_kernel<128, true>), egrid, dim3(256), 0, s, e);
+            else hipLaunchKernelGGL((expand_kernel<256, true>), egrid, dim3(256), 0, s, e);
+        } else {
+            if (view->head_dim == 128) hipLaunchKernelGGL((expand_kernel<128, false>), egrid, dim3(256), 0, s, e);
+            else hipLaunchKernelGGL((expand_kernel<256, false>), egrid, dim3(256), 0, s, e);
+        }
+    };
     // (a workspace sized for the MFMA path alone runs that path)
+    const SuffixPlan tile_plan = make_suffix_plan(view, q_heads, token_count, bound, false, stride_bound);
+    const uint64_t dec_off = current ? tile_plan.tile_bytes : 0;  // the tiles stay below the records
     if (suffix_runs_as_decode(view, q_heads, token_count, prefill_state != nullptr) &&
-        workspace_bytes >= suffix_by_decode_bytes(view, q_heads, token_count, bound32)) {
+        workspace_bytes >= dec_off + suffix_by_decode_bytes(view, q_heads, token_count, bound32)) {
         // the suffix's own rows first; every token then reads its context from the cache
         if (k_new != nullptr) {
             const miikv_status ast = miikv_append_f16(view, k_new, v_new, token_count, base_position, seq,
                                                       prefill_state, nullptr, stream);
             if (ast != MIIKV_OK) return ast;
         }
+        if (current) {
+            if (tile_plan.steps > 65535u * 64u) return MIIKV_EINVAL;
+            expand(tile_plan, false);  // the suffix's own steps, for the next call
+        }
         return suffix_by_decode(view, q, q_dtype, q_heads, scale, token_count, base_position, seq, prefill_state,
-                                bound32, out, gate, gated_out, workspace, workspace_bytes, stream);
+                                bound32, out, gate, gated_out, static_cast<uint8_t*>(workspace) + dec_off,
+                                workspace_bytes - dec_off, stream);
     }
-    SuffixPlan plan = make_suffix_plan(view, q_heads, token_count, bound, true);
+    SuffixPlan plan = make_suffix_plan(view, q_heads, token_count, bound, true, stride_bound);
     if (workspace_bytes < plan.total()) {
-        plan = make_suffix_plan(view, q_heads, token_count, bound, false);
+        plan = tile_plan;
         if (workspace_bytes < plan.total()) return MIIKV_EWORKSPACE;
     }
     if (plan.steps > 65535u * 64u) return MIIKV_EINVAL;
-    _Float16* tiles = static_cast<_Float16*>(workspace);
-    hipStream_t s = static_cast<hipStream_t>(stream);
 
-    ExpandArgs e;
-    e.g = make_geo(*view);
-    e.seq = seq;
-    e.key_count = static_cast<uint32_t>(std::min<uint64_t>(bound, 0xffffffffu));
-    e.ps = prefill_state;
-    e.steps = plan.steps;
-    e.tiles = tiles;
-    e.k_new = k_new;
-    e.v_new = v_new;
-    e.token_count = token_count;
-    e.base_position = base_position;
-    const dim3 egrid(plan.steps, view->kv_heads);
-    if (k_new != nullptr) {
-        if (view->head_dim == 128) hipLaunchKernelGGL((expand_kernel<128, true>), egrid, dim3(256), 0, s, e);
-        else hipLaunchKernelGGL((expand_kernel<256, true>), egrid, dim3(256), 0, s, e);
-    } else {
-        if (view->head_dim == 128) hipLaunchKernelGGL((expand_kernel<128, false>), egrid, dim3(256), 0, s, e);
-        else hipLaunchKernelGGL((expand_kernel<256, false>), egrid, dim3(256), 0, s, e);
-    }
+    expand(plan, k_new != nullptr);
 
     SuffixArgs a;
-    a.g = e.g;
+    a.g = make_geo(*view);
     a.q = q;
     a.q_f32 = q_dtype == MIIKV_DTYPE_F32;
     a.q_heads = q_heads;
@@ -796,7 +820,7 @@ extern "C" miikv_status miikv_suffix_attn(const miikv_view* view, const void* q,
                                           float* gated_out, void* workspace, uint64_t workspace_bytes,
                                           void* stream) {
     return suffix_impl(view, nullptr, nullptr, q, q_dtype, q_heads, scale, token_count, base_position, seq,
-                       prefill_state, out, gate, gated_out, workspace, workspace_bytes, stream);
+                       prefill_state, 0u, out, gate, gated_out, workspace, workspace_bytes, stream);
 }
 
 extern "C" miikv_status miikv_suffix_append_attn(const miikv_view* view, const uint16_t* k_new, const uint16_t* v_new,
@@ -807,5 +831,16 @@ extern "C" miikv_status miikv_suffix_append_attn(const miikv_view* view, const u
                                                  uint64_t workspace_bytes, void* stream) {
     if (k_new == nullptr || v_new == nullptr) return MIIKV_EINVAL;
     return suffix_impl(view, k_new, v_new, q, q_dtype, q_heads, scale, token_count, base_position, seq,
-                       prefill_state, out, gate, gated_out, workspace, workspace_bytes, stream);
+                       prefill_state, 0u, out, gate, gated_out, workspace, workspace_bytes, stream);
+}
+
+extern "C" miikv_status miikv_suffix_attn_ex(const miikv_view* view, const uint16_t* k_new, const uint16_t* v_new,
+                                             const void* q, uint32_t q_dtype, uint32_t q_heads, float scale,
+                                             uint32_t token_count, uint32_t base_position, uint32_t seq,
+                                             const miikv_prefill_state* prefill_state, uint32_t flags, float* out,
+                                             const float* gate, float* gated_out, void* workspace,
+                                             uint64_t workspace_bytes, void* stream) {
+    if ((k_new == nullptr) != (v_new == nullptr)) return MIIKV_EINVAL;
+    return suffix_impl(view, k_new, v_new, q, q_dtype, q_heads, scale, token_count, base_position, seq,
+                       prefill_state, flags, out, gate, gated_out, workspace, workspace_bytes, stream);
 }

@@ -48,6 +48,11 @@ struct ExpandArgs {
     const uint16_t* v_new;
     uint32_t token_count;
     uint32_t base_position;
+    // Incremental tiles: grid x covers steps step0 + (gridDim.x - 1 - blockIdx.x); with
+    // `current` set the steps wholly below the base position (the prefill state's, on
+    // the device) are already expanded in the tile area and are skipped.
+    uint32_t step0;
+    uint32_t current;
 };
 
 struct SuffixArgs {

@@ -410,7 +410,7 @@ def suffix_attention(cache: KvCache, q: torch.Tensor, base_position: int, scale:
                      gate: torch.Tensor | None = None, out: torch.Tensor | None = None,
                      gated_out: torch.Tensor | None = None, split: bool = True,
                      k_new: torch.Tensor | None = None, v_new: torch.Tensor | None = None,
-                     workspace: torch.Tensor | None = None, stream=None):
+                     workspace: torch.Tensor | None = None, tiles_current: bool = False, stream=None):
     """Causal attention of a T-token suffix (rows already appended at base_position..)
     over the cache.  q: [T, q_heads, head_dim] fp16/fp32.  Returns (out, gated_out).
     With k_new / v_new (fp16 [T, kv_heads, head_dim]) the suffix's rows are quantised
@@ -418,7 +418,12 @@ def suffix_attention(cache: KvCache, q: torch.Tensor, base_position: int, scale:
 
     The workspace holds the context's expanded fp16 tiles plus, for split-K, the
     partial records: split=True allocates suffix_workspace_bytes() (unless given);
-    split=False allocates the tiles only, which runs one split."""
+    split=False allocates the tiles only, which runs one split.
+
+    tiles_current (chunked prefill, with the same `workspace` for every chunk of one
+    sequence and layer): the workspace's tiles of the keys below the base position
+    are current from earlier calls, so only the new steps are expanded
+    (MIIKV_SUFFIX_TILES_CURRENT)."""
     t, q_heads, d = q.shape
     if d != cache.head_dim or not q.is_contiguous() or q.dtype not in (torch.float16,
                                                                         torch.float32):
@@ -453,6 +458,12 @@ def suffix_attention(cache: KvCache, q: torch.Tensor, base_position: int, scale:
             if tns.dtype != torch.float16 or tuple(tns.shape) != (t, cache.kv_heads, d) or \
                     not tns.is_contiguous():
                 raise ValueError("k_new/v_new must be contiguous fp16 [T, kv_heads, head_dim]")
+    if tiles_current:
+        call("miikv_suffix_attn_ex", cache.view, _ptr(k_new), _ptr(v_new), _ptr(q), qd, q_heads, float(scale), t,
+             base_position, seq, _ptr(prefill_state), _lib.SUFFIX_TILES_CURRENT, _ptr(out), _ptr(gate),
+             _ptr(gated_out), _ptr(workspace), ws_bytes, _stream(stream))
+        return out, gated_out
+    if k_new is not None:
         call("miikv_suffix_append_attn", cache.view, _ptr(k_new), _ptr(v_new), _ptr(q), qd, q_heads,
              float(scale), t, base_position, seq, _ptr(prefill_state), _ptr(out), _ptr(gate),
              _ptr(gated_out), _ptr(workspace), ws_bytes, _stream(stream))

@@ -141,7 +141,7 @@ def test_suffix_workspace_bytes_plan():
     (2*D*32 halves per step and kv head) plus, when the key range is split, one record
     per query row (token x head of the group), kv head and split: the row's normalised
     output in fp16 (2*D bytes) and its (m, l) pair in fp32 (8 bytes).  Short suffixes,
-    which may run as a batch of decodes, get at least the decode records' room."""
+    which may run as a batch of decodes, get the tiles plus the decode records' room."""
     L = _lib()
     lib = L.lib()
     v = _view(page_tokens=8704, kv_heads=4, head_dim=256)
@@ -154,10 +154,11 @@ def test_suffix_workspace_bytes_plan():
     # 17 tokens (no packing: 17 decode row sets) run on the MFMA path, one split
     assert lib.miikv_suffix_workspace_bytes(ctypes.byref(short), 24, 17) == 4 * 8 * 2 * 256 * 32 * 2
     # 16 tokens may run as decodes (2 tokens per row set, or 16 row sets with a device
-    # token count): room for the larger of those plans and the tiles
+    # token count): the tiles (kept current for chunked prefill) plus the larger of
+    # those plans' records
     dec = max(lib.miikv_decode_workspace_bytes(ctypes.byref(short), 24, 16, 256),
               lib.miikv_decode_workspace_bytes(ctypes.byref(short), 48, 8, 256))
-    assert lib.miikv_suffix_workspace_bytes(ctypes.byref(short), 24, 16) == max(dec, 4 * 8 * 2 * 256 * 32 * 2)
+    assert lib.miikv_suffix_workspace_bytes(ctypes.byref(short), 24, 16) == 4 * 8 * 2 * 256 * 32 * 2 + dec
     assert lib.miikv_suffix_workspace_bytes(ctypes.byref(v), 24, 0) == 0
     assert lib.miikv_suffix_workspace_bytes(ctypes.byref(v), 25, 512) == 0  # invalid heads
 

@@ -114,15 +114,23 @@ def test_suffix_split_matches_unsplit(gpu):
 
 
 def test_suffix_workspace_too_small_is_rejected(gpu):
+    """64 tokens (the MFMA path): a workspace holding just the context's tiles runs
+    one split (same results as the full workspace within the split tolerance, and the
+    oracle's); one byte less is rejected."""
     import miinfer_amd as m
     rng = np.random.default_rng(12)
-    cache, _ = _setup(gpu, rng, 24, 4, 256, 2048, 16, 2048 + 64)
-    q = _dev(randn_f16(rng, (16, 24, 256)), gpu)
-    need = m.suffix_workspace_bytes(cache, 24, 16)
-    assert need > 0
+    hq, hk, d, prefix, t = 24, 4, 256, 2048, 64
+    cache, ref = _setup(gpu, rng, hq, hk, d, prefix, t, prefix + t)
+    q16 = randn_f16(rng, (t, hq, d))
+    q = _dev(q16, gpu)
+    tiles = hk * ((prefix + t + 31) // 32) * 2 * d * 32 * 2
+    assert m.suffix_workspace_bytes(cache, hq, t) > tiles
+    out, _ = m.suffix_attention(cache, q, prefix, workspace=torch.empty(tiles, dtype=torch.uint8, device=gpu))
+    torch.cuda.synchronize()
+    expect = oracle.suffix_attention_q8(q16.astype(np.float32), *ref, prefix, hq, 1 / math.sqrt(d))
+    assert_attention_close(out.cpu().numpy(), expect, "single split")
     with pytest.raises(m.MiikvError):
-        m.suffix_attention(cache, q, 2048, workspace=torch.empty(need // 2, dtype=torch.uint8,
-                                                                  device=gpu))
+        m.suffix_attention(cache, q, prefix, workspace=torch.empty(tiles - 1, dtype=torch.uint8, device=gpu))
 
 
 def _canon_all(cache, seq, n):
@@ -356,3 +364,87 @@ def test_suffix_64k_prefix_sampled_tokens(gpu, split):
     for tok in (0, 31, 63):
         expect = oracle.attention_q8(q[tok].astype(np.float32), *ref, prefix + tok + 1, hq, 1 / math.sqrt(d))
         assert_attention_close(out[tok], expect, f"token {tok}")
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_suffix_chunked_prefill_current_tiles(gpu, fused):
+    """Chunked prefill with one workspace and MIIKV_SUFFIX_TILES_CURRENT: each chunk
+    expands only its own steps (chunk sizes aligned, unaligned and short, the short
+    ones running as decodes while keeping the tiles current), and every chunk's output
+    equals a fresh call's over the same cache bit for bit, and the oracle."""
+    import miinfer_amd as m
+    rng = np.random.default_rng(77 + fused)
+    hq, hk, d, cap = 24, 4, 256, 1024
+    chunks = [64, 64, 3, 100, 64, 5, 250, 1, 96]
+    total = sum(chunks)
+    k = randn_f16(rng, (total, hk, d))
+    v = randn_f16(rng, (total, hk, d))
+    kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+    vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+    cache = m.KvCache.contiguous(hk, d, cap)
+    fresh = m.KvCache.contiguous(hk, d, cap)
+    ws = torch.empty(max(m.suffix_workspace_bytes(cache, hq, t) for t in set(chunks)), dtype=torch.uint8, device=gpu)
+    base = 0
+    for t in chunks:
+        q = randn_f16(rng, (t, hq, d))
+        kn, vn = _dev(k[base:base + t], gpu), _dev(v[base:base + t], gpu)
+        fresh.append(kn, vn, base_position=base)
+        if fused:
+            got, _ = m.suffix_attention(cache, _dev(q, gpu), base, k_new=kn, v_new=vn, workspace=ws,
+                                        tiles_current=True)
+        else:
+            cache.append(kn, vn, base_position=base)
+            got, _ = m.suffix_attention(cache, _dev(q, gpu), base, workspace=ws, tiles_current=True)
+        ref, _ = m.suffix_attention(fresh, _dev(q, gpu), base)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), (base, t, (got - ref).abs().max().item())
+        expect = oracle.suffix_attention_q8(q.astype(np.float32), kc[:, :base + t], ks[:, :base + t],
+                                            vc[:, :base + t], vs[:, :base + t], base, hq, 1 / math.sqrt(d))
+        assert_attention_close(got.cpu().numpy(), expect, f"chunk at {base}")
+        base += t
+
+
+def test_suffix_chunked_prefill_current_tiles_graph(gpu):
+    """The reference's pipeline shape: one captured suffix step (paged cache, positions
+    from a device prefill state, current tiles) replayed for successive 64-token chunks,
+    the last one shorter on the device; every replay checked against the oracle."""
+    import miinfer_amd as m
+    rng = np.random.default_rng(5)
+    hq, hk, d, pt, t = 24, 4, 256, 256, 64
+    npages = 4
+    table = _dev(rng.permutation(npages + 3)[:npages].astype(np.int32).reshape(1, npages), gpu)
+    cache = m.KvCache.paged_cache(hk, d, npages + 3, table, page_tokens=pt)
+    total = 5 * t
+    k = randn_f16(rng, (total, hk, d))
+    v = randn_f16(rng, (total, hk, d))
+    kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+    vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+    k_in = torch.zeros((t, hk, d), dtype=torch.float16, device=gpu)
+    v_in = torch.zeros_like(k_in)
+    q_in = torch.zeros((t, hq, d), dtype=torch.float16, device=gpu)
+    out = torch.zeros((t, hq, d), dtype=torch.float32, device=gpu)
+    ps = m.make_prefill_state(0, t, device=gpu)
+    ws = torch.empty(m.suffix_workspace_bytes(cache, hq, t), dtype=torch.uint8, device=gpu)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.graph(g, stream=s):
+        m.suffix_attention(cache, q_in, 0, prefill_state=ps, out=out, workspace=ws, k_new=k_in, v_new=v_in,
+                           tiles_current=True)
+    torch.cuda.synchronize()
+    base = 0
+    for n in (t, t, t, t, 37):
+        q = randn_f16(rng, (t, hq, d))
+        k_in.copy_(_dev(np.pad(k[base:base + n], ((0, t - n), (0, 0), (0, 0))), gpu))
+        v_in.copy_(_dev(np.pad(v[base:base + n], ((0, t - n), (0, 0), (0, 0))), gpu))
+        q_in.copy_(_dev(q, gpu))
+        ps[0] = base
+        ps[1] = n
+        ps[2] = base + n
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        expect = oracle.suffix_attention_q8(q[:n].astype(np.float32), kc[:, :base + n], ks[:, :base + n],
+                                            vc[:, :base + n], vs[:, :base + n], base, hq, 1 / math.sqrt(d))
+        assert_attention_close(out[:n].cpu().numpy(), expect, f"replay at {base}")
+        base += n
