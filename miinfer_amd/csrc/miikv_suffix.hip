@@ -253,6 +253,15 @@ constexpr uint32_t kDist = MIIKV_SUFFIX_DIST;
 constexpr uint32_t kSufBufs = kSufStagger ? kDist + 2 : kDist + 1;  // LDS tile buffers
 
 
+// The softmax keeps its VALU count low (v_max3 row max, v_dot2 row sum): VALU work
+// of the two waves of a SIMD hides only partly under their MFMAs.
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float max3_raw(float x, float y, float z) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(y), "v"(z));
+    return r;
+}
+
 template <uint32_t D>
 __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
     constexpr uint32_t NB = D / 32;         // PV M-tiles
@@ -379,9 +388,12 @@ __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
                 if (!(key <= lim && key < key_hi)) acc[r] = -INFINITY;
             }
         }
-        float cmax = fmaxf(acc[0], acc[1]);
-#pragma unroll
-        for (uint32_t r = 2; r < 16; r += 2) cmax = fmaxf(cmax, fmaxf(acc[r], acc[r + 1]));
+        // v_max3 straight on the MFMA results: fmaxf would first quieten each input
+        // (one more v_max per element), and the scores hold no NaN.
+        const float t0 = max3_raw(acc[0], acc[1], acc[2]), t1 = max3_raw(acc[3], acc[4], acc[5]);
+        const float t2 = max3_raw(acc[6], acc[7], acc[8]), t3 = max3_raw(acc[9], acc[10], acc[11]);
+        const float t4 = max3_raw(acc[12], acc[13], acc[14]);
+        float cmax = max3_raw(max3_raw(t0, t1, t2), max3_raw(t3, t4, acc[15]), -INFINITY);
         cmax = swap32_reduce(cmax, MaxOp{});
         const float cm = cmax * a.scale_log2;
         const bool grow = cm > m_run + kSlackS;
@@ -395,16 +407,20 @@ __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
         }
         // A row with no visible key yet keeps m_run = -inf; subtracting 0 keeps p = 0.
         const float m_use = m_run == -INFINITY ? 0.0f : m_run;
-        float lsum = 0.0f;
+        // l sums the fp16 weights the PV MFMAs use, two per v_dot2 (fp32 accumulation).
 #pragma unroll
         for (uint32_t kc = 0; kc < 2; ++kc)
 #pragma unroll
-            for (uint32_t e = 0; e < 8; ++e) {
-                const float p = sfx_exp2(fmaf(acc[8 * kc + e], a.scale_log2, -m_use));
-                lsum += p;
-                pb[kc][e] = static_cast<_Float16>(p);  // round to nearest: no bias against l_run
-            }
-        l_run += lsum;
+            for (uint32_t e = 0; e < 8; ++e)
+                pb[kc][e] = static_cast<_Float16>(sfx_exp2(fmaf(acc[8 * kc + e], a.scale_log2, -m_use)));
+        const half2v one2 = {(_Float16)1.0f, (_Float16)1.0f};
+        float ls0 = 0.0f, ls1 = 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+            ls0 = __builtin_amdgcn_fdot2(half2v{pb[0][2 * j], pb[0][2 * j + 1]}, one2, ls0, false);
+            ls1 = __builtin_amdgcn_fdot2(half2v{pb[1][2 * j], pb[1][2 * j + 1]}, one2, ls1, false);
+        }
+        l_run += ls0 + ls1;
     };
     // ---- O^T += V^T P^T of step s
     auto values = [&](uint32_t s, const half8 (&pb)[2]) __attribute__((always_inline)) {
