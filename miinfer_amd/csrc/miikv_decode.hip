@@ -349,34 +349,22 @@ __device__ void append_record(const SplitArgs& a, uint32_t b, uint32_t h, uint32
 // one-step ring (fp16 fragments take twice the registers).
 // Waves per SIMD of a decode_kernel instance: the tuned value, except q8 keys with fp16
 // values at D = 256, which need a wave's full register file (two waves spilled 122).
-// Lane n of a row of 16 takes the value of lane n + k (DPP row_shl); k <= 8.
+// Lane n of a row of 16 takes the value of lane n + K (DPP row_shl; 0 past the row).
 template <uint32_t K>
 __device__ __forceinline__ float dpp_row_shl(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x100 + K, 0xF, 0xF,
                                                                  false));
 }
-__device__ __forceinline__ float row_shl_by(float x, uint32_t k) {
-    switch (k) {
-        case 1: return dpp_row_shl<1>(x);
-        case 2: return dpp_row_shl<2>(x);
-        case 3: return dpp_row_shl<3>(x);
-        case 4: return dpp_row_shl<4>(x);
-        case 5: return dpp_row_shl<5>(x);
-        case 6: return dpp_row_shl<6>(x);
-        case 7: return dpp_row_shl<7>(x);
-        default: return dpp_row_shl<8>(x);
-    }
-}
-
 template <uint32_t D, bool QF32, bool KF16, bool VF16>
 constexpr uint32_t decode_waves_per_eu() {
     return (D == 256 && VF16 && !KF16) ? 1u : DecodeTuning<D, QF32>::waves_per_eu;
 }
 // An fp32 query is split into fp16 hi + lo parts.  QPAIR (G <= 8): the lo parts ride in
-// the QK MFMA's unused columns G..2G-1 (B operand column G + g = lo of head g), so one
-// MFMA per block carries both and the two column sums meet with one row shift per
-// score; the fp16-query register budget and occupancy then hold.  Otherwise (G > 8) the
-// lo parts are a second fragment set and a second MFMA per block.
+// the QK MFMA's unused columns 8..8+G-1 (B operand column 8 + g = lo of head g), so one
+// MFMA per block carries both and the two column sums meet with one 8-lane row shift
+// per score (a constant DPP shift); the fp16-query register budget and occupancy then
+// hold.  Otherwise (G > 8) the lo parts are a second fragment set and a second MFMA per
+// block.
 template <uint32_t D, bool QF32, bool APPEND, bool KF16 = false, bool VF16 = false, bool QPAIR = false>
 __global__ void __launch_bounds__(64 * kWavesPerWg)
 __attribute__((amdgpu_waves_per_eu(decode_waves_per_eu<D, QF32 && !QPAIR, KF16, VF16>())))
@@ -502,7 +490,7 @@ decode_kernel(SplitArgs a) {
     uint4 qraw[QF32 ? 1 : NB];
     float4 q32raw[QF32 ? NB : 1][2];
     {
-        const uint32_t qh = QPAIR && n >= G ? min(n - G, G - 1) : min(n, G - 1);
+        const uint32_t qh = QPAIR && n >= 8 ? min(n - 8, G - 1) : min(n, G - 1);
         // packed tokens (a short suffix): column qh is token pack*b + qh / Gt, head qh % Gt
         const uint32_t Gt = a.pack == 1 ? G : G / a.pack;
         const uint32_t tp = a.pack == 1 ? 0u : qh / Gt;
@@ -537,16 +525,16 @@ decode_kernel(SplitArgs a) {
             half8 v = {};
             half8 lo = {};
             float qs = 0.0f;
-            if (n < (QPAIR ? 2 * G : G)) {
+            if (n < G || (QPAIR && n >= 8 && n < 8 + G)) {
                 if constexpr (QPAIR) {
-                    // columns < G: hi parts; columns G..2G-1: lo parts of head n - G
+                    // columns < G: hi parts; columns 8..8+G-1: lo parts of head n - 8
                     const float4 x0 = q32raw[blk][0];
                     const float4 x1 = q32raw[blk][1];
                     const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
                     for (int i = 0; i < 8; ++i) {
                         const _Float16 hi = static_cast<_Float16>(xs[i]);
-                        v[i] = n < G ? hi : static_cast<_Float16>(xs[i] - static_cast<float>(hi));
+                        v[i] = n < 8 ? hi : static_cast<_Float16>(xs[i] - static_cast<float>(hi));
                         qs += static_cast<float>(v[i]);
                     }
                 } else if constexpr (QF32) {
@@ -649,7 +637,7 @@ decode_kernel(SplitArgs a) {
                 }
                 if constexpr (QPAIR) {
 #pragma unroll
-                    for (uint32_t i = 0; i < 4; ++i) c[i] += row_shl_by(c[i], G);  // + lo column
+                    for (uint32_t i = 0; i < 4; ++i) c[i] += dpp_row_shl<8>(c[i]);  // + lo column
                 }
 #pragma unroll
                 for (uint32_t i = 0; i < 4; ++i) s[J][i] = c[i] * a.scale_log2;
@@ -689,7 +677,7 @@ decode_kernel(SplitArgs a) {
             }
             if constexpr (QPAIR) {
 #pragma unroll
-                for (uint32_t i = 0; i < 4; ++i) acc[i] += row_shl_by(acc[i], G);  // + lo column
+                for (uint32_t i = 0; i < 4; ++i) acc[i] += dpp_row_shl<8>(acc[i]);  // + lo column
             }
 #pragma unroll
             for (uint32_t i = 0; i < 4; ++i) {
@@ -947,13 +935,16 @@ extern "C" miikv_status miikv_workspace_init(void* workspace, uint64_t bytes, vo
     return hip_status(hipGetLastError());
 }
 
+#ifndef MIIKV_DECODE_QPAIR
+#define MIIKV_DECODE_QPAIR 1
+#endif
 namespace {
 template <uint32_t D, bool F32, bool APP, bool KF, bool VF>
 void launch_decode_t(dim3 grid, size_t lds, hipStream_t s, const SplitArgs& a) {
     // An fp32 query of up to 8 heads per kv head pairs its lo parts into the spare columns
-    // at D = 256, where the second fragment set costs occupancy; at D = 128 the second
-    // set fits and the pairing's per-score row shift (a switch on G) measured slower.
-    if (F32 && D == 256 && 2 * a.group <= 16)
+    // (at D = 256 the second fragment set would cost occupancy; at D = 128 it doubles the
+    // score MFMAs).
+    if (F32 && a.group <= 8 && MIIKV_DECODE_QPAIR)
         hipLaunchKernelGGL((decode_kernel<D, F32, APP, KF, VF, F32>), grid, dim3(64 * kWavesPerWg), lds, s, a);
     else
         hipLaunchKernelGGL((decode_kernel<D, F32, APP, KF, VF, false>), grid, dim3(64 * kWavesPerWg), lds, s, a);
