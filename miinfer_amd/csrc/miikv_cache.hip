@@ -124,8 +124,12 @@ __device__ __forceinline__ void k_norm_rope16(float (&x)[16], const float* w, ui
     for (int i = 0; i < 16; ++i) partner[i] = dpp_mov<0x4E>(x[i]);  // lane ^ 2
     if (q16 >= 4) return;
     float angle = static_cast<float>(position);
-    const uint32_t i0 = 16 * (q16 & 1);  // first pair index of this lane
-    for (uint32_t i = 0; i < i0; ++i) angle *= step;
+    // first pair index of this lane: 0, or 16 (step applied 16 times, in order)
+#pragma unroll
+    for (uint32_t i = 0; i < 16; ++i) {
+        const float next = angle * step;
+        angle = (q16 & 1) ? next : angle;
+    }
     const bool low = q16 < 2;           // dims i (low) or i + 32 (high) of the pairs
 #pragma unroll
     for (int j = 0; j < 16; ++j) {

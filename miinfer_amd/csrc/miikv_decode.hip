@@ -248,8 +248,14 @@ __device__ void k_prologue(float& kx, float w, uint32_t tid, uint32_t position, 
     const float r = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
     kx = kx * r * w;
     if (tid < 64) {
+        // position * step * step ... ((tid & 31) factors, in that order), unrolled with
+        // selects rather than a loop whose trip count differs per lane
         float angle = static_cast<float>(position);
-        for (uint32_t i = 0; i < (tid & 31); ++i) angle *= step;
+#pragma unroll
+        for (uint32_t i = 0; i < 31; ++i) {
+            const float next = angle * step;
+            angle = i < (tid & 31) ? next : angle;
+        }
         float sn, cs;
         rope_sincos_d(angle, &sn, &cs);
         const float other = __shfl_xor(kx, 32, 64);
