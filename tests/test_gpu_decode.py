@@ -354,3 +354,31 @@ def test_decode_d256_single_sequence_plans(gpu, length, cap):
     torch.cuda.synchronize()
     expect = oracle.attention_q8(q[0].astype(np.float32), *ref, length, hq, 1 / math.sqrt(d))
     assert_attention_close(out[0].cpu().numpy(), expect, f"L={length} cap={cap}")
+
+
+# (hq, hk, d, length): 32q/8kv/D128 and 24q/4kv/D256 pair the query's lo parts into
+# spare MFMA columns; 32q/2kv/D128 (16 heads per kv head) carries them as a second
+# fragment set.
+@pytest.mark.parametrize("hq,hk,d,length", [(32, 8, 128, 3000), (24, 4, 256, 2500), (32, 2, 128, 1800)])
+def test_decode_fp32_query_low_parts_count(gpu, hq, hk, d, length):
+    """An fp32 query enters as fp16 hi + lo parts.  The attention tolerance alone would
+    not notice lost lo parts (they move the output by less than it), so: the result
+    differs from the same query rounded to fp16, and is closer to the fp32 oracle."""
+    import miinfer_amd as m
+    rng = np.random.default_rng(hq + d + length)
+    cache, ref = _filled_contiguous(gpu, rng, hk, d, ((length + 255) // 256) * 256, length)
+    q32 = (rng.standard_normal((1, hq, d)) * 3).astype(np.float32)
+    q16 = q32.astype(np.float16)
+    lens = _dev(np.array([length], np.int32), gpu)
+    scale = 2 / math.sqrt(d)  # sharper softmax: more weight on the scores
+    o32, _ = m.decode_attention(cache, _dev(q32, gpu), lengths=lens, max_context=cache.capacity, scale=scale)
+    o16, _ = m.decode_attention(cache, _dev(q16, gpu), lengths=lens, max_context=cache.capacity, scale=scale)
+    torch.cuda.synchronize()
+    o32, o16 = o32[0].cpu().numpy(), o16[0].cpu().numpy()
+    expect = oracle.attention_q8(q32[0], *ref, length, hq, scale)
+    assert_attention_close(o32, expect, "fp32 q")
+    e32 = float(np.linalg.norm(o32 - expect))
+    e16 = float(np.linalg.norm(o16 - expect))
+    print(f"hq={hq} hk={hk} d={d}: |o32-ref|={e32:.3e} |o16-ref|={e16:.3e}")
+    assert not np.array_equal(o32, o16)
+    assert e32 < 0.5 * e16, (e32, e16)

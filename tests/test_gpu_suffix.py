@@ -333,10 +333,11 @@ def test_suffix_short_packed_tokens(gpu, hq, hk, d, prefix, t):
     assert_attention_close(gated.cpu().numpy(), expect / (1 + np.exp(-gate)), "packed gated")
 
 
-# fp32 queries: 16q/4kv/D256 with 2 tokens per row set takes the paired-column
-# variant (hi parts in columns 0..7, lo parts in 8..15); 32q/8kv/D128 t=4 the
-# second fragment set.
-@pytest.mark.parametrize("hq,hk,d,prefix,t", [(16, 4, 256, 1500, 2), (16, 4, 256, 900, 4), (32, 8, 128, 2000, 4)])
+# fp32 queries: 16q/4kv/D256 and 32q/8kv/D128 with 2 tokens per row set (8 columns)
+# take the paired-column variant (hi parts in columns 0..7, lo parts in 8..15);
+# 32q/8kv/D128 t=4 (16 columns) the second fragment set.
+@pytest.mark.parametrize("hq,hk,d,prefix,t", [(16, 4, 256, 1500, 2), (16, 4, 256, 900, 4), (32, 8, 128, 2000, 4),
+                                              (32, 8, 128, 2100, 2)])
 def test_suffix_short_packed_tokens_fp32_query(gpu, hq, hk, d, prefix, t):
     import miinfer_amd as m
     rng = np.random.default_rng(prefix + 7 * t)
