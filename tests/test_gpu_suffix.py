@@ -449,3 +449,23 @@ def test_suffix_chunked_prefill_current_tiles_graph(gpu):
                                             vc[:, :base + n], vs[:, :base + n], base, hq, 1 / math.sqrt(d))
         assert_attention_close(out[:n].cpu().numpy(), expect, f"replay at {base}")
         base += n
+
+
+def test_suffix_mfma_path_rounds_fp32_query_to_fp16(gpu):
+    """The MFMA path's query operand is fp16: an fp32 query gives exactly the result of
+    the same query rounded to fp16 (a documented contract: the lo parts would need a
+    second fragment set, 64 more registers per wave than two waves per SIMD leave).
+    Short suffixes on the decode route keep the lo parts (they differ)."""
+    import miinfer_amd as m
+    hq, hk, d, prefix = 24, 4, 256, 1500
+    for t, mfma in ((96, True), (4, False)):
+        rng = np.random.default_rng(t)
+        cache, ref = _setup(gpu, rng, hq, hk, d, prefix, t, ((prefix + t + 63) // 64) * 64)
+        q32 = rng.standard_normal((t, hq, d)).astype(np.float32)
+        o32, _ = m.suffix_attention(cache, _dev(q32, gpu), prefix, out=torch.empty((t, hq, d), device=gpu))
+        o16, _ = m.suffix_attention(cache, _dev(q32.astype(np.float16), gpu), prefix,
+                                    out=torch.empty((t, hq, d), device=gpu))
+        torch.cuda.synchronize()
+        o32, o16 = o32.cpu().numpy(), o16.cpu().numpy()
+        assert np.array_equal(o32, o16) == mfma, t
+        assert_attention_close(o32, oracle.suffix_attention_q8(q32, *ref, prefix, hq, 1 / math.sqrt(d)), "fp32 q")
