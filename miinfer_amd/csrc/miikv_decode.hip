@@ -59,6 +59,9 @@ namespace {
 #ifndef MIIKV_WPE_D128
 #define MIIKV_WPE_D128 2
 #endif
+#ifndef MIIKV_RING_F16_D128
+#define MIIKV_RING_F16_D128 2
+#endif
 #ifndef MIIKV_RING_D256
 #define MIIKV_RING_D256 1
 #endif
@@ -351,8 +354,10 @@ __device__ void append_record(const SplitArgs& a, uint32_t b, uint32_t h, uint32
 
 // KF16 / VF16: the K / V plane holds fp16 rows (quant modes FP16_*, the reference's
 // control path, qwen3_wave64_splitk_stage1_f16_kernel at qwen3_primitives.hip:2198-2293):
-// the fragments are loaded as fp16 and enter the MFMAs unscaled; those variants run a
-// one-step ring (fp16 fragments take twice the registers).
+// the fragments are loaded as fp16 and enter the MFMAs unscaled.  fp16 fragments take
+// twice the registers: D = 128 runs a two-step ring at two waves per SIMD (config 2,
+// FP16_FP16: 27.4 -> 26.7 us against one step at three), D = 256 (and a second query
+// fragment set) one step.
 // Waves per SIMD of a decode_kernel instance: the tuned value, except q8 keys with fp16
 // values at D = 256, which need a wave's full register file (two waves spilled 122).
 // Lane n of a row of 16 takes the value of lane n + K (DPP row_shl; 0 past the row).
@@ -485,7 +490,7 @@ decode_kernel(SplitArgs a) {
     };
 
     // Ring of kRing step buffers; the first kRing-1 are loaded before L is known.
-    constexpr uint32_t kRing = (KF16 || VF16) ? 1u : DecodeTuning<D, kLo>::ring;
+    constexpr uint32_t kRing = (KF16 || VF16) ? (D == 128 && !kLo ? MIIKV_RING_F16_D128 : 1u) : DecodeTuning<D, kLo>::ring;
     Step S[kRing];
 #pragma unroll
     for (uint32_t r = 0; r + 1 < kRing; ++r)
