@@ -357,9 +357,11 @@ def test_decode_d256_single_sequence_plans(gpu, length, cap):
 
 
 # (hq, hk, d, length): 32q/8kv/D128 and 24q/4kv/D256 pair the query's lo parts into
-# spare MFMA columns; 32q/2kv/D128 (16 heads per kv head) carries them as a second
-# fragment set.
-@pytest.mark.parametrize("hq,hk,d,length", [(32, 8, 128, 3000), (24, 4, 256, 2500), (32, 2, 128, 1800)])
+# spare MFMA columns, as do the edges 8q/8kv (one head: columns 0 and 8) and 16q/2kv
+# (eight heads: all 16 columns); 32q/2kv/D128 (16 heads per kv head) carries them as
+# a second fragment set.
+@pytest.mark.parametrize("hq,hk,d,length", [(32, 8, 128, 3000), (24, 4, 256, 2500), (32, 2, 128, 1800),
+                                            (8, 8, 128, 2200), (16, 2, 256, 1300)])
 def test_decode_fp32_query_low_parts_count(gpu, hq, hk, d, length):
     """An fp32 query enters as fp16 hi + lo parts.  The attention tolerance alone would
     not notice lost lo parts (they move the output by less than it), so: the result
