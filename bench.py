@@ -362,6 +362,17 @@ def bench_c4(dev, args) -> int:
                                        ws_s.numel(), P(s.cuda_stream)) == 0
         short[f"T{ts}_us"] = round(sorted(_time_graph(attn_short, max(4, nrep // 24), 3, inner=8)[0]
                                           for _ in range(3))[1], 2)
+    # The exact route (MIIKV_SUFFIX_EXACT, fp32 query): every token as a decode.
+    q32 = q.float()
+    ws_x = torch.empty(m.suffix_workspace_bytes(cache, hq, t, exact=True), dtype=torch.uint8, device=dev)
+
+    def attn_exact(s):
+        assert L.miikv_suffix_attn_ex(cache.view, None, None, P(q32.data_ptr()), _lib.DTYPE_F32, hq,
+                                      ctypes.c_float(1 / math.sqrt(d)), t, prefix, 0, None, _lib.SUFFIX_EXACT,
+                                      P(out.data_ptr()), None, None, P(ws_x.data_ptr()), ws_x.numel(),
+                                      P(s.cuda_stream)) == 0
+    us_exact = sorted(_time_graph(attn_exact, max(4, nrep // 48), 3, inner=4)[0] for _ in range(3))[1]
+    del ws_x
     ladder = suffix_ladder(dev) if not getattr(args, "no_sweep", False) else None
     chunked = chunked_prefill(dev) if not getattr(args, "no_sweep", False) else None
     pairs = sum(prefix + i + 1 for i in range(t))
@@ -384,6 +395,9 @@ def bench_c4(dev, args) -> int:
                         "GBs": round(prefix * append_bytes(hkv, d) / (us_bulk * 1e-6) / 1e9, 1)},
         "short_suffix": dict(short, note="miikv_suffix_attn with T tokens over the same 8192-token prefix "
                                          "(a batch of decodes, 2 tokens per context pass)"),
+        "exact_route": {"us": round(us_exact, 2), "TFLOPs": round(flops / (us_exact * 1e-6) / 1e12, 2),
+                        "note": "miikv_suffix_attn_ex with MIIKV_SUFFIX_EXACT and an fp32 query: every token as a "
+                                "decode (the query's low half kept, block scales in fp32)"},
         "reference_ladder": ladder,
         "chunked_prefill": chunked,
     }), flush=True)

@@ -326,8 +326,23 @@ miikv_status miikv_suffix_append_attn(const miikv_view* view, const uint16_t* k_
  * base position on (instead of the whole context) and leaves its own steps current
  * for the next call, also when a short suffix runs as decodes.  One workspace per
  * (layer, sequence); a workspace of miikv_suffix_workspace_bytes() bytes suffices.
- * The first call of a sequence (base position 0) needs no earlier call. */
+ * The first call of a sequence (base position 0) needs no earlier call.
+ * MIIKV_SUFFIX_EXACT: every token runs as a decode (batches of decodes over the
+ * sequence, as short suffixes do), which keeps an fp32 query's low half and applies
+ * the block scales in fp32 -- the reference's fp32 products
+ * (qwen3_primitives.hip:6789-7207) to the decode path's precision -- where the MFMA
+ * path takes the query and the dequantised keys as fp16.  It streams the context
+ * once per row set of tokens, so it costs several times the MFMA path on long
+ * suffixes.  Needs q_heads / kv_heads <= 16 (else MIIKV_EUNSUPPORTED) and a
+ * workspace of miikv_suffix_workspace_bytes_ex(view, q_heads, token_count, flags)
+ * bytes (else MIIKV_EWORKSPACE; it never falls back to the MFMA path). */
 #define MIIKV_SUFFIX_TILES_CURRENT 1u
+#define MIIKV_SUFFIX_EXACT 2u
+/* Workspace of miikv_suffix_attn_ex with `flags`: miikv_suffix_workspace_bytes(),
+ * or more with MIIKV_SUFFIX_EXACT; 0 for invalid arguments or an unsupported
+ * geometry. */
+uint64_t miikv_suffix_workspace_bytes_ex(const miikv_view* view, uint32_t q_heads, uint32_t token_count,
+                                         uint32_t flags);
 miikv_status miikv_suffix_attn_ex(const miikv_view* view, const uint16_t* k_new, const uint16_t* v_new,
                                   const void* q, uint32_t q_dtype, uint32_t q_heads, float scale,
                                   uint32_t token_count, uint32_t base_position, uint32_t seq,

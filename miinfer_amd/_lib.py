@@ -26,6 +26,7 @@ KV_Q8_FP16 = 1
 KV_FP16_Q8 = 2
 KV_Q8_Q8 = 3
 SUFFIX_TILES_CURRENT = 1  # MIIKV_SUFFIX_TILES_CURRENT
+SUFFIX_EXACT = 2  # MIIKV_SUFFIX_EXACT
 
 DTYPE_F16 = 0
 DTYPE_F32 = 1
@@ -102,6 +103,7 @@ SIGNATURES = {
     "miikv_clone_state": (ctypes.c_int, [_P, _P, _U64, _U32, _P]),
     "miikv_stream_read": (ctypes.c_int, [_P, _U64, _P, _U32, _P]),
     "miikv_suffix_workspace_bytes": (_U64, [_VP, _U32, _U32]),
+    "miikv_suffix_workspace_bytes_ex": (_U64, [_VP, _U32, _U32, _U32]),
     "miikv_pool_create": (_P, [_U32]),
     "miikv_pool_destroy": (None, [_P]),
     "miikv_pool_alloc": (ctypes.c_int32, [_P]),

@@ -696,6 +696,20 @@ extern "C" uint64_t miikv_suffix_workspace_bytes(const miikv_view* view, uint32_
     return p.tile_bytes + std::max(dec, p.part_bytes);
 }
 
+// Exact route: the tiles (kept for MIIKV_SUFFIX_TILES_CURRENT, whose decode-route
+// records sit above them) plus the records of every token as a decode.
+extern "C" uint64_t miikv_suffix_workspace_bytes_ex(const miikv_view* view, uint32_t q_heads, uint32_t token_count,
+                                                    uint32_t flags) {
+    if ((flags & ~(MIIKV_SUFFIX_TILES_CURRENT | MIIKV_SUFFIX_EXACT)) != 0) return 0;
+    const uint64_t base = miikv_suffix_workspace_bytes(view, q_heads, token_count);
+    if (base == 0 || (flags & MIIKV_SUFFIX_EXACT) == 0) return base;
+    if (!decode_columns_fit(q_heads / view->kv_heads, view->head_dim)) return 0;
+    const uint64_t cap = view_seq_capacity(view);
+    const SuffixPlan tiles = make_suffix_plan(view, q_heads, token_count, cap, false);
+    const uint32_t cap32 = static_cast<uint32_t>(std::min<uint64_t>(cap, 0xffffffffu));
+    return std::max(base, tiles.tile_bytes + suffix_by_decode_bytes(view, q_heads, token_count, cap32));
+}
+
 static miikv_status suffix_impl(const miikv_view* view, const uint16_t* k_new, const uint16_t* v_new, const void* q,
                                 uint32_t q_dtype, uint32_t q_heads, float scale, uint32_t token_count,
                                 uint32_t base_position, uint32_t seq, const miikv_prefill_state* prefill_state,
@@ -709,8 +723,10 @@ static miikv_status suffix_impl(const miikv_view* view, const uint16_t* k_new, c
     if (out == nullptr && !(gate != nullptr && gated_out != nullptr)) return MIIKV_EINVAL;
     if ((gate == nullptr) != (gated_out == nullptr)) return MIIKV_EINVAL;
     if (view->layout == MIIKV_LAYOUT_CONTIGUOUS && seq != 0) return MIIKV_EINVAL;
-    if ((flags & ~MIIKV_SUFFIX_TILES_CURRENT) != 0) return MIIKV_EINVAL;
+    if ((flags & ~(MIIKV_SUFFIX_TILES_CURRENT | MIIKV_SUFFIX_EXACT)) != 0) return MIIKV_EINVAL;
     const bool current = (flags & MIIKV_SUFFIX_TILES_CURRENT) != 0;
+    const bool exact = (flags & MIIKV_SUFFIX_EXACT) != 0;
+    if (exact && !decode_columns_fit(G, view->head_dim)) return MIIKV_EUNSUPPORTED;
     if (token_count == 0) return MIIKV_OK;
     if (k_new != nullptr && view->quant_mode != MIIKV_KV_Q8_Q8) return MIIKV_EUNSUPPORTED;  // stores q8 rows
     const uint64_t cap = view_seq_capacity(view);
@@ -758,8 +774,10 @@ static miikv_status suffix_impl(const miikv_view* view, const uint16_t* k_new, c
     // (a workspace sized for the MFMA path alone runs that path)
     const SuffixPlan tile_plan = make_suffix_plan(view, q_heads, token_count, bound, false, stride_bound);
     const uint64_t dec_off = current ? tile_plan.tile_bytes : 0;  // the tiles stay below the records
-    if (suffix_runs_as_decode(view, q_heads, token_count, prefill_state != nullptr) &&
-        workspace_bytes >= dec_off + suffix_by_decode_bytes(view, q_heads, token_count, bound32)) {
+    const bool by_decode = exact || suffix_runs_as_decode(view, q_heads, token_count, prefill_state != nullptr);
+    const bool dec_fits = workspace_bytes >= dec_off + suffix_by_decode_bytes(view, q_heads, token_count, bound32);
+    if (exact && !dec_fits) return MIIKV_EWORKSPACE;
+    if (by_decode && dec_fits) {
         // the suffix's own rows first; every token then reads its context from the cache
         if (k_new != nullptr) {
             const miikv_status ast = miikv_append_f16(view, k_new, v_new, token_count, base_position, seq,

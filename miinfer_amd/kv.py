@@ -410,7 +410,8 @@ def suffix_attention(cache: KvCache, q: torch.Tensor, base_position: int, scale:
                      gate: torch.Tensor | None = None, out: torch.Tensor | None = None,
                      gated_out: torch.Tensor | None = None, split: bool = True,
                      k_new: torch.Tensor | None = None, v_new: torch.Tensor | None = None,
-                     workspace: torch.Tensor | None = None, tiles_current: bool = False, stream=None):
+                     workspace: torch.Tensor | None = None, tiles_current: bool = False, exact: bool = False,
+                     stream=None):
     """Causal attention of a T-token suffix (rows already appended at base_position..)
     over the cache.  q: [T, q_heads, head_dim] fp16/fp32.  Returns (out, gated_out).
     With k_new / v_new (fp16 [T, kv_heads, head_dim]) the suffix's rows are quantised
@@ -423,7 +424,12 @@ def suffix_attention(cache: KvCache, q: torch.Tensor, base_position: int, scale:
     tiles_current (chunked prefill, with the same `workspace` for every chunk of one
     sequence and layer): the workspace's tiles of the keys below the base position
     are current from earlier calls, so only the new steps are expanded
-    (MIIKV_SUFFIX_TILES_CURRENT)."""
+    (MIIKV_SUFFIX_TILES_CURRENT).
+
+    exact (MIIKV_SUFFIX_EXACT): every token runs as a decode, keeping an fp32 query's
+    low half and applying the block scales in fp32, instead of the MFMA path's fp16
+    query and tiles; it streams the context once per row set of tokens (slower on
+    long suffixes) and needs suffix_workspace_bytes(..., exact=True)."""
     t, q_heads, d = q.shape
     if d != cache.head_dim or not q.is_contiguous() or q.dtype not in (torch.float16,
                                                                         torch.float32):
@@ -444,8 +450,8 @@ def suffix_attention(cache: KvCache, q: torch.Tensor, base_position: int, scale:
         if gate is not None and gated_out is None:
             gated_out = torch.empty((t, q_heads, d), dtype=torch.float32, device=q.device)
         if workspace is None:
-            if split:
-                need = suffix_workspace_bytes(cache, q_heads, t)
+            if split or exact:
+                need = suffix_workspace_bytes(cache, q_heads, t, exact=exact)
             else:
                 bound = cache.capacity if prefill_state is not None else base_position + t
                 need = cache.kv_heads * ((bound + 31) // 32) * 2 * d * 32 * 2
@@ -458,9 +464,10 @@ def suffix_attention(cache: KvCache, q: torch.Tensor, base_position: int, scale:
             if tns.dtype != torch.float16 or tuple(tns.shape) != (t, cache.kv_heads, d) or \
                     not tns.is_contiguous():
                 raise ValueError("k_new/v_new must be contiguous fp16 [T, kv_heads, head_dim]")
-    if tiles_current:
+    if tiles_current or exact:
+        flags = (_lib.SUFFIX_TILES_CURRENT if tiles_current else 0) | (_lib.SUFFIX_EXACT if exact else 0)
         call("miikv_suffix_attn_ex", cache.view, _ptr(k_new), _ptr(v_new), _ptr(q), qd, q_heads, float(scale), t,
-             base_position, seq, _ptr(prefill_state), _lib.SUFFIX_TILES_CURRENT, _ptr(out), _ptr(gate),
+             base_position, seq, _ptr(prefill_state), flags, _ptr(out), _ptr(gate),
              _ptr(gated_out), _ptr(workspace), ws_bytes, _stream(stream))
         return out, gated_out
     if k_new is not None:
@@ -474,7 +481,9 @@ def suffix_attention(cache: KvCache, q: torch.Tensor, base_position: int, scale:
     return out, gated_out
 
 
-def suffix_workspace_bytes(cache: KvCache, q_heads: int, tokens: int) -> int:
+def suffix_workspace_bytes(cache: KvCache, q_heads: int, tokens: int, exact: bool = False) -> int:
+    if exact:
+        return int(lib().miikv_suffix_workspace_bytes_ex(cache.view, q_heads, tokens, _lib.SUFFIX_EXACT))
     return int(lib().miikv_suffix_workspace_bytes(cache.view, q_heads, tokens))
 
 

@@ -189,3 +189,23 @@ def test_decode_state_advance_rejects_before_launch():
     assert lib.miikv_decode_state_advance(None, None, 0, None, 0, None) == L.MIIKV_EINVAL
     assert lib.miikv_decode_state_advance(p, None, 0, stops, 9, None) == L.MIIKV_EINVAL
     assert lib.miikv_decode_state_advance(p, None, 0, None, 2, None) == L.MIIKV_EINVAL
+
+
+def test_suffix_workspace_bytes_ex():
+    """With MIIKV_SUFFIX_EXACT the workspace holds the tiles plus every token's decode
+    records (at least the plain size); the flag needs <= 16 query heads per kv head;
+    unknown flags give 0."""
+    L = _lib()
+    lib = L.lib()
+    v = _view(page_tokens=8704, kv_heads=4, head_dim=256)
+    base = lib.miikv_suffix_workspace_bytes(ctypes.byref(v), 24, 512)
+    assert lib.miikv_suffix_workspace_bytes_ex(ctypes.byref(v), 24, 512, 0) == base
+    assert lib.miikv_suffix_workspace_bytes_ex(ctypes.byref(v), 24, 512, L.SUFFIX_TILES_CURRENT) == base
+    ex = lib.miikv_suffix_workspace_bytes_ex(ctypes.byref(v), 24, 512, L.SUFFIX_EXACT)
+    tiles = 4 * (8704 // 32) * 2 * 256 * 32 * 2
+    assert ex >= base and ex > tiles
+    assert lib.miikv_suffix_workspace_bytes_ex(ctypes.byref(v), 24, 512, L.SUFFIX_EXACT | L.SUFFIX_TILES_CURRENT) == ex
+    assert lib.miikv_suffix_workspace_bytes_ex(ctypes.byref(v), 24, 512, 4) == 0
+    wide = _view(page_tokens=1024, kv_heads=1, head_dim=128)
+    assert lib.miikv_suffix_workspace_bytes_ex(ctypes.byref(wide), 32, 64, L.SUFFIX_EXACT) == 0  # 32 heads per kv head
+    assert lib.miikv_suffix_workspace_bytes_ex(ctypes.byref(wide), 32, 64, 0) > 0

@@ -367,14 +367,16 @@ def test_suffix_64k_prefix_sampled_tokens(gpu, split):
         assert_attention_close(out[tok], expect, f"token {tok}")
 
 
-@pytest.mark.parametrize("fused", [False, True])
-def test_suffix_chunked_prefill_current_tiles(gpu, fused):
+@pytest.mark.parametrize("fused,exact", [(False, False), (True, False), (False, True)])
+def test_suffix_chunked_prefill_current_tiles(gpu, fused, exact):
     """Chunked prefill with one workspace and MIIKV_SUFFIX_TILES_CURRENT: each chunk
     expands only its own steps (chunk sizes aligned, unaligned and short, the short
     ones running as decodes while keeping the tiles current), and every chunk's output
-    equals a fresh call's over the same cache bit for bit, and the oracle."""
+    equals a fresh call's over the same cache bit for bit, and the oracle.  With
+    `exact`, odd chunks run with MIIKV_SUFFIX_EXACT (as decodes) and must still leave
+    the tiles current for the MFMA chunks after them."""
     import miinfer_amd as m
-    rng = np.random.default_rng(77 + fused)
+    rng = np.random.default_rng(77 + fused + 2 * exact)
     hq, hk, d, cap = 24, 4, 256, 1024
     chunks = [64, 64, 3, 100, 64, 5, 250, 1, 96]
     total = sum(chunks)
@@ -384,9 +386,11 @@ def test_suffix_chunked_prefill_current_tiles(gpu, fused):
     vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
     cache = m.KvCache.contiguous(hk, d, cap)
     fresh = m.KvCache.contiguous(hk, d, cap)
-    ws = torch.empty(max(m.suffix_workspace_bytes(cache, hq, t) for t in set(chunks)), dtype=torch.uint8, device=gpu)
+    ws = torch.empty(max(m.suffix_workspace_bytes(cache, hq, t, exact=exact) for t in set(chunks)),
+                     dtype=torch.uint8, device=gpu)
     base = 0
-    for t in chunks:
+    for i, t in enumerate(chunks):
+        ex = exact and i % 2 == 1
         q = randn_f16(rng, (t, hq, d))
         kn, vn = _dev(k[base:base + t], gpu), _dev(v[base:base + t], gpu)
         fresh.append(kn, vn, base_position=base)
@@ -395,8 +399,8 @@ def test_suffix_chunked_prefill_current_tiles(gpu, fused):
                                         tiles_current=True)
         else:
             cache.append(kn, vn, base_position=base)
-            got, _ = m.suffix_attention(cache, _dev(q, gpu), base, workspace=ws, tiles_current=True)
-        ref, _ = m.suffix_attention(fresh, _dev(q, gpu), base)
+            got, _ = m.suffix_attention(cache, _dev(q, gpu), base, workspace=ws, tiles_current=True, exact=ex)
+        ref, _ = m.suffix_attention(fresh, _dev(q, gpu), base, exact=ex)
         torch.cuda.synchronize()
         assert torch.equal(got, ref), (base, t, (got - ref).abs().max().item())
         expect = oracle.suffix_attention_q8(q.astype(np.float32), kc[:, :base + t], ks[:, :base + t],
@@ -469,3 +473,62 @@ def test_suffix_mfma_path_rounds_fp32_query_to_fp16(gpu):
         o32, o16 = o32.cpu().numpy(), o16.cpu().numpy()
         assert np.array_equal(o32, o16) == mfma, t
         assert_attention_close(o32, oracle.suffix_attention_q8(q32, *ref, prefix, hq, 1 / math.sqrt(d)), "fp32 q")
+
+
+# (t, q fp32, fused store + gate, device prefill state)
+@pytest.mark.parametrize("t,f32,fused,dev_state", [(96, True, False, False), (512, True, False, False),
+                                                   (100, True, True, False), (70, False, False, True),
+                                                   (7, True, False, False)])
+def test_suffix_exact_route(gpu, t, f32, fused, dev_state):
+    """MIIKV_SUFFIX_EXACT runs every token as a decode: the fp32 query's low half and
+    the block scales in fp32 keep sharp attention (queries x3, scale x2, logits of
+    standard deviation ~6) within the attention tolerance, where the MFMA path's fp16
+    query and tiles do not; with the fused store, a gate and a device prefill state."""
+    import miinfer_amd as m
+    hq, hk, d, prefix = 24, 4, 256, 1500
+    rng = np.random.default_rng(t + 3 * fused)
+    cap = ((prefix + t + 255) // 256) * 256
+    k = randn_f16(rng, (prefix + t, hk, d))
+    v = randn_f16(rng, (prefix + t, hk, d))
+    kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+    vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+    cache = m.KvCache.contiguous(hk, d, cap)
+    cache.append(_dev(k[:prefix], gpu), _dev(v[:prefix], gpu), base_position=0)
+    kn, vn = _dev(k[prefix:], gpu), _dev(v[prefix:], gpu)
+    if not fused:
+        cache.append(kn, vn, base_position=prefix)
+    q = (rng.standard_normal((t, hq, d)) * 3).astype(np.float32 if f32 else np.float16)
+    gate = rng.standard_normal((t, hq, d)).astype(np.float32)
+    scale = 2 / math.sqrt(d)
+    ps = m.make_prefill_state(prefix, t, cap, device=gpu) if dev_state else None
+    kw = dict(k_new=kn, v_new=vn) if fused else {}
+    out, gated = m.suffix_attention(cache, _dev(q, gpu), prefix, scale, prefill_state=ps, gate=_dev(gate, gpu),
+                                    out=torch.empty((t, hq, d), device=gpu), exact=True, **kw)
+    torch.cuda.synchronize()
+    expect = oracle.suffix_attention_q8(q.astype(np.float32), kc, ks, vc, vs, prefix, hq, scale)
+    assert_attention_close(out.cpu().numpy(), expect, "exact")
+    assert_attention_close(gated.cpu().numpy(), expect / (1 + np.exp(-gate)), "exact gated")
+    if fused:  # the rows were stored with the append rule
+        got_kc, got_ks, _, _ = cache.export_canonical(0, prefix, t)
+        torch.cuda.synchronize()
+        assert np.array_equal(got_kc.cpu().numpy(), kc[:, prefix:])
+        assert np.array_equal(got_ks.cpu().numpy().view(np.uint16), ks[:, prefix:])
+
+
+def test_suffix_exact_route_errors(gpu):
+    import miinfer_amd as m
+    from miinfer_amd import _lib
+    cache = m.KvCache.contiguous(1, 128, 1024)
+    cache.append(_dev(np.zeros((600, 1, 128), np.float16), gpu), _dev(np.zeros((600, 1, 128), np.float16), gpu))
+    q = torch.zeros((64, 32, 128), device=gpu)  # 32 query heads per kv head: no decode layout
+    with pytest.raises(_lib.MiikvError) as err:
+        m.suffix_attention(cache, q, 536, exact=True, workspace=torch.empty(1 << 26, dtype=torch.uint8, device=gpu))
+    assert err.value.status == _lib.MIIKV_EUNSUPPORTED
+    c4 = m.KvCache.contiguous(4, 256, 1024)
+    c4.append(_dev(np.zeros((600, 4, 256), np.float16), gpu), _dev(np.zeros((600, 4, 256), np.float16), gpu))
+    q4 = torch.zeros((64, 24, 256), device=gpu)
+    small = torch.empty(m.suffix_workspace_bytes(c4, 24, 64), dtype=torch.uint8, device=gpu)
+    assert m.suffix_workspace_bytes(c4, 24, 64, exact=True) > small.numel()
+    with pytest.raises(_lib.MiikvError) as err:  # never falls back to the MFMA path
+        m.suffix_attention(c4, q4, 536, exact=True, workspace=small)
+    assert err.value.status == _lib.MIIKV_EWORKSPACE
