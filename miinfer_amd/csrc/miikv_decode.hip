@@ -878,7 +878,8 @@ struct Plan {
     uint64_t part_bytes;
 };
 
-Plan make_plan(const miikv_view* v, uint32_t q_heads, uint32_t batch, uint32_t max_context) {
+Plan make_plan(const miikv_view* v, uint32_t q_heads, uint32_t batch, uint32_t max_context,
+               uint32_t cpw_cap = 64) {
     Plan p;
     const uint64_t chunks = (static_cast<uint64_t>(max_context) + kChunk - 1) / kChunk;
     const uint64_t waves = chunks * v->kv_heads * batch;
@@ -902,7 +903,7 @@ Plan make_plan(const miikv_view* v, uint32_t q_heads, uint32_t batch, uint32_t m
     p.adaptive = batch > 1 && fixed_cpw == 0;
     if (fixed_cpw != 0) cpw = fixed_cpw;
     if (cpw < 1) cpw = 1;
-    if (cpw > 64) cpw = 64;
+    if (cpw > cpw_cap) cpw = cpw_cap;
     p.cpw = static_cast<uint32_t>(cpw);
     const uint64_t tps = kWavesPerWg * cpw * kChunk;
     p.splits = static_cast<uint32_t>((static_cast<uint64_t>(max_context) + tps - 1) / tps);
@@ -946,6 +947,10 @@ extern "C" miikv_status miikv_workspace_init(void* workspace, uint64_t bytes, vo
     return hip_status(hipGetLastError());
 }
 
+#ifndef MIIKV_ROWSET_MAX_CPW
+#define MIIKV_ROWSET_MAX_CPW 32
+#endif
+constexpr uint32_t kRowsetMaxCpw = MIIKV_ROWSET_MAX_CPW;
 #ifndef MIIKV_DECODE_QPAIR
 #define MIIKV_DECODE_QPAIR 1
 #endif
@@ -1041,7 +1046,7 @@ static miikv_status decode_impl(const miikv_view* view, const NewRows& rows,
     if (rows.any() && view->quant_mode != MIIKV_KV_Q8_Q8) return MIIKV_EUNSUPPORTED;
     if (rows.k_norm_weight != nullptr && (!std::isfinite(rows.theta) || !std::isfinite(rows.epsilon)))
         return MIIKV_EINVAL;
-    const Plan p = make_plan(view, q_heads * pack, batch, max_context);
+    const Plan p = make_plan(view, q_heads * pack, batch, max_context, rs != nullptr ? kRowsetMaxCpw : 64u);
     if (workspace == nullptr || workspace_bytes < p.counter_bytes + p.part_bytes) return MIIKV_EWORKSPACE;
     if (p.splits > 65535u || batch > 65535u || static_cast<uint64_t>(batch) * view->kv_heads > 0x7fffffffu)
         return MIIKV_EINVAL;
@@ -1055,6 +1060,12 @@ static miikv_status decode_impl(const miikv_view* view, const NewRows& rows,
     a.scale_log2 = scale * kLog2e;
     a.len_bstep = 0;
     a.count_ptr = nullptr;
+    // Row sets of one sequence all read the same keys: with long items the workgroups
+    // running at once stream the same addresses together, so the row-set route caps
+    // the steps per wave lower (host plan and device choice alike: the records are
+    // sized for the host's floor; exact suffix route at config 4: 1372 us at 64,
+    // 1000 at 32, 1055 at 16); decode batches of distinct sequences keep 64.
+    a.max_cpw = rs != nullptr ? kRowsetMaxCpw : 64u;
     if (rs != nullptr) {  // row set b: len_add + b * pack (its last token's context)
         a.len_ptr = rs->len_ptr;
         a.len_stride = 0;
@@ -1143,8 +1154,8 @@ uint32_t suffix_pack(const miikv_view* view, uint32_t q_heads, uint32_t token_co
 uint64_t suffix_by_decode_bytes(const miikv_view* view, uint32_t q_heads, uint32_t token_count, uint32_t bound) {
     // the larger of the packed (host token count) and unpacked (device count) plans
     const uint32_t pk = suffix_pack(view, q_heads, token_count, false);
-    const Plan p1 = make_plan(view, q_heads, token_count, bound);
-    const Plan pp = make_plan(view, q_heads * pk, token_count / pk, bound);
+    const Plan p1 = make_plan(view, q_heads, token_count, bound, kRowsetMaxCpw);
+    const Plan pp = make_plan(view, q_heads * pk, token_count / pk, bound, kRowsetMaxCpw);
     return std::max(p1.counter_bytes + p1.part_bytes, pp.counter_bytes + pp.part_bytes);
 }
 

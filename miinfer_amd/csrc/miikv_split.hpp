@@ -33,6 +33,7 @@ struct SplitArgs {
     uint32_t cpw;         // chunks per wave
     uint32_t max_splits;  // splits per (sequence, kv head)
     uint32_t batch;       // sequences (row-sets)
+    uint32_t max_cpw;     // cap of the device-side steps per wave
     // batch > 1: resident workgroups of the split kernel; the steps per wave are
     // then chosen on the device from the lengths (at least cpw), 0: always cpw
     uint32_t slots;
@@ -92,7 +93,7 @@ __device__ uint32_t launch_cpw(const SplitArgs& a) {
     const unsigned long long room = a.slots > fixed_items ? a.slots - fixed_items : a.slots;
     const unsigned long long per = static_cast<unsigned long long>(kWavesPerWg) * kChunk * room;
     const unsigned long long cpw = (total + per - 1) / per;
-    return static_cast<uint32_t>(cpw < a.cpw ? a.cpw : (cpw > 64 ? 64 : cpw));
+    return static_cast<uint32_t>(cpw < a.cpw ? a.cpw : (cpw > a.max_cpw ? a.max_cpw : cpw));
 }
 
 // Split count of sequence b at `cpw` steps per wave (0 when L == 0).
