@@ -947,6 +947,9 @@ extern "C" miikv_status miikv_workspace_init(void* workspace, uint64_t bytes, vo
     return hip_status(hipGetLastError());
 }
 
+#ifndef MIIKV_NARROW_COMBINE
+#define MIIKV_NARROW_COMBINE 1
+#endif
 #ifndef MIIKV_ROWSET_MAX_CPW
 #define MIIKV_ROWSET_MAX_CPW 32
 #endif
@@ -1114,8 +1117,12 @@ static miikv_status decode_impl(const miikv_view* view, const NewRows& rows,
     const dim3 grid(static_cast<uint32_t>(wgs));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool f32 = q_dtype == MIIKV_DTYPE_F32;
-    // combine: one workgroup per (sequence, kv head, 32 output elements)
+    // combine: one workgroup per (sequence, kv head, 32 output elements), or, with at
+    // most kNarrowRecords records per row set, one thread per 4 output elements
     const dim3 cgrid(batch * view->kv_heads, G * view->head_dim / 32);
+    const bool narrow = p.splits + 1 <= kNarrowRecords && MIIKV_NARROW_COMBINE;
+    const uint64_t nthreads = static_cast<uint64_t>(batch) * view->kv_heads * G * view->head_dim / 4;
+    const dim3 ngrid(static_cast<uint32_t>((nthreads + 255) / 256));
     const bool app = rows.any();
     const bool kf = mode_k_f16(view->quant_mode), vf = mode_v_f16(view->quant_mode);
     if (view->head_dim == 128) {
@@ -1123,11 +1130,15 @@ static miikv_status decode_impl(const miikv_view* view, const NewRows& rows,
 #ifdef MIIKV_EXP_NO_COMBINE
         return hip_status(hipGetLastError());
 #endif
-        if (app) hipLaunchKernelGGL((combine_kernel<128, true>), cgrid, dim3(256), 0, s, a);
+        if (narrow && app) hipLaunchKernelGGL((combine_narrow_kernel<128, true>), ngrid, dim3(256), 0, s, a);
+        else if (narrow) hipLaunchKernelGGL((combine_narrow_kernel<128, false>), ngrid, dim3(256), 0, s, a);
+        else if (app) hipLaunchKernelGGL((combine_kernel<128, true>), cgrid, dim3(256), 0, s, a);
         else hipLaunchKernelGGL((combine_kernel<128, false>), cgrid, dim3(256), 0, s, a);
     } else {
         launch_decode<256>(f32, app, kf, vf, grid, lds, s, a);
-        if (app) hipLaunchKernelGGL((combine_kernel<256, true>), cgrid, dim3(256), 0, s, a);
+        if (narrow && app) hipLaunchKernelGGL((combine_narrow_kernel<256, true>), ngrid, dim3(256), 0, s, a);
+        else if (narrow) hipLaunchKernelGGL((combine_narrow_kernel<256, false>), ngrid, dim3(256), 0, s, a);
+        else if (app) hipLaunchKernelGGL((combine_kernel<256, true>), cgrid, dim3(256), 0, s, a);
         else hipLaunchKernelGGL((combine_kernel<256, false>), cgrid, dim3(256), 0, s, a);
     }
     return hip_status(hipGetLastError());

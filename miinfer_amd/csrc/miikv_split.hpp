@@ -130,6 +130,52 @@ __device__ __forceinline__ void merge_state(float& m, float& l, float4& acc, flo
     acc.w = acc.w * f1 + a2.w * f2;
 }
 
+// Output of 4 merged elements e..e+3 (thread q of the 8 holding a 32-value block that
+// starts at element blk0 of the launch's rows): out = acc / L, 0 when L == 0
+// (qwen3_primitives.hip:2349); gated = out * sigmoid(gate); the Q8_1 block.  All 8
+// threads of a block call it (the block's reductions); `live` = false computes but
+// stores nothing.
+__device__ __forceinline__ void combine_emit(const SplitArgs& a, size_t out_row0, uint32_t e, uint32_t q, size_t blk0,
+                                             float l, float4 acc, const float (&gv)[4], bool live) {
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const float vals[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
+    float gated[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (a.out && live) *reinterpret_cast<float4*>(a.out + out_row0 + e) = make_float4(vals[0], vals[1], vals[2], vals[3]);
+    if (a.gate) {
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k) gated[k] = vals[k] * (1.0f / (1.0f + expf(-gv[k])));
+        if (a.gated_out && live)
+            *reinterpret_cast<float4*>(a.gated_out + out_row0 + e) = make_float4(gated[0], gated[1], gated[2], gated[3]);
+    }
+    if (a.gate && a.gated_q8_1) {
+        // Q8_1 block of these 32 gated values (qwen3_primitives.hip:2354-2384):
+        // d = amax/127, q = clamp(roundf(x/d), -127, 127), s = sum(q)*d.
+        float amax = fmaxf(fmaxf(fabsf(gated[0]), fabsf(gated[1])), fmaxf(fabsf(gated[2]), fabsf(gated[3])));
+        amax = group_reduce<8>(amax, MaxOp{});
+        const float d = amax / 127.0f;
+        const float qinv = d != 0.0f ? 1.0f / d : 0.0f;
+        int qs[4];
+        int sum = 0;
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k) {
+            qs[k] = max(-127, min(127, static_cast<int>(roundf(gated[k] * qinv))));
+            sum += qs[k];
+        }
+        sum = group_reduce<8>(sum, AddOp{});
+        if (!live) return;
+        const size_t blk = (out_row0 + blk0) / 32;
+        uint8_t* bp = a.gated_q8_1 + blk * 36;
+        *reinterpret_cast<uint32_t*>(bp + 4 + 4 * q) =
+            (static_cast<uint32_t>(qs[0]) & 0xffu) | ((static_cast<uint32_t>(qs[1]) & 0xffu) << 8) |
+            ((static_cast<uint32_t>(qs[2]) & 0xffu) << 16) | ((static_cast<uint32_t>(qs[3]) & 0xffu) << 24);
+        if (q == 0) {
+            *reinterpret_cast<uint16_t*>(bp) = f32_to_f16_bits(d);
+            *reinterpret_cast<uint16_t*>(bp + 2) = f32_to_f16_bits(static_cast<float>(sum) * d);
+        }
+    }
+}
+
+
 template <uint32_t D, bool APPEND>
 __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
     const uint32_t bh = blockIdx.x;
@@ -208,42 +254,64 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
     if (tid >= 8) return;
 #pragma unroll
     for (uint32_t w = 1; w < 4; ++w) merge_state(m, l, acc, s_m[w][q], s_l[w][q], s_acc[w][q]);
-    // out = acc / L, 0 when L == 0 (qwen3_primitives.hip:2349); gated = out * sigmoid(gate).
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    const float vals[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
-    float gated[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (a.out) *reinterpret_cast<float4*>(a.out + out_row0 + e) = make_float4(vals[0], vals[1], vals[2], vals[3]);
-    if (a.gate) {
-#pragma unroll
-        for (uint32_t k = 0; k < 4; ++k) gated[k] = vals[k] * (1.0f / (1.0f + expf(-gv[k])));
-        if (a.gated_out)
-            *reinterpret_cast<float4*>(a.gated_out + out_row0 + e) = make_float4(gated[0], gated[1], gated[2], gated[3]);
+    combine_emit(a, out_row0, e, q, blockIdx.y * 32, l, acc, gv, true);
+}
+
+
+// Cross-split combine for launches with few records per row set (the host's bound,
+// max_splits + 1 <= kNarrowRecords: the row-set route of long suffixes): one thread per
+// 4 consecutive outputs of one (row set, kv head) folds all of that row set's records
+// itself, so the grid is one thread per 4 outputs instead of a 256-thread workgroup
+// per 32; 8 consecutive threads hold one 32-value block (Q8_1 epilogue).
+constexpr uint32_t kNarrowRecords = 8;
+template <uint32_t D, bool APPEND>
+__global__ void __launch_bounds__(256) combine_narrow_kernel(SplitArgs a) {
+    const uint32_t G = a.group;
+    const uint32_t GD = G * D;
+    const uint32_t cpw = launch_cpw(a);  // every thread of the workgroup takes part
+    const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const uint64_t per = GD / 4;
+    const uint32_t bh = static_cast<uint32_t>(idx / per);
+    const bool live = bh < a.batch * a.g.kv_heads;
+    const uint32_t bhc = live ? bh : 0;
+    const uint32_t b = bhc / a.g.kv_heads;
+    const uint32_t h = bhc % a.g.kv_heads;
+    const uint32_t e = static_cast<uint32_t>(idx % per) * 4;
+    const uint32_t q = (e / 4) & 7;
+    const uint32_t hn = e / D;
+    const uint32_t Gt = G / a.pack, tp = hn / Gt;
+    const size_t out_row0 = ((static_cast<size_t>(b) * a.pack + tp) * a.q_heads + static_cast<size_t>(h) * Gt +
+                             (hn - tp * Gt)) * D - static_cast<size_t>(hn) * D;
+    const uint32_t rec = record_floats(G, D);
+    const float* part = a.part + (static_cast<size_t>(bhc) * (a.max_splits + 1)) * rec;
+    float gv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (a.gate != nullptr) {
+        const float4 g4 = *reinterpret_cast<const float4*>(a.gate + out_row0 + e);
+        gv[0] = g4.x; gv[1] = g4.y; gv[2] = g4.z; gv[3] = g4.w;
     }
-    if (a.gate && a.gated_q8_1) {
-        // Q8_1 block of these 32 gated values (qwen3_primitives.hip:2354-2384):
-        // d = amax/127, q = clamp(roundf(x/d), -127, 127), s = sum(q)*d.
-        float amax = fmaxf(fmaxf(fabsf(gated[0]), fabsf(gated[1])), fmaxf(fabsf(gated[2]), fabsf(gated[3])));
-        amax = group_reduce<8>(amax, MaxOp{});
-        const float d = amax / 127.0f;
-        const float qinv = d != 0.0f ? 1.0f / d : 0.0f;
-        int qs[4];
-        int sum = 0;
+    // a whole 32-value block shares b (GD is a multiple of 32), so the 8 threads of a
+    // block take the same exit
+    if (a.count_ptr != nullptr && b >= *a.count_ptr) return;
+    const uint32_t L = split_length(a, b);
+    const uint32_t nrec = split_count(L, cpw) + (APPEND && L > 0 ? 1u : 0u);
+    float m = -INFINITY, l = 0.0f;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float ms[kNarrowRecords], ls[kNarrowRecords];
+    float4 vv[kNarrowRecords];
 #pragma unroll
-        for (uint32_t k = 0; k < 4; ++k) {
-            qs[k] = max(-127, min(127, static_cast<int>(roundf(gated[k] * qinv))));
-            sum += qs[k];
-        }
-        sum = group_reduce<8>(sum, AddOp{});
-        const size_t blk = (out_row0 + blockIdx.y * 32) / 32;
-        uint8_t* bp = a.gated_q8_1 + blk * 36;
-        *reinterpret_cast<uint32_t*>(bp + 4 + 4 * q) =
-            (static_cast<uint32_t>(qs[0]) & 0xffu) | ((static_cast<uint32_t>(qs[1]) & 0xffu) << 8) |
-            ((static_cast<uint32_t>(qs[2]) & 0xffu) << 16) | ((static_cast<uint32_t>(qs[3]) & 0xffu) << 24);
-        if (q == 0) {
-            *reinterpret_cast<uint16_t*>(bp) = f32_to_f16_bits(d);
-            *reinterpret_cast<uint16_t*>(bp + 2) = f32_to_f16_bits(static_cast<float>(sum) * d);
+    for (uint32_t sp = 0; sp < kNarrowRecords; ++sp) {  // all loads before the first merge
+        ms[sp] = -INFINITY;
+        if (sp < nrec) {
+            const float* r = part + static_cast<size_t>(sp) * rec;
+            ms[sp] = r[GD + hn];
+            ls[sp] = r[GD + G + hn];
+            vv[sp] = *reinterpret_cast<const float4*>(r + e);
         }
     }
+#pragma unroll
+    for (uint32_t sp = 0; sp < kNarrowRecords; ++sp)
+        if (sp < nrec) merge_state(m, l, acc, ms[sp], ls[sp], vv[sp]);
+    combine_emit(a, out_row0, e, q, e - 4 * q, l, acc, gv, live);
 }
 
 }  // namespace
