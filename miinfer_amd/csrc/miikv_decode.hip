@@ -950,6 +950,9 @@ extern "C" miikv_status miikv_workspace_init(void* workspace, uint64_t bytes, vo
 #ifndef MIIKV_NARROW_COMBINE
 #define MIIKV_NARROW_COMBINE 1
 #endif
+#ifndef MIIKV_NARROW_THREADS
+#define MIIKV_NARROW_THREADS 16384
+#endif
 #ifndef MIIKV_ROWSET_MAX_CPW
 #define MIIKV_ROWSET_MAX_CPW 32
 #endif
@@ -1117,11 +1120,13 @@ static miikv_status decode_impl(const miikv_view* view, const NewRows& rows,
     const dim3 grid(static_cast<uint32_t>(wgs));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool f32 = q_dtype == MIIKV_DTYPE_F32;
-    // combine: one workgroup per (sequence, kv head, 32 output elements), or, with at
-    // most kNarrowRecords records per row set, one thread per 4 output elements
+    // combine: one workgroup per (sequence, kv head, 32 output elements), or one thread
+    // per 4 output elements when a row set holds at most kNarrowRecords records or the
+    // launch has threads enough that way (config 2's single sequence: 1024 threads
+    // for 65 records each, which the wide form reads in one round trip)
     const dim3 cgrid(batch * view->kv_heads, G * view->head_dim / 32);
-    const bool narrow = p.splits + 1 <= kNarrowRecords && MIIKV_NARROW_COMBINE;
     const uint64_t nthreads = static_cast<uint64_t>(batch) * view->kv_heads * G * view->head_dim / 4;
+    const bool narrow = (p.splits + 1 <= kNarrowRecords || nthreads >= MIIKV_NARROW_THREADS) && MIIKV_NARROW_COMBINE;
     const dim3 ngrid(static_cast<uint32_t>((nthreads + 255) / 256));
     const bool app = rows.any();
     const bool kf = mode_k_f16(view->quant_mode), vf = mode_v_f16(view->quant_mode);

@@ -258,11 +258,11 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
 }
 
 
-// Cross-split combine for launches with few records per row set (the host's bound,
-// max_splits + 1 <= kNarrowRecords: the row-set route of long suffixes): one thread per
-// 4 consecutive outputs of one (row set, kv head) folds all of that row set's records
-// itself, so the grid is one thread per 4 outputs instead of a 256-thread workgroup
-// per 32; 8 consecutive threads hold one 32-value block (Q8_1 epilogue).
+// Cross-split combine for launches with few records per row set or many row sets:
+// one thread per 4 consecutive outputs of one (row set, kv head) folds all of that row
+// set's records itself, kNarrowRecords loads in flight at a time, so the grid is one
+// thread per 4 outputs instead of a 256-thread workgroup per 32; 8 consecutive threads
+// hold one 32-value block (Q8_1 epilogue).
 constexpr uint32_t kNarrowRecords = 8;
 template <uint32_t D, bool APPEND>
 __global__ void __launch_bounds__(256) combine_narrow_kernel(SplitArgs a) {
@@ -296,21 +296,23 @@ __global__ void __launch_bounds__(256) combine_narrow_kernel(SplitArgs a) {
     const uint32_t nrec = split_count(L, cpw) + (APPEND && L > 0 ? 1u : 0u);
     float m = -INFINITY, l = 0.0f;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    float ms[kNarrowRecords], ls[kNarrowRecords];
-    float4 vv[kNarrowRecords];
+    for (uint32_t sp0 = 0; sp0 < nrec; sp0 += kNarrowRecords) {  // batches: all loads, then the merges
+        float ms[kNarrowRecords], ls[kNarrowRecords];
+        float4 vv[kNarrowRecords];
 #pragma unroll
-    for (uint32_t sp = 0; sp < kNarrowRecords; ++sp) {  // all loads before the first merge
-        ms[sp] = -INFINITY;
-        if (sp < nrec) {
-            const float* r = part + static_cast<size_t>(sp) * rec;
-            ms[sp] = r[GD + hn];
-            ls[sp] = r[GD + G + hn];
-            vv[sp] = *reinterpret_cast<const float4*>(r + e);
+        for (uint32_t j = 0; j < kNarrowRecords; ++j) {
+            ms[j] = -INFINITY;
+            if (sp0 + j < nrec) {
+                const float* r = part + static_cast<size_t>(sp0 + j) * rec;
+                ms[j] = r[GD + hn];
+                ls[j] = r[GD + G + hn];
+                vv[j] = *reinterpret_cast<const float4*>(r + e);
+            }
         }
-    }
 #pragma unroll
-    for (uint32_t sp = 0; sp < kNarrowRecords; ++sp)
-        if (sp < nrec) merge_state(m, l, acc, ms[sp], ls[sp], vv[sp]);
+        for (uint32_t j = 0; j < kNarrowRecords; ++j)
+            if (sp0 + j < nrec) merge_state(m, l, acc, ms[j], ls[j], vv[j]);
+    }
     combine_emit(a, out_row0, e, q, e - 4 * q, l, acc, gv, live);
 }
 
