@@ -384,3 +384,69 @@ def test_decode_fp32_query_low_parts_count(gpu, hq, hk, d, length):
     print(f"hq={hq} hk={hk} d={d}: |o32-ref|={e32:.3e} |o16-ref|={e16:.3e}")
     assert not np.array_equal(o32, o16)
     assert e32 < 0.5 * e16, (e32, e16)
+
+
+# seeds 10-13 fix shapes with at least 16384 combine threads (the narrow combine
+# whatever the record bound): 16 x 24q/4kv/D256 (config 3's shape), 24 x 32q/8kv/D128,
+# 20 x 48q/8kv/D128, 12 x 64q/8kv/D256
+_WIDE_BATCHES = {10: (256, 4, 6, 16), 11: (128, 8, 4, 24), 12: (128, 8, 6, 20), 13: (256, 8, 8, 12)}
+
+
+@pytest.mark.parametrize("seed", range(14))
+def test_decode_random_batches(gpu, seed):
+    """Seeded random batches of paged decodes (batch, heads per kv head, head_dim, ragged
+    lengths including 0 and 1, context bound, query dtype, gate): the plan's split
+    size, the device's choice of steps per wave and the combine form (the wide one,
+    or one thread per 4 outputs) all vary with them; every row against the oracle."""
+    import miinfer_amd as m
+    rng = np.random.default_rng(1000 + seed)
+    d = int(rng.choice([128, 256]))
+    hk = int(rng.choice([1, 2, 4, 8]))
+    g = int(rng.choice([1, 2, 4, 6, 8]))
+    hq = hk * g
+    batch = int(rng.integers(1, 25))
+    if seed in _WIDE_BATCHES:
+        d, hk, g, batch = _WIDE_BATCHES[seed]
+        hq = hk * g
+    pt = 256
+    lens = rng.integers(0, 2500, size=batch)
+    lens[rng.random(batch) < 0.15] = 0
+    lens[rng.random(batch) < 0.1] = 1
+    pages = [max(1, (int(n) + pt) // pt) for n in lens]
+    stride = max(pages) + int(rng.integers(0, 3))  # a context bound above the longest sequence
+    total = sum(pages)
+    perm = rng.permutation(total).astype(np.int32)
+    table = np.zeros((batch, stride), np.int32)
+    o = 0
+    for s, p in enumerate(pages):
+        table[s, :p] = perm[o:o + p]
+        table[s, p:] = perm[o + p - 1]  # unused entries name a valid page
+        o += p
+    cache = m.KvCache.paged_cache(hk, d, total, _dev(table, gpu), page_tokens=pt)
+    refs = []
+    for s, n in enumerate(lens):
+        n = int(n)
+        k = randn_f16(rng, (n, hk, d))
+        v = randn_f16(rng, (n, hk, d))
+        if n:
+            cache.append(_dev(k, gpu), _dev(v, gpu), base_position=0, seq=s)
+        kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+        vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+        refs.append((kc, ks, vc, vs))
+    f32 = bool(rng.integers(0, 2))
+    q = rng.standard_normal((batch, hq, d)).astype(np.float32) if f32 else randn_f16(rng, (batch, hq, d))
+    gate = rng.standard_normal((batch, hq, d)).astype(np.float32) if rng.integers(0, 2) else None
+    out, gated = m.decode_attention(cache, _dev(q, gpu), lengths=_dev(lens.astype(np.int32), gpu),
+                                    max_context=stride * pt, gate=None if gate is None else _dev(gate, gpu),
+                                    out=torch.empty((batch, hq, d), device=gpu))
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    what = f"seed {seed}: batch {batch} {hq}q/{hk}kv/D{d} f32={f32} gate={gate is not None}"
+    for s, n in enumerate(lens):
+        if n == 0:
+            assert not out[s].any(), what
+            continue
+        expect = oracle.attention_q8(q[s].astype(np.float32), *refs[s], int(n), hq, 1 / math.sqrt(d))
+        assert_attention_close(out[s], expect, f"{what} seq {s} L={n}")
+        if gate is not None:
+            assert_attention_close(gated[s].cpu().numpy(), expect / (1 + np.exp(-gate[s])), f"{what} gated seq {s}")
