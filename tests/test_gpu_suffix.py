@@ -532,3 +532,40 @@ def test_suffix_exact_route_errors(gpu):
     with pytest.raises(_lib.MiikvError) as err:  # never falls back to the MFMA path
         m.suffix_attention(c4, q4, 536, exact=True, workspace=small)
     assert err.value.status == _lib.MIIKV_EWORKSPACE
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_suffix_random(gpu, seed):
+    """Seeded random suffixes: token count (both sides of the decode-route rule),
+    prefix, head layout, fused store, MIIKV_SUFFIX_EXACT, query dtype and gate; every
+    output against the oracle."""
+    import miinfer_amd as m
+    rng = np.random.default_rng(2000 + seed)
+    hq, hk, d = [(24, 4, 256), (32, 8, 128), (16, 16, 128), (8, 2, 256), (6, 1, 128)][int(rng.integers(0, 5))]
+    t = int(rng.choice([1, 2, 3, 5, 8, 16, 33, 64, 65, 130, 300]))
+    prefix = int(rng.integers(0, 3000))
+    fused = bool(rng.integers(0, 2))
+    exact = bool(rng.integers(0, 2))
+    f32 = bool(rng.integers(0, 2))
+    cap = ((prefix + t + 63) // 64) * 64
+    k = randn_f16(rng, (prefix + t, hk, d))
+    v = randn_f16(rng, (prefix + t, hk, d))
+    kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+    vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+    cache = m.KvCache.contiguous(hk, d, cap)
+    if prefix:
+        cache.append(_dev(k[:prefix], gpu), _dev(v[:prefix], gpu), base_position=0)
+    kn, vn = _dev(k[prefix:], gpu), _dev(v[prefix:], gpu)
+    if not fused:
+        cache.append(kn, vn, base_position=prefix)
+    q = rng.standard_normal((t, hq, d)).astype(np.float32) if f32 else randn_f16(rng, (t, hq, d))
+    gate = rng.standard_normal((t, hq, d)).astype(np.float32) if rng.integers(0, 2) else None
+    kw = dict(k_new=kn, v_new=vn) if fused else {}
+    out, gated = m.suffix_attention(cache, _dev(q, gpu), prefix, gate=None if gate is None else _dev(gate, gpu),
+                                    out=torch.empty((t, hq, d), device=gpu), exact=exact, **kw)
+    torch.cuda.synchronize()
+    what = f"seed {seed}: {hq}q/{hk}kv/D{d} T={t} P={prefix} fused={fused} exact={exact} f32={f32}"
+    expect = oracle.suffix_attention_q8(q.astype(np.float32), kc, ks, vc, vs, prefix, hq, 1 / math.sqrt(d))
+    assert_attention_close(out.cpu().numpy(), expect, what)
+    if gate is not None:
+        assert_attention_close(gated.cpu().numpy(), expect / (1 + np.exp(-gate)), what + " gated")
