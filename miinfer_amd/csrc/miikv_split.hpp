@@ -130,6 +130,18 @@ __device__ __forceinline__ void merge_state(float& m, float& l, float4& acc, flo
     acc.w = acc.w * f1 + a2.w * f2;
 }
 
+// Gate values of elements i..i+3, loaded without a branch (without a gate, any valid
+// 16 bytes, here `fallback`, are read and ignored): a load in a branch is waited for at
+// the branch's end, which would hold back the loads issued after it.
+__device__ __forceinline__ void combine_gate(const SplitArgs& a, size_t i, const float* fallback, float (&gv)[4]) {
+    const bool has = a.gate != nullptr;
+    const float4 g4 = *reinterpret_cast<const float4*>(has ? a.gate + i : fallback);
+    gv[0] = has ? g4.x : 0.0f;
+    gv[1] = has ? g4.y : 0.0f;
+    gv[2] = has ? g4.z : 0.0f;
+    gv[3] = has ? g4.w : 0.0f;
+}
+
 // Output of 4 merged elements e..e+3 (thread q of the 8 holding a 32-value block that
 // starts at element blk0 of the launch's rows): out = acc / L, 0 when L == 0
 // (qwen3_primitives.hip:2349); gated = out * sigmoid(gate); the Q8_1 block.  All 8
@@ -197,11 +209,6 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
     const float* part = a.part + (static_cast<size_t>(bh) * slots) * rec;
 
     constexpr uint32_t kSpec = 3;
-    float gv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (a.gate != nullptr && tid < 8) {
-        const float4 g4 = *reinterpret_cast<const float4*>(a.gate + out_row0 + e);
-        gv[0] = g4.x; gv[1] = g4.y; gv[2] = g4.z; gv[3] = g4.w;
-    }
     float ms[kSpec], ls[kSpec];
     float4 vv[kSpec];
 #pragma unroll
@@ -217,6 +224,8 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
             vv[j] = *reinterpret_cast<const float4*>(r + e);
         }
     }
+    float gv[4];
+    combine_gate(a, out_row0 + e, part, gv);
     const uint32_t cpw = launch_cpw(a);
     if (a.count_ptr != nullptr && b >= *a.count_ptr) return;
     const uint32_t L = split_length(a, b);
@@ -268,7 +277,6 @@ template <uint32_t D, bool APPEND>
 __global__ void __launch_bounds__(256) combine_narrow_kernel(SplitArgs a) {
     const uint32_t G = a.group;
     const uint32_t GD = G * D;
-    const uint32_t cpw = launch_cpw(a);  // every thread of the workgroup takes part
     const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
     const uint64_t per = GD / 4;
     const uint32_t bh = static_cast<uint32_t>(idx / per);
@@ -284,11 +292,24 @@ __global__ void __launch_bounds__(256) combine_narrow_kernel(SplitArgs a) {
                              (hn - tp * Gt)) * D - static_cast<size_t>(hn) * D;
     const uint32_t rec = record_floats(G, D);
     const float* part = a.part + (static_cast<size_t>(bhc) * (a.max_splits + 1)) * rec;
-    float gv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (a.gate != nullptr) {
-        const float4 g4 = *reinterpret_cast<const float4*>(a.gate + out_row0 + e);
-        gv[0] = g4.x; gv[1] = g4.y; gv[2] = g4.z; gv[3] = g4.w;
+    // The first batch of record slots is read before the context length arrives (slots
+    // past the row set's count hold stale bytes and are dropped below), then the gate.
+    const uint32_t slots = a.max_splits + 1;
+    float ms[kNarrowRecords], ls[kNarrowRecords];
+    float4 vv[kNarrowRecords];
+#pragma unroll
+    for (uint32_t j = 0; j < kNarrowRecords; ++j) {
+        if (j < slots) {
+            const float* r = part + static_cast<size_t>(j) * rec;
+            ms[j] = r[GD + hn];
+            ls[j] = r[GD + G + hn];
+            vv[j] = *reinterpret_cast<const float4*>(r + e);
+        }
     }
+    float gv[4];
+    combine_gate(a, out_row0 + e, part, gv);
+    // steps per wave (every thread of the workgroup takes part) with the loads in flight
+    const uint32_t cpw = launch_cpw(a);
     // a whole 32-value block shares b (GD is a multiple of 32), so the 8 threads of a
     // block take the same exit
     if (a.count_ptr != nullptr && b >= *a.count_ptr) return;
@@ -296,9 +317,10 @@ __global__ void __launch_bounds__(256) combine_narrow_kernel(SplitArgs a) {
     const uint32_t nrec = split_count(L, cpw) + (APPEND && L > 0 ? 1u : 0u);
     float m = -INFINITY, l = 0.0f;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (uint32_t sp0 = 0; sp0 < nrec; sp0 += kNarrowRecords) {  // batches: all loads, then the merges
-        float ms[kNarrowRecords], ls[kNarrowRecords];
-        float4 vv[kNarrowRecords];
+#pragma unroll
+    for (uint32_t j = 0; j < kNarrowRecords; ++j)
+        if (j < nrec) merge_state(m, l, acc, ms[j], ls[j], vv[j]);
+    for (uint32_t sp0 = kNarrowRecords; sp0 < nrec; sp0 += kNarrowRecords) {  // further batches
 #pragma unroll
         for (uint32_t j = 0; j < kNarrowRecords; ++j) {
             ms[j] = -INFINITY;
