@@ -362,8 +362,19 @@ def bench_c4(dev, args) -> int:
                                        ws_s.numel(), P(s.cuda_stream)) == 0
         short[f"T{ts}_us"] = round(sorted(_time_graph(attn_short, max(4, nrep // 24), 3, inner=8)[0]
                                           for _ in range(3))[1], 2)
-    # The exact route (MIIKV_SUFFIX_EXACT, fp32 query): every token as a decode.
+    # The reference's own call arguments (attention_layer.cpp:297-343): fp32 q_rope,
+    # gate and gated output, on the MFMA path.
     q32 = q.float()
+    gate = torch.randn((t, hq, d), device=dev)
+    gated = torch.empty((t, hq, d), device=dev)
+
+    def attn_ref(s):
+        assert L.miikv_suffix_attn(cache.view, P(q32.data_ptr()), _lib.DTYPE_F32, hq,
+                                   ctypes.c_float(1 / math.sqrt(d)), t, prefix, 0, None,
+                                   None, P(gate.data_ptr()), P(gated.data_ptr()), P(ws.data_ptr()), ws_bytes,
+                                   P(s.cuda_stream)) == 0
+    us_ref = sorted(_time_graph(attn_ref, max(4, nrep // 24), 3, inner=8)[0] for _ in range(3))[1]
+    # The exact route (MIIKV_SUFFIX_EXACT, fp32 query): every token as a decode.
     ws_x = torch.empty(m.suffix_workspace_bytes(cache, hq, t, exact=True), dtype=torch.uint8, device=dev)
 
     def attn_exact(s):
@@ -395,6 +406,9 @@ def bench_c4(dev, args) -> int:
                         "GBs": round(prefix * append_bytes(hkv, d) / (us_bulk * 1e-6) / 1e9, 1)},
         "short_suffix": dict(short, note="miikv_suffix_attn with T tokens over the same 8192-token prefix "
                                          "(a batch of decodes, 2 tokens per context pass)"),
+        "reference_signature": {"us": round(us_ref, 2), "TFLOPs": round(flops / (us_ref * 1e-6) / 1e12, 2),
+                                "note": "miikv_suffix_attn with an fp32 query, gate and gated output (the "
+                                        "reference's arguments), MFMA path"},
         "exact_route": {"us": round(us_exact, 2), "TFLOPs": round(flops / (us_exact * 1e-6) / 1e12, 2),
                         "note": "miikv_suffix_attn_ex with MIIKV_SUFFIX_EXACT and an fp32 query: every token as a "
                                 "decode (the query's low half kept, block scales in fp32)"},

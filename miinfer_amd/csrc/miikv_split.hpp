@@ -130,16 +130,15 @@ __device__ __forceinline__ void merge_state(float& m, float& l, float4& acc, flo
     acc.w = acc.w * f1 + a2.w * f2;
 }
 
-// Gate values of elements i..i+3, loaded without a branch (without a gate, any valid
-// 16 bytes, here `fallback`, are read and ignored): a load in a branch is waited for at
-// the branch's end, which would hold back the loads issued after it.
-__device__ __forceinline__ void combine_gate(const SplitArgs& a, size_t i, const float* fallback, float (&gv)[4]) {
-    const bool has = a.gate != nullptr;
-    const float4 g4 = *reinterpret_cast<const float4*>(has ? a.gate + i : fallback);
-    gv[0] = has ? g4.x : 0.0f;
-    gv[1] = has ? g4.y : 0.0f;
-    gv[2] = has ? g4.z : 0.0f;
-    gv[3] = has ? g4.w : 0.0f;
+// Gate values of elements i..i+3.  Called after the record loads are issued: a load
+// in a branch is waited for at the branch's end, which would otherwise hold back the
+// loads issued after it (here everything it waits for is needed next).
+__device__ __forceinline__ void combine_gate(const SplitArgs& a, size_t i, float (&gv)[4]) {
+    gv[0] = gv[1] = gv[2] = gv[3] = 0.0f;
+    if (a.gate != nullptr) {
+        const float4 g4 = *reinterpret_cast<const float4*>(a.gate + i);
+        gv[0] = g4.x; gv[1] = g4.y; gv[2] = g4.z; gv[3] = g4.w;
+    }
 }
 
 // Output of 4 merged elements e..e+3 (thread q of the 8 holding a 32-value block that
@@ -225,7 +224,7 @@ __global__ void __launch_bounds__(256) combine_kernel(SplitArgs a) {
         }
     }
     float gv[4];
-    combine_gate(a, out_row0 + e, part, gv);
+    combine_gate(a, out_row0 + e, gv);
     const uint32_t cpw = launch_cpw(a);
     if (a.count_ptr != nullptr && b >= *a.count_ptr) return;
     const uint32_t L = split_length(a, b);
@@ -307,7 +306,7 @@ __global__ void __launch_bounds__(256) combine_narrow_kernel(SplitArgs a) {
         }
     }
     float gv[4];
-    combine_gate(a, out_row0 + e, part, gv);
+    combine_gate(a, out_row0 + e, gv);
     // steps per wave (every thread of the workgroup takes part) with the loads in flight
     const uint32_t cpw = launch_cpw(a);
     // a whole 32-value block shares b (GD is a multiple of 32), so the 8 threads of a

@@ -322,23 +322,38 @@ __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
     // ---- Q^T fragments (B operand): row n, dims 16c + 8hh .. +7.
     half8 qf[NC];
     {
-        const size_t qrow = (static_cast<size_t>(t_row) * a.q_heads + qh) * D;
+        const size_t qrow = (static_cast<size_t>(t_row) * a.q_heads + qh) * D;  // a valid row also when !row_ok
+        if (a.q_f32) {
+            // Batches of four fragments, loaded without a branch and then converted: a
+            // per-fragment load in a branch was waited for at the branch's end, one
+            // round trip per fragment.
 #pragma unroll
-        for (uint32_t c = 0; c < NC; ++c) {
-            half8 v = {};
-            if (row_ok) {
-                if (a.q_f32) {
-                    const float* qp = static_cast<const float*>(a.q) + qrow + c * 16 + hh * 8;
-                    const float4 x0 = *reinterpret_cast<const float4*>(qp);
-                    const float4 x1 = *reinterpret_cast<const float4*>(qp + 4);
-                    v[0] = (_Float16)x0.x; v[1] = (_Float16)x0.y; v[2] = (_Float16)x0.z; v[3] = (_Float16)x0.w;
-                    v[4] = (_Float16)x1.x; v[5] = (_Float16)x1.y; v[6] = (_Float16)x1.z; v[7] = (_Float16)x1.w;
-                } else {
+            for (uint32_t c0 = 0; c0 < NC; c0 += 4) {
+                float4 x[4][2];
+#pragma unroll
+                for (uint32_t j = 0; j < 4; ++j) {
+                    const float* qp = static_cast<const float*>(a.q) + qrow + (c0 + j) * 16 + hh * 8;
+                    x[j][0] = *reinterpret_cast<const float4*>(qp);
+                    x[j][1] = *reinterpret_cast<const float4*>(qp + 4);
+                }
+#pragma unroll
+                for (uint32_t j = 0; j < 4; ++j) {
+                    half8 v;
+                    v[0] = (_Float16)x[j][0].x; v[1] = (_Float16)x[j][0].y; v[2] = (_Float16)x[j][0].z; v[3] = (_Float16)x[j][0].w;
+                    v[4] = (_Float16)x[j][1].x; v[5] = (_Float16)x[j][1].y; v[6] = (_Float16)x[j][1].z; v[7] = (_Float16)x[j][1].w;
+                    qf[c0 + j] = row_ok ? v : half8{};
+                }
+            }
+        } else {
+#pragma unroll
+            for (uint32_t c = 0; c < NC; ++c) {
+                half8 v = {};
+                if (row_ok) {
                     const uint16_t* qp = static_cast<const uint16_t*>(a.q) + qrow + c * 16 + hh * 8;
                     v = __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(qp));
                 }
+                qf[c] = v;
             }
-            qf[c] = v;
         }
     }
 
@@ -550,24 +565,15 @@ __global__ void __launch_bounds__(256) suffix_combine_kernel(SuffixCombineArgs a
     const _Float16* po = static_cast<const _Float16*>(a.part);
     const float2* ml = reinterpret_cast<const float2*>(po + part_o_halves(a.splits, a.kv_heads, rows_cap, D));
     const size_t oi = (static_cast<size_t>(t) * a.q_heads + h * G + g) * D + kCombVec * dv;
-    // The gate goes out with the first batch of records (no round trip of its own).
-    float gv[kCombVec] = {};
-    if (a.gate && a.gated_out) {
-#pragma unroll
-        for (uint32_t c = 0; c < kCombVec; c += 4) {
-            const float4 x = *reinterpret_cast<const float4*>(a.gate + oi + c);
-            gv[c] = x.x; gv[c + 1] = x.y; gv[c + 2] = x.z; gv[c + 3] = x.w;
-        }
-    }
     // Records hold O_s / l_s: each split enters with weight l_s e^{m_s - M}.
     using HalfV = _Float16 __attribute__((ext_vector_type(kCombVec)));
     float M = -INFINITY, Ls = 0.0f;
     float acc[kCombVec] = {};
     // Batches of kU splits: every load of a batch is issued before the first merge.
     constexpr uint32_t kU = 8;
-    for (uint32_t sp0 = 0; sp0 < nsplit; sp0 += kU) {
-        float2 e[kU];
-        HalfV v[kU];
+    float2 e[kU];
+    HalfV v[kU];
+    auto load_batch = [&](uint32_t sp0) {
 #pragma unroll
         for (uint32_t j = 0; j < kU; ++j) {
             const uint32_t sp = min(sp0 + j, nsplit - 1);
@@ -575,6 +581,8 @@ __global__ void __launch_bounds__(256) suffix_combine_kernel(SuffixCombineArgs a
             e[j] = ml[pr];
             v[j] = *reinterpret_cast<const HalfV*>(po + pr * D + kCombVec * dv);
         }
+    };
+    auto merge_batch = [&](uint32_t sp0) {
 #pragma unroll
         for (uint32_t j = 0; j < kU; ++j) {
             const float mn = fmaxf(M, e[j].x);
@@ -586,6 +594,23 @@ __global__ void __launch_bounds__(256) suffix_combine_kernel(SuffixCombineArgs a
 #pragma unroll
             for (uint32_t c = 0; c < kCombVec; ++c) acc[c] = acc[c] * fo + static_cast<float>(v[j][c]) * ws;
         }
+    };
+    if (nsplit > 0) load_batch(0);
+    // The gate goes out right after the first batch of records: a load in a branch
+    // (or still in flight at the head of the batch loop) is waited for before the
+    // loads after it are issued, and here everything it waits for is needed next.
+    float gv[kCombVec] = {};
+    if (a.gate && a.gated_out) {
+#pragma unroll
+        for (uint32_t c = 0; c < kCombVec; c += 4) {
+            const float4 x = *reinterpret_cast<const float4*>(a.gate + oi + c);
+            gv[c] = x.x; gv[c + 1] = x.y; gv[c + 2] = x.z; gv[c + 3] = x.w;
+        }
+    }
+    if (nsplit > 0) merge_batch(0);
+    for (uint32_t sp0 = kU; sp0 < nsplit; sp0 += kU) {
+        load_batch(sp0);
+        merge_batch(sp0);
     }
     const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
 #pragma unroll
