@@ -270,6 +270,10 @@ __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
     constexpr uint32_t CHUNKS = TILE * 2 / 1024;  // 1 KiB copy chunks per step
     static_assert(CHUNKS % kSufWaves == 0, "copy chunks must split evenly over waves");
     __shared__ __align__(16) _Float16 s_t[kSufBufs][TILE];
+    // The tile buffers are the kernel's whole LDS.  Measured at D = 256: 8 bytes of
+    // LDS beyond 128 KiB (two flags) slowed the step loop by ~12%, so any other LDS
+    // variable has to live inside these buffers.
+    static_assert(sizeof(s_t) <= 128u * 1024u, "suffix LDS must stay within 128 KiB");
 
     uint32_t T = a.token_count;
     uint32_t P = a.base_position;
