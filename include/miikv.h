@@ -182,7 +182,9 @@ miikv_status miikv_append_batch_f16(const miikv_view* view, const uint16_t* k, c
 /* ---- split-K GQA decode attention ---------------------------------------- */
 
 /* Workspace bytes needed by miikv_decode_attn for `batch` sequences of at most
- * `max_context` tokens (per-split partial softmax records).  Its contents need
+ * `max_context` tokens (per-split partial softmax records); 0 for an invalid
+ * geometry or one decode does not serve (more than 16 query heads per kv head,
+ * for which miikv_decode_attn returns MIIKV_EUNSUPPORTED).  Its contents need
  * no initialisation; miikv_workspace_init zero-fills a buffer with a kernel
  * (no memset node), e.g. for reproducible dumps. */
 uint64_t miikv_decode_workspace_bytes(const miikv_view* view, uint32_t q_heads, uint32_t batch,

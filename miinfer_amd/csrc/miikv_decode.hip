@@ -924,6 +924,7 @@ extern "C" uint64_t miikv_decode_workspace_bytes(const miikv_view* view, uint32_
                                                  uint32_t max_context) {
     if (validate_view(view) != MIIKV_OK || view->kv_heads == 0 || q_heads % view->kv_heads != 0 || batch == 0)
         return 0;
+    if (q_heads / view->kv_heads > 16) return 0;  // the MFMA serves at most 16 query heads per kv head
     const Plan p = make_plan(view, q_heads, batch, max_context);
     return p.counter_bytes + p.part_bytes;
 }

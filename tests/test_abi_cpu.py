@@ -112,6 +112,14 @@ def test_decode_rejects_before_launch():
     assert lib.miikv_decode_attn(ctypes.byref(v), ctypes.c_void_p(0x10), 0, 32, f, 1,
                                  ctypes.c_void_p(0x20), None, 4096, ctypes.c_void_p(0x30),
                                  ctypes.c_void_p(0x40), None, ws, need, None) == L.MIIKV_EINVAL
+    # more than 16 query heads per kv head (the MFMA's columns): not served by decode,
+    # no workspace size; the suffix path (rows are (token, head) pairs) still serves it
+    assert lib.miikv_decode_attn(ctypes.byref(v), ctypes.c_void_p(0x10), 0, 17 * 8, f, 1,
+                                 ctypes.c_void_p(0x20), None, 4096, ctypes.c_void_p(0x30), None,
+                                 None, ws, 1 << 30, None) == L.MIIKV_EUNSUPPORTED
+    assert lib.miikv_decode_workspace_bytes(ctypes.byref(v), 17 * 8, 1, 4096) == 0
+    assert lib.miikv_decode_workspace_bytes(ctypes.byref(v), 16 * 8, 1, 4096) > 0
+    assert lib.miikv_suffix_workspace_bytes(ctypes.byref(v), 17 * 8, 4) > 0
 
 
 def test_append_rejects_before_launch():

@@ -33,7 +33,10 @@ def _setup(gpu, rng, hq, hk, d, prefix, t, cap):
 @pytest.mark.parametrize("hq,hk,d,prefix,t", [(24, 4, 256, 300, 40), (32, 8, 128, 1000, 64),
                                               (24, 4, 256, 0, 17), (6, 1, 128, 64, 1),
                                               (24, 4, 256, 257, 33), (24, 4, 256, 5000, 3),
-                                              (8, 8, 128, 3000, 130)])
+                                              (8, 8, 128, 3000, 130),
+                                              # more query heads per kv head than decode's
+                                              # 16 MFMA columns: the MFMA path only
+                                              (34, 2, 128, 300, 9), (40, 2, 256, 100, 20)])
 @pytest.mark.parametrize("split", [True, False])
 def test_suffix_small(gpu, hq, hk, d, prefix, t, split):
     import miinfer_amd as m
