@@ -433,7 +433,9 @@ miikv_status miikv_pool_fork_n(miikv_pool* pool, const int32_t* parent_row, uint
 miikv_status miikv_pool_prepare_append(miikv_pool* pool, int32_t* row, uint32_t row_capacity,
                                        uint32_t position, uint32_t page_tokens,
                                        int32_t* copy_src, int32_t* copy_dst, uint32_t* n_copies);
-miikv_status miikv_pool_release(miikv_pool* pool, const int32_t* row, uint32_t length,
+/* Drop one reference on each page backing `length` tokens of `row`, and set
+ * those entries to -1 (a released row starts over as an empty row). */
+miikv_status miikv_pool_release(miikv_pool* pool, int32_t* row, uint32_t length,
                                 uint32_t page_tokens);
 
 /* Prefix fingerprint and match policy.  Restates ReusableContext

@@ -55,34 +55,6 @@ __device__ __forceinline__ void load16_f32(const float* p, float (&x)[16]) {
     }
 }
 
-// sin and cos of a RoPE angle (|a| < 2^17), the same float arithmetic in the CPU oracle
-// so the rotated keys are bit-identical there: a Cody-Waite reduction by pi/2 in three
-// parts (1.5703125 holds 8 bits, so k * P1 is exact for k < 2^16) with fused
-// multiply-adds, then the Taylor polynomials of sin and cos on [-pi/4, pi/4] (truncation
-// below 1e-11) in Horner form, and the quadrant.  Within two ulps of sin and cos.
-__device__ __forceinline__ void rope_sincos(float a, float* s, float* c) {
-#pragma clang fp contract(off)
-    const float k = rintf(a * 6.366197467e-01f);
-    float r = fmaf(-k, 1.5703125f, a);
-    r = fmaf(-k, 4.838267923e-04f, r);
-    r = fmaf(-k, 2.563282919e-12f, r);
-    const float r2 = r * r;
-    float ps = fmaf(r2, -2.505210794e-08f, 2.755731884e-06f);
-    ps = fmaf(r2, ps, -1.984127011e-04f);
-    ps = fmaf(r2, ps, 8.333333768e-03f);
-    ps = fmaf(r2, ps, -1.666666716e-01f);
-    const float sr = fmaf(r * r2, ps, r);
-    float pc = fmaf(r2, 2.087675588e-09f, -2.755731998e-07f);
-    pc = fmaf(r2, pc, 2.480158764e-05f);
-    pc = fmaf(r2, pc, -1.388888923e-03f);
-    pc = fmaf(r2, pc, 4.166666791e-02f);
-    pc = fmaf(r2, pc, -5.000000000e-01f);
-    const float cr = fmaf(r2, pc, 1.0f);
-    const int q = static_cast<int>(k) & 3;
-    *s = q == 0 ? sr : q == 1 ? cr : q == 2 ? -sr : -cr;
-    *c = q == 0 ? cr : q == 1 ? -sr : q == 2 ? -cr : sr;
-}
-
 // K prologue on one lane's 16 dims d0 = 16*q16 ..: RMSNorm * weight, then RoPE on
 // dims 0..63 (gfx906/kernels/qwen3_primitives.hip:7257-7281, 622-659).
 // The sum of squares follows the reference's 256-lane LDS tree exactly: element t
@@ -667,9 +639,8 @@ static miikv_status launch_append(const miikv_view* view, const AppendIn& in, ui
     // Positions known on the host: [head partial group][whole groups][tail partial group].
     // (The grouped store assembles q8 codes and scales; caches with an fp16 plane take
     // the per-row kernel.)
-    static const bool rows_only = std::getenv("MIIKV_APPEND_ROWS_ONLY") != nullptr;  // measurement
     if (ps == nullptr && ds == nullptr && positions == nullptr && rows_tokens >= kTileAppendMin &&
-        view->quant_mode == MIIKV_KV_Q8_Q8 && !rows_only) {
+        view->quant_mode == MIIKV_KV_Q8_Q8) {
         const uint32_t D = view->head_dim;
         const uint32_t head = (32 - base % 32) % 32;
         const uint32_t whole = (rows_tokens - head) / 32;

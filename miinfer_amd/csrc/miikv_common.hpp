@@ -8,6 +8,7 @@
 #include <cstdint>
 
 #include "miikv.h"
+#include "miikv_rope.h"
 
 namespace miikv {
 

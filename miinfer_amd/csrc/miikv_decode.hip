@@ -29,12 +29,6 @@
 // gated = out * sigmoid(gate).  With the fused append, the last workgroups of
 // the grid quantise, store and score the new token and write it as one more
 // record (append_record).
-//
-// Measurement switches (never defined by the product build; each gives wrong
-// results by design and exists to time one part of the kernel in isolation):
-// MIIKV_EXP_NO_LOOP (no step: the fixed cost of a launch), MIIKV_EXP_NO_COMPUTE
-// (loads only), MIIKV_EXP_NO_KBIAS (no code bias), MIIKV_EXP_EXP2F (library exp2),
-// MIIKV_EXP_NO_COMBINE (D = 128: no combine launch).
 #include "miikv_common.hpp"
 #include "miikv_split.hpp"
 
@@ -143,11 +137,7 @@ __device__ __forceinline__ float wave_max_xor_16_32(float x) {
 
 // Raw v_exp_f32: no denormal range fix-up (results below 2^-126 flush to 0, which
 // only drops probabilities that are already negligible); exp2(-inf) == 0.
-#ifdef MIIKV_EXP_EXP2F
-__device__ __forceinline__ float fast_exp2(float x) { return exp2f(x); }
-#else
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-#endif
 
 
 // Packed work items of a batch: sequence b owns ceil(L_b / split tokens) * kv_heads
@@ -195,31 +185,6 @@ __device__ bool locate_item(const SplitArgs& a, uint32_t cpw, uint32_t id, uint3
     return true;
 }
 
-// sin and cos of a RoPE angle: the arithmetic of miikv_cache.hip's rope_sincos (and of
-// the CPU oracle), so the fused store rotates keys to the same bits as miikv_append_f32.
-__device__ __forceinline__ void rope_sincos_d(float a, float* s, float* c) {
-#pragma clang fp contract(off)
-    const float k = rintf(a * 6.366197467e-01f);
-    float r = fmaf(-k, 1.5703125f, a);
-    r = fmaf(-k, 4.838267923e-04f, r);
-    r = fmaf(-k, 2.563282919e-12f, r);
-    const float r2 = r * r;
-    float ps = fmaf(r2, -2.505210794e-08f, 2.755731884e-06f);
-    ps = fmaf(r2, ps, -1.984127011e-04f);
-    ps = fmaf(r2, ps, 8.333333768e-03f);
-    ps = fmaf(r2, ps, -1.666666716e-01f);
-    const float sr = fmaf(r * r2, ps, r);
-    float pc = fmaf(r2, 2.087675588e-09f, -2.755731998e-07f);
-    pc = fmaf(r2, pc, 2.480158764e-05f);
-    pc = fmaf(r2, pc, -1.388888923e-03f);
-    pc = fmaf(r2, pc, 4.166666791e-02f);
-    pc = fmaf(r2, pc, -5.000000000e-01f);
-    const float cr = fmaf(r2, pc, 1.0f);
-    const int q = static_cast<int>(k) & 3;
-    *s = q == 0 ? sr : q == 1 ? cr : q == 2 ? -sr : -cr;
-    *c = q == 0 ? cr : q == 1 ? -sr : q == 2 ? -cr : sr;
-}
-
 // The reference's K prologue for one row held one value per thread (thread t < D owns
 // dim t), in its own shape (qwen35_decoupled_k_norm_rope_kv_store_batch_quant_kernel,
 // gfx906/kernels/qwen3_primitives.hip:7257-7281): sum of squares by the tree
@@ -260,7 +225,7 @@ __device__ void k_prologue(float& kx, float w, uint32_t tid, uint32_t position, 
             angle = i < (tid & 31) ? next : angle;
         }
         float sn, cs;
-        rope_sincos_d(angle, &sn, &cs);
+        rope_sincos(angle, &sn, &cs);
         const float other = __shfl_xor(kx, 32, 64);
         kx = tid < 32 ? kx * cs - other * sn : other * sn + kx * cs;
     }
@@ -591,11 +556,7 @@ decode_kernel(SplitArgs a) {
     // (Lc_col); steps past Lc_lo, the shortest, mask per column.
     const uint32_t Lc_lo = Lc - (a.pack - 1);
     const uint32_t Lc_col = a.pack == 1 ? Lc : Lc - (a.pack - 1 - min(n, G - 1) / (G / a.pack));
-#ifdef MIIKV_EXP_NO_LOOP
-    const uint32_t n_steps = 0;
-#else
     const uint32_t n_steps = first < nsteps ? min(n_max, (nsteps - first + stride - 1) / stride) : 0;
-#endif
     // Per-wave LDS staging of one step's scales: [K: 32*NB][V: 32*NB] fp16.  Each lane
     // loads NB/2 scales (no redundancy) and re-reads the 4*NB it needs from LDS.
     uint16_t* s_sc = reinterpret_cast<uint16_t*>(smem + 32 * kWavesPerWg + kWavesPerWg * G * D) + wave * (2 * kChunk * NB);
@@ -605,21 +566,6 @@ decode_kernel(SplitArgs a) {
     // past L may hold anything, including non-finite scales).
     auto compute_step = [&](uint32_t c, const Step& st) __attribute__((always_inline)) {
         const uint32_t tok0 = c * kChunk;
-#ifdef MIIKV_EXP_NO_COMPUTE
-        {
-            uint32_t x = reinterpret_cast<const uint32_t*>(&st.ks)[0] ^ reinterpret_cast<const uint32_t*>(&st.vs)[0];
-#pragma unroll
-            for (uint32_t J = 0; J < 2; ++J)
-#pragma unroll
-                for (uint32_t cc = 0; cc < NC; ++cc)
-                    x ^= st.k[J][cc][0].x ^ st.k[J][cc][0].y ^ st.k[J][cc][0].z ^ st.k[J][cc][0].w;
-#pragma unroll
-            for (uint32_t mt = 0; mt < NM; ++mt) x ^= st.v[mt].x ^ st.v[mt].y;
-            l_run += static_cast<float>(x & 1u);
-            m_run = 0.0f;
-            return;
-        }
-#endif
         const bool tail = tok0 + kChunk > Lc_lo;
         if constexpr (!KF16) *reinterpret_cast<ScaleVec*>(s_sc + lane * (NB / 2)) = st.ks;
         if constexpr (!VF16) {
@@ -665,15 +611,9 @@ decode_kernel(SplitArgs a) {
 #pragma unroll
             for (uint32_t cc = 0; cc < NC; ++cc) {
                 const uint4 w = st.k[J][cc][0];
-#ifdef MIIKV_EXP_NO_KBIAS
-                const half8 a0 = codes8_to_half8(w.x, w.y);
-                const half8 a1 = codes8_to_half8(w.z, w.w);
-                const float b0 = 0.0f, b1 = 0.0f;
-#else
                 const half8 a0 = codes8_to_half8_biased(w.x, w.y);  // block 2cc
                 const half8 a1 = codes8_to_half8_biased(w.z, w.w);  // block 2cc+1
                 const float b0 = -kbias[2 * cc], b1 = -kbias[2 * cc + 1];
-#endif
                 float4v c0 = mfma_16x16x32(a0, qf[2 * cc], float4v{b0, b0, b0, b0});
                 float4v c1 = mfma_16x16x32(a1, qf[2 * cc + 1], float4v{b1, b1, b1, b1});
                 if (kLo) {
@@ -889,19 +829,11 @@ Plan make_plan(const miikv_view* v, uint32_t q_heads, uint32_t batch, uint32_t m
     // 23.0; 4k and 64k unchanged).  Batches keep the full target (config 3 is tuned so).
     const uint64_t target = (v->head_dim == 256 && batch == 1) ? kTargetWaves / 2 : kTargetWaves;
     uint64_t cpw = (waves + target - 1) / target;
-    // MIIKV_DECODE_STEPS_PER_WAVE fixes the 32-token steps per wave (split size =
-    // 4 waves x steps x 32 tokens), a tuning override in the spirit of the
-    // reference's MIINFER_ATTENTION_SPLITS (qwen3_primitives.hip:5229-5245).
-    static const uint64_t fixed_cpw = [] {
-        const char* e = std::getenv("MIIKV_DECODE_STEPS_PER_WAVE");
-        return e ? std::strtoull(e, nullptr, 10) : 0ull;
-    }();
     // A batch: cpw is the floor of the device-side choice (launch_cpw), which
     // can only raise it; the records and the grid are sized for the floor, a
     // quarter of the all-sequences-full value.
     if (batch > 1) cpw = (cpw + 3) / 4;
-    p.adaptive = batch > 1 && fixed_cpw == 0;
-    if (fixed_cpw != 0) cpw = fixed_cpw;
+    p.adaptive = batch > 1;
     if (cpw < 1) cpw = 1;
     if (cpw > cpw_cap) cpw = cpw_cap;
     p.cpw = static_cast<uint32_t>(cpw);
@@ -1133,9 +1065,6 @@ static miikv_status decode_impl(const miikv_view* view, const NewRows& rows,
     const bool kf = mode_k_f16(view->quant_mode), vf = mode_v_f16(view->quant_mode);
     if (view->head_dim == 128) {
         launch_decode<128>(f32, app, kf, vf, grid, lds, s, a);
-#ifdef MIIKV_EXP_NO_COMBINE
-        return hip_status(hipGetLastError());
-#endif
         if (narrow && app) hipLaunchKernelGGL((combine_narrow_kernel<128, true>), ngrid, dim3(256), 0, s, a);
         else if (narrow) hipLaunchKernelGGL((combine_narrow_kernel<128, false>), ngrid, dim3(256), 0, s, a);
         else if (app) hipLaunchKernelGGL((combine_kernel<128, true>), cgrid, dim3(256), 0, s, a);
@@ -1185,8 +1114,7 @@ miikv_status suffix_by_decode(const miikv_view* view, const void* q, uint32_t q_
     rs.len_add = prefill_state ? 1u : base_position + 1u;
     rs.count_ptr = prefill_state ? &prefill_state->token_count : nullptr;
     rs.seq = seq;
-    static const bool no_pack = std::getenv("MIIKV_SUFFIX_NO_PACK") != nullptr;  // measurement
-    rs.pack = no_pack ? 1u : suffix_pack(view, q_heads, token_count, prefill_state != nullptr);
+    rs.pack = suffix_pack(view, q_heads, token_count, prefill_state != nullptr);
     return decode_impl(view, NewRows{}, q, q_dtype, q_heads, scale, token_count, nullptr, nullptr, bound, out, gate,
                        gated_out, nullptr, workspace, workspace_bytes, stream, &rs);
 }

@@ -171,12 +171,18 @@ extern "C" miikv_status miikv_pool_prepare_append(miikv_pool* p, int32_t* row, u
     return MIIKV_OK;
 }
 
-extern "C" miikv_status miikv_pool_release(miikv_pool* p, const int32_t* row, uint32_t length, uint32_t page_tokens) {
+// Drops the row's page references and marks its entries -1, so that a row reused
+// after release cannot hand prepare_append a page id that may since belong to
+// another sequence.
+extern "C" miikv_status miikv_pool_release(miikv_pool* p, int32_t* row, uint32_t length, uint32_t page_tokens) {
     if (p == nullptr || page_tokens == 0 || (length > 0 && row == nullptr)) return MIIKV_EINVAL;
     const uint32_t np = pages_for(length, page_tokens);
     for (uint32_t i = 0; i < np; ++i)
         if (!valid_page(p, row[i]) || p->refs[static_cast<size_t>(row[i])] == 0) return MIIKV_EINVAL;
-    for (uint32_t i = 0; i < np; ++i) miikv_pool_unref(p, row[i]);
+    for (uint32_t i = 0; i < np; ++i) {
+        miikv_pool_unref(p, row[i]);
+        row[i] = -1;
+    }
     return MIIKV_OK;
 }
 

@@ -29,9 +29,6 @@
 // and stores its rows; otherwise each (token, kv head, split) writes a partial
 // record (unnormalised O, running max, sum) and suffix_combine_kernel merges
 // them with token t's context length P + t + 1.
-//
-// MIIKV_SFX_EXP_NOLOOP (never defined by the product build) times the kernel's
-// fixed cost with a single step per workgroup; its results are wrong by design.
 #include "miikv_suffix.hpp"
 
 #include <algorithm>
@@ -317,11 +314,7 @@ __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
     if (key_lo >= nkeys) return;  // no row of this workgroup has keys in this split
     const uint32_t key_hi = min(nkeys, key_lo + a.split_keys);
     const uint32_t s_begin = key_lo / kSufStep;
-#ifdef MIIKV_SFX_EXP_NOLOOP
-    const uint32_t s_end = s_begin + 1;
-#else
     const uint32_t s_end = (key_hi + kSufStep - 1) / kSufStep;
-#endif
 
     // ---- Q^T fragments (B operand): row n, dims 16c + 8hh .. +7.
     half8 qf[NC];
@@ -650,11 +643,9 @@ namespace {
 // 76.3/34.2, T=16 76.8/47.0.  Without packing (a device token count), 24q/4kv/D256:
 // context 8192 T=12 41.4/36.7, T=16 42.7/46.7; context 32768 T=6 80.3/54.9, T=8
 // 80.7/77.8.  So: at most 6 row sets above a 16384-position capacity, 12 at or
-// below it.  MIIKV_SUFFIX_DECODE_MAX_T (a token count) overrides the rule.
+// below it.
 bool suffix_runs_as_decode(const miikv_view* v, uint32_t q_heads, uint32_t token_count, bool device_count) {
     if (!decode_columns_fit(q_heads / v->kv_heads, v->head_dim)) return false;
-    static const char* env = std::getenv("MIIKV_SUFFIX_DECODE_MAX_T");
-    if (env) return token_count <= static_cast<uint32_t>(std::strtoul(env, nullptr, 10));
     if (token_count > kSuffixDecodeMaxT) return false;
     const uint32_t rows = token_count / suffix_pack(v, q_heads, token_count, device_count);
     return rows <= (view_seq_capacity(v) <= 16384 ? kSuffixDecodeMaxRowsShort : kSuffixDecodeMaxRows);
@@ -690,7 +681,6 @@ SuffixPlan make_suffix_plan(const miikv_view* v, uint32_t q_heads, uint32_t toke
     // second partial round costs a full one), at least 256 keys each.
     const uint64_t by_keys = std::min<uint64_t>((key_bound + 255) / 256, kSufMaxSplits);
     uint64_t want = std::max<uint64_t>(1, kSufSlots / wgs);
-    if (const char* e = std::getenv("MIIKV_SUFFIX_SPLITS")) want = std::strtoul(e, nullptr, 10);
     want = std::max<uint64_t>(1, std::min<uint64_t>({want, by_keys, kSufMaxSplits}));
     if (want <= 1) return p;
     const uint64_t unit = kSufStep;

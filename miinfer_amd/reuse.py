@@ -82,6 +82,10 @@ class PagePool:
                                     parent_row.size, _i32p(src), _i32p(dst), ctypes.byref(nc),
                                     ctypes.byref(done))
         if r != 0:
+            # the forks completed before the pool ran out hold page references and fresh
+            # pages: give them back, so a failed call leaves the pool as it found it
+            for c in range(done.value):
+                self.release(rows[c], length, page_tokens)
             raise MemoryError(f"page pool exhausted after {done.value} of {n} forks")
         return rows, list(zip(src[:nc.value].tolist(), dst[:nc.value].tolist()))
 
@@ -97,8 +101,11 @@ class PagePool:
         return [(int(src[0]), int(dst[0]))] if n.value else []
 
     def release(self, row: np.ndarray, length: int, page_tokens: int) -> None:
-        row = np.ascontiguousarray(row, np.int32)
-        call("miikv_pool_release", self._h, _i32p(row), length, page_tokens)
+        """Drop the row's page references; its entries become -1 (in place)."""
+        work = np.ascontiguousarray(row, np.int32)
+        call("miikv_pool_release", self._h, _i32p(work), length, page_tokens)
+        if work is not row:
+            row[...] = work
 
 
 def run_page_copies(cache: KvCache, copies, stream=None) -> None:

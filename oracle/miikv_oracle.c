@@ -121,7 +121,7 @@ void miikv_oracle_quantize_rows_f32(const float* rows, size_t n_rows, uint32_t h
 }
 
 /* sin and cos of a RoPE angle with the float arithmetic of the library's prologue
- * (miinfer_amd/csrc/miikv_cache.hip rope_sincos): Cody-Waite reduction by pi/2 in three
+ * (miinfer_amd/csrc/miikv_rope.h, rope_sincos): Cody-Waite reduction by pi/2 in three
  * parts with fused multiply-adds, Taylor polynomials on [-pi/4, pi/4], quadrant.  The
  * reference calls cosf / sinf (qwen3_primitives.hip:651-652); this pair is pinned
  * against float64 sin / cos in the tests (within two ulps). */

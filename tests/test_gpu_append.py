@@ -184,7 +184,7 @@ def test_append_f32_norm_rope_matches_oracle(gpu, hk, d, theta, base):
 
 
 @pytest.mark.parametrize("hk,d", [(8, 128), (4, 256)])
-def test_append_tile_path_matches_row_path(gpu, hk, d, monkeypatch):
+def test_append_tile_path_matches_row_path(gpu, hk, d):
     """Bulk appends send whole 32-token groups through the LDS-assembled tile kernel and
     the partial groups at either end through the per-row kernel: the bytes must equal
     the per-row kernel's alone (same arithmetic), for fp16 rows against the oracle too,
@@ -201,18 +201,22 @@ def test_append_tile_path_matches_row_path(gpu, hk, d, monkeypatch):
     w = rng.uniform(0.5, 1.5, d).astype(np.float32)
 
     def run(rows_only):
-        if rows_only:
-            monkeypatch.setenv("MIIKV_APPEND_ROWS_ONLY", "1")
-        else:
-            monkeypatch.delenv("MIIKV_APPEND_ROWS_ONLY", raising=False)
+        # rows_only: chunks below the grouped store's 64-token minimum, so every row goes
+        # through the per-row kernel
+        step = 40 if rows_only else 400
+
+        def put(cache, fn, k, v, base, **kw):
+            for t0 in range(0, k.shape[0], step):
+                fn(_dev(k[t0:t0 + step], gpu), _dev(v[t0:t0 + step], gpu), base_position=base + t0, **kw)
+
         out = []
         for layout in ("contiguous", "paged"):
             cache = (m.KvCache.contiguous(hk, d, 768) if layout == "contiguous"
                      else m.KvCache.paged_cache(hk, d, 4, table, page_tokens=pt))
-            cache.append(_dev(k16[:300], gpu), _dev(v16[:300], gpu), base_position=45)
-            cache.append_f32(_dev(k32[:100], gpu), _dev(v32[:100], gpu), base_position=345,
-                             k_norm_weight=_dev(w, gpu), theta=1.0e6, epsilon=1e-6)
-            cache.append_f32(_dev(k32[100:400], gpu), _dev(v32[100:400], gpu), base_position=445)
+            put(cache, cache.append, k16[:300], v16[:300], 45)
+            put(cache, cache.append_f32, k32[:100], v32[:100], 345, k_norm_weight=_dev(w, gpu), theta=1.0e6,
+                epsilon=1e-6)
+            put(cache, cache.append_f32, k32[100:400], v32[100:400], 445)
             out.append(_export_np(cache, 0, 0, 745))
         return out
 

@@ -361,15 +361,15 @@ def test_k_norm_sum_of_squares_follows_the_reference_tree(d):
 
 def test_rope_sincos_close_to_float64():
     """The prologue's sin/cos pair against float64 sin and cos of the same float32 angle,
-    over the RoPE angle range (positions < 2^16 times step^i <= 1) and around multiples of
+    over the RoPE angle range (positions up to 131072 times step^i <= 1) and around multiples of
     pi/2, where the reduction matters: within 2.5 float32 ulps where |value| >= 1/16 and
     within 1e-7 absolute everywhere (libm's sinf/cosf are within half an ulp; a wrong
     quadrant, sign, reduction constant or polynomial coefficient is off by far more)."""
     rng = np.random.default_rng(7)
     angles = np.concatenate([
-        rng.uniform(0, 65536, 4000), rng.uniform(0, 8, 2000),
-        (np.arange(1, 40000, 37) * (np.pi / 2))[:1000] + rng.uniform(-1e-3, 1e-3, 1000),
-        [0.0, 1e-8, 0.5, 1.0, 65535.0]]).astype(np.float32)
+        rng.uniform(0, 131072, 4000), rng.uniform(0, 8, 2000),
+        (np.arange(1, 83000, 83) * (np.pi / 2))[:1000] + rng.uniform(-1e-3, 1e-3, 1000),
+        [0.0, 1e-8, 0.5, 1.0, 65535.0, 131071.0]]).astype(np.float32)
     worst_ulps, worst_abs = 0.0, 0.0
     for a in angles:
         s, c = oracle.rope_sincos(float(a))
@@ -378,3 +378,36 @@ def test_rope_sincos_close_to_float64():
                 worst_ulps = max(worst_ulps, abs(got - exact) / float(np.spacing(np.float32(abs(exact)))))
             worst_abs = max(worst_abs, abs(got - exact))
     assert worst_ulps <= 2.5 and worst_abs <= 1e-7, (worst_ulps, worst_abs)
+
+
+def test_library_rope_sincos_header_matches_the_oracle(tmp_path):
+    """The kernels' rope_sincos (miinfer_amd/csrc/miikv_rope.h, included by every kernel
+    that rotates keys) compiled for the host gives the oracle's bits at RoPE angles up
+    to the largest supported position (131072) and around multiples of pi/2, so the
+    device code and the oracle cannot drift apart unnoticed."""
+    import ctypes
+    import shutil
+    import subprocess
+    cxx = shutil.which("g++")
+    if cxx is None:
+        pytest.skip("no host C++ compiler")
+    src = tmp_path / "rope_pin.cpp"
+    src.write_text('#include "miikv_rope.h"\n'
+                   'extern "C" void pin_rope(float a, float* s, float* c) { miikv::rope_sincos(a, s, c); }\n')
+    so = tmp_path / "librope_pin.so"
+    csrc = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "miinfer_amd", "csrc")
+    subprocess.run([cxx, "-O2", "-ffp-contract=off", "-Wno-unknown-pragmas", "-shared", "-fPIC",
+                    "-I", csrc, str(src), "-o", str(so)], check=True)
+    lib = ctypes.CDLL(str(so))
+    lib.pin_rope.argtypes = [ctypes.c_float, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float)]
+    rng = np.random.default_rng(11)
+    angles = np.concatenate([
+        rng.uniform(0, 131072, 3000), rng.uniform(0, 8, 500),
+        (np.arange(1, 83000, 83) * (np.pi / 2)) + rng.uniform(-1e-3, 1e-3, 1000),
+        [0.0, 1e-8, 65535.0, 65536.0, 131071.0]]).astype(np.float32)
+    s, c = ctypes.c_float(), ctypes.c_float()
+    for a in angles:
+        lib.pin_rope(float(a), ctypes.byref(s), ctypes.byref(c))
+        es, ec = oracle.rope_sincos(float(a))
+        assert (np.float32(s.value).view(np.uint32), np.float32(c.value).view(np.uint32)) == \
+            (np.float32(es).view(np.uint32), np.float32(ec).view(np.uint32)), float(a)

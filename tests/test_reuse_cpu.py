@@ -292,3 +292,33 @@ def test_registry_lru_eviction():
     before = pool.free_pages
     evicted = reg.evict_until_free(before + 1)     # a (least recent) holds 2 pages alone
     assert evicted == [ids["a"]] and pool.free_pages == before + 2
+
+
+def test_pool_release_clears_the_row_so_a_reused_row_cannot_write_a_foreign_page():
+    """A released row's entries become -1: reusing it allocates fresh pages instead of
+    handing back a page id that the pool has since given to another sequence."""
+    from miinfer_amd import reuse
+    pt = 256
+    pool = reuse.PagePool(4)
+    row = np.full(2, -1, np.int32)
+    assert pool.prepare_append(row, 0, pt) == []
+    old = int(row[0])
+    pool.release(row, 10, pt)
+    assert np.all(row == -1) and pool.refcount(old) == 0
+    other = np.full(2, -1, np.int32)
+    assert pool.prepare_append(other, 0, pt) == []
+    assert int(other[0]) == old  # the freed page now belongs to `other`
+    assert pool.prepare_append(row, 0, pt) == []  # the stale row gets a page of its own
+    assert int(row[0]) != old and pool.refcount(old) == 1 and pool.refcount(int(row[0])) == 1
+
+
+def test_fork_many_exhaustion_leaves_the_pool_unchanged():
+    """The Python wrapper gives back the forks completed before the pool ran out."""
+    from miinfer_amd.reuse import PagePool
+    pt, length = 256, 256 * 2 + 7
+    pool = PagePool(5)
+    row = np.array([pool.alloc() for _ in range(3)], np.int32)
+    free, refs = pool.free_pages, [pool.refcount(p) for p in range(5)]
+    with pytest.raises(MemoryError):
+        pool.fork_many(row, length, pt, 5)
+    assert pool.free_pages == free and [pool.refcount(p) for p in range(5)] == refs

@@ -99,6 +99,11 @@ def test_noalloc_paged_batch(gpu):
         a = _run(caches[0], kn, vn, q, lens, stride * pt, False, gpu)
         b = _run(caches[1], kn, vn, q, lens, stride * pt, True, gpu)
         assert torch.equal(a[0], b[0]), f"lens={lens_l}"
+        # the fused append wrote the same bytes into each sequence's pages
+        for s_, n in enumerate(lens_l):
+            ea, eb = caches[0].export_canonical(s_, 0, n), caches[1].export_canonical(s_, 0, n)
+            for x, y in zip(ea, eb):
+                assert torch.equal(x, y), f"lens={lens_l} seq={s_}"
 
 
 def test_noalloc_rejects_geometry_beyond_scratch(gpu):
