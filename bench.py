@@ -19,6 +19,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 
@@ -811,6 +812,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=640)
     ap.add_argument("--context", type=int, default=32768)
     ap.add_argument("--layers", type=int, default=8)
+    ap.add_argument("--repeats", type=int, default=10,
+                    help="timed blocks of --steps steps each (median and p10/p90 over them)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-sweep", action="store_true",
@@ -823,6 +826,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.steps < 1:
         ap.error("--steps must be at least 1")
+    if args.repeats < 1:
+        ap.error("--repeats must be at least 1")
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this path runs on a single MI355X "
               "(it would shard by kv head or by sequence with no exchange; only one GPU's share runs here)", file=sys.stderr)
@@ -952,7 +957,7 @@ def main() -> int:
 
     def stats(per):
         per = sorted(per)
-        return per[len(per) // 2], per[len(per) // 10], per[(9 * len(per)) // 10]
+        return statistics.median(per), per[len(per) // 10], per[(9 * len(per)) // 10]
 
     # At least --warmup steps, in whole replays and no fewer than five (clocks and the
     # graphs' first-replay upload settle), and one replay of each remainder graph.
@@ -961,12 +966,18 @@ def main() -> int:
         run(kind, warm, timed=False)
         if rem:
             run(kind, rem, timed=False)
+    # The timed block is exactly --steps steps; it is repeated `repeats` times so that
+    # the headline is a median with a real spread (per block: total time / steps).
+    repeats = args.repeats
     torch.cuda.synchronize()
     t_start = time.perf_counter()
-    ms, per = run("step", args.steps)
+    blocks = [run("step", args.steps, timed=False)[0] for _ in range(repeats)]
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_start
-    ms_dec, per_dec = run("decode", args.steps)
+    blocks_dec = [run("decode", args.steps, timed=False)[0] for _ in range(repeats)]
+    per = [b * 1e3 / args.steps for b in blocks]
+    per_dec = [b * 1e3 / args.steps for b in blocks_dec]
+    ms = statistics.median(blocks)
 
     us_step, us_p10, us_p90 = stats(per)
     us_dec, us_dec_p10, us_dec_p90 = stats(per_dec)
@@ -988,13 +999,14 @@ def main() -> int:
         "us_per_layer_token": round(us_step, 3),
         "us_per_layer_token_p10": round(us_p10, 3),
         "us_per_layer_token_p90": round(us_p90, 3),
-        "timing": {"steps_requested": args.steps, "steps_timed": args.steps,
-                   "timed_ms_total": round(ms, 4), "mean_us_per_step": round(ms * 1e3 / args.steps, 3),
+        "timing": {"steps_requested": args.steps, "steps_per_block": args.steps, "repeats": repeats,
+                   "block_ms_median": round(ms, 4), "block_ms_all": [round(b, 4) for b in blocks],
                    "samples": len(per),
-                   "protocol": f"exactly --steps steps: graph replays of {graph_steps} steps "
-                               f"(8 rounds over {nl} rotated layer caches) plus one remainder replay, "
-                               "HIP events around each replay; value and us_per_layer_token are the "
-                               "median over the full replays (p10/p90 beside them)"},
+                   "protocol": f"a timed block is exactly --steps steps (graph replays of {graph_steps} "
+                               f"steps, 8 rounds over {nl} rotated layer caches, plus one replay of the "
+                               "remainder), HIP events around the block; the block runs --repeats times "
+                               "after the warmup; value and us_per_layer_token are the median over the "
+                               "blocks of block time / steps, p10/p90 beside them"},
         "pct_hbm_peak": round(100 * value / PEAK_HBM_GBS, 2),
         "higher_is_better": True,
         "scaling": "weak",

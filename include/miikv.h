@@ -67,8 +67,8 @@ enum { MIIKV_LAYOUT_CONTIGUOUS = 0, MIIKV_LAYOUT_PAGED = 1 };
  * plane holds the fp16 rows themselves in the same tiled element order (2 bytes per
  * element, twice the bytes of a q8 code plane) and has no scales (its scale pointer
  * may be NULL).  Every mode is accepted by append, decode, suffix attention,
- * export/import, the dequantising export and page copies; the fused append +
- * attention entry points and the session file store q8 rows only (MIIKV_KV_Q8_Q8,
+ * export/import, the dequantising export, page copies and session files; the fused
+ * append + attention entry points store q8 rows only (MIIKV_KV_Q8_Q8,
  * MIIKV_EUNSUPPORTED otherwise). */
 enum { MIIKV_KV_FP16_FP16 = 0, MIIKV_KV_Q8_FP16 = 1, MIIKV_KV_FP16_Q8 = 2, MIIKV_KV_Q8_Q8 = 3 };
 
@@ -507,13 +507,20 @@ miikv_status miikv_registry_set_layout_version(miikv_registry* reg, uint32_t ent
  * magic "MISS", version 20260928, followed by prefix_length u32 tokens, the
  * recurrent state bytes (per GDN layer: state then conv history, in segment
  * order) and the KV bytes (per attention layer the raw compact form of
- * src/prefill_v2/kv_cache.cpp:227-297: for each kv head K codes [P][D] then K
- * scales, then the same for V).  kv_quant_mode MIIKV_SESSION_KV_Q8_0_32 marks
- * scales per 32-value block ([P][D/32] fp16 per head), 2*P*Hkv*(D + D/16)
- * bytes per layer; the reference's per-row modes 0..3 are not produced here and
- * are rejected on load. */
+ * src/prefill_v2/kv_cache.cpp:227-297: for each kv head its K part -- fp16 rows
+ * [P][D], or q8 codes [P][D] then scales -- then the same for V).  kv_quant_mode
+ * is the cache's mode (persistent_session.cpp:54 writes the model's mode): an
+ * FP16_FP16 cache is written as the reference's mode 0 (kv_cache.hpp:16-21), byte
+ * for byte its raw format; a cache with a q8 plane holds one fp16 scale per
+ * 32-value block ([P][D/32] per head, where the reference's modes 1..3 hold one per
+ * row), so it gets a value of its own: MIIKV_SESSION_KV_Q8_0_32 (both planes q8),
+ * ..._Q8_0_32_FP16 (q8 K, fp16 V), ..._FP16_Q8_0_32 (fp16 K, q8 V).  The
+ * reference's per-row modes 1..3 are not produced here and are rejected on load. */
 #define MIIKV_SESSION_VERSION 20260928u
+#define MIIKV_SESSION_KV_FP16_FP16 0u
 #define MIIKV_SESSION_KV_Q8_0_32 4u
+#define MIIKV_SESSION_KV_Q8_0_32_FP16 5u
+#define MIIKV_SESSION_KV_FP16_Q8_0_32 6u
 #pragma pack(push, 1)
 typedef struct miikv_session_header {
     char magic[4];
@@ -531,6 +538,10 @@ typedef struct miikv_session_header {
     uint64_t created_timestamp;
 } miikv_session_header;
 #pragma pack(pop)
+
+/* The session-file kv_quant_mode written for a view quant mode (MIIKV_KV_*);
+ * 0xff for an unknown mode. */
+uint32_t miikv_session_kv_mode(uint32_t view_quant_mode);
 
 /* "sess_<16 hex digits of token_hash>_p<prefix_length>.miinfer" into out
  * (persistent_session.cpp:27-32).  Returns MIIKV_EINVAL if out_cap is short. */

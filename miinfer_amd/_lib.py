@@ -124,6 +124,7 @@ SIGNATURES = {
     "miikv_prefix_length": (_U32, [_P]),
     "miikv_prefix_hash": (_U64, [_P]),
     "miikv_prefix_set_layout_version": (None, [_P, _U32]),
+    "miikv_session_kv_mode": (_U32, [_U32]),
     "miikv_session_filename": (ctypes.c_int, [_U64, _U32, ctypes.c_char_p, ctypes.c_size_t]),
     "miikv_session_save": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _P, _U32, _P,
                                            _U32, _U32, _P, _P, _U32, _P]),

@@ -1,7 +1,7 @@
 // Persistent session files (.miinfer): the reference's on-disk prefix state
 // (include/miinfer/prefill_v2/persistent_session.hpp:18-69,
-// src/prefill_v2/persistent_session.cpp:27-320) for q8_0-32 caches in any
-// layout.  Host code over the HIP runtime: the KV bytes move through
+// src/prefill_v2/persistent_session.cpp:27-320) for caches of every quant mode in
+// any layout.  Host code over the HIP runtime: the KV bytes move through
 // miikv_export_canonical / miikv_import_canonical and one device staging buffer.
 #include <hip/hip_runtime_api.h>
 
@@ -23,8 +23,10 @@ namespace {
 constexpr char kMagic[4] = {'M', 'I', 'S', 'S'};
 
 struct Geometry {
-    uint32_t kv_heads = 0, head_dim = 0;
-    uint64_t layer_bytes = 0;  // 2 * P * Hkv * (D + 2 * D/32)
+    uint32_t kv_heads = 0, head_dim = 0, quant_mode = 0;
+    bool k_f16 = false, v_f16 = false;
+    uint64_t k_head = 0, v_head = 0;  // raw bytes of one head's K (V) part: rows, then scales
+    uint64_t layer_bytes = 0;         // kv_heads * (k_head + v_head)
 };
 
 uint64_t view_capacity(const miikv_view& v) {
@@ -32,23 +34,49 @@ uint64_t view_capacity(const miikv_view& v) {
                                           : static_cast<uint64_t>(v.page_tokens);
 }
 
-// Every layer must share one geometry (the file splits kv_bytes evenly,
-// persistent_session.cpp:251) and hold P tokens.
+bool is_f16_k(uint32_t mode) { return mode == MIIKV_KV_FP16_FP16 || mode == MIIKV_KV_FP16_Q8; }
+bool is_f16_v(uint32_t mode) { return mode == MIIKV_KV_FP16_FP16 || mode == MIIKV_KV_Q8_FP16; }
+
+}  // namespace
+
+// Session-file kv_quant_mode of a view quant mode, and back (0xff: none).
+extern "C" uint32_t miikv_session_kv_mode(uint32_t view_quant_mode) {
+    switch (view_quant_mode) {
+        case MIIKV_KV_FP16_FP16: return MIIKV_SESSION_KV_FP16_FP16;
+        case MIIKV_KV_Q8_FP16: return MIIKV_SESSION_KV_Q8_0_32_FP16;
+        case MIIKV_KV_FP16_Q8: return MIIKV_SESSION_KV_FP16_Q8_0_32;
+        case MIIKV_KV_Q8_Q8: return MIIKV_SESSION_KV_Q8_0_32;
+        default: return 0xffu;
+    }
+}
+
+namespace {
+
+// Every layer must share one geometry and quant mode (the file splits kv_bytes
+// evenly, persistent_session.cpp:251) and hold P tokens.
 bool layers_geometry(const miikv_view* layers, uint32_t count, uint32_t P, Geometry& g) {
     if (layers == nullptr || count == 0) return false;
     for (uint32_t i = 0; i < count; ++i) {
         const miikv_view& v = layers[i];
-        if (v.quant_mode != MIIKV_KV_Q8_Q8 || v.head_dim == 0 || v.head_dim % 32 != 0 || v.kv_heads == 0)
+        if (miikv_session_kv_mode(v.quant_mode) == 0xffu || v.head_dim == 0 || v.head_dim % 32 != 0 ||
+            v.kv_heads == 0)
             return false;
         if (i == 0) {
             g.kv_heads = v.kv_heads;
             g.head_dim = v.head_dim;
-        } else if (v.kv_heads != g.kv_heads || v.head_dim != g.head_dim) {
+            g.quant_mode = v.quant_mode;
+        } else if (v.kv_heads != g.kv_heads || v.head_dim != g.head_dim || v.quant_mode != g.quant_mode) {
             return false;
         }
         if (P > view_capacity(v)) return false;
     }
-    g.layer_bytes = 2ull * P * g.kv_heads * (g.head_dim + 2ull * (g.head_dim / 32));
+    g.k_f16 = is_f16_k(g.quant_mode);
+    g.v_f16 = is_f16_v(g.quant_mode);
+    const uint64_t rows16 = 2ull * P * g.head_dim;                       // fp16 rows
+    const uint64_t rows8 = static_cast<uint64_t>(P) * g.head_dim + 2ull * P * (g.head_dim / 32);  // codes + scales
+    g.k_head = g.k_f16 ? rows16 : rows8;
+    g.v_head = g.v_f16 ? rows16 : rows8;
+    g.layer_bytes = static_cast<uint64_t>(g.kv_heads) * (g.k_head + g.v_head);
     return true;
 }
 
@@ -71,30 +99,67 @@ struct Staging {
         if (base) (void)hipFree(base);
     }
     hipError_t alloc(uint32_t P, const Geometry& g) {
-        const size_t codes = static_cast<size_t>(P) * g.kv_heads * g.head_dim;
+        // an fp16 plane's rows take 2 bytes per element in the codes buffer
+        const size_t elems = static_cast<size_t>(P) * g.kv_heads * g.head_dim;
         const size_t scales = static_cast<size_t>(P) * g.kv_heads * (g.head_dim / 32) * 2;
-        const size_t c_al = (codes + 255) / 256 * 256, s_al = (scales + 255) / 256 * 256;
-        hipError_t e = hipMalloc(&base, 2 * (c_al + s_al));
+        const size_t kc_al = (elems * (g.k_f16 ? 2 : 1) + 255) / 256 * 256;
+        const size_t vc_al = (elems * (g.v_f16 ? 2 : 1) + 255) / 256 * 256;
+        const size_t s_al = (scales + 255) / 256 * 256;
+        hipError_t e = hipMalloc(&base, kc_al + vc_al + 2 * s_al);
         if (e != hipSuccess) return e;
         uint8_t* p = static_cast<uint8_t*>(base);
         kc = reinterpret_cast<int8_t*>(p);
-        ks = reinterpret_cast<uint16_t*>(p + c_al);
-        vc = reinterpret_cast<int8_t*>(p + c_al + s_al);
-        vs = reinterpret_cast<uint16_t*>(p + 2 * c_al + s_al);
+        ks = g.k_f16 ? nullptr : reinterpret_cast<uint16_t*>(p + kc_al);
+        vc = reinterpret_cast<int8_t*>(p + kc_al + s_al);
+        vs = g.v_f16 ? nullptr : reinterpret_cast<uint16_t*>(p + kc_al + s_al + vc_al);
         return hipSuccess;
     }
 };
 
-// Host offsets of head h's planes inside one layer's raw bytes.
+// Raw layout of one layer (kv_cache.cpp:227-297): for each kv head its K rows (fp16
+// [P][D], or q8 codes [P][D] then scales [P][D/32]), then the same for V.  Host offsets
+// of head h's parts and their device spans in the staging buffer.
 struct RawPlanes {
-    uint64_t k_codes, k_scales, v_codes, v_scales;
+    uint64_t k_rows, k_scales, v_rows, v_scales;  // file offsets
+    uint64_t k_row_bytes, v_row_bytes, scale_bytes;  // per head
 };
 RawPlanes raw_planes(uint32_t P, const Geometry& g, uint32_t h) {
-    const uint64_t codes = static_cast<uint64_t>(P) * g.head_dim;
-    const uint64_t scales = static_cast<uint64_t>(P) * (g.head_dim / 32) * 2;
-    const uint64_t per_head = codes + scales;
-    const uint64_t v0 = per_head * g.kv_heads;
-    return {per_head * h, per_head * h + codes, v0 + per_head * h, v0 + per_head * h + codes};
+    RawPlanes r;
+    r.k_row_bytes = static_cast<uint64_t>(P) * g.head_dim * (g.k_f16 ? 2 : 1);
+    r.v_row_bytes = static_cast<uint64_t>(P) * g.head_dim * (g.v_f16 ? 2 : 1);
+    r.scale_bytes = 2ull * P * (g.head_dim / 32);
+    const uint64_t v0 = g.k_head * g.kv_heads;
+    r.k_rows = g.k_head * h;
+    r.k_scales = r.k_rows + r.k_row_bytes;
+    r.v_rows = v0 + g.v_head * h;
+    r.v_scales = r.v_rows + r.v_row_bytes;
+    return r;
+}
+
+// One layer between the staging buffer and its raw bytes: device -> host (save) or
+// host -> device (load), for every head.
+hipError_t move_layer(const Staging& st, const Geometry& g, uint32_t P, uint8_t* raw, bool to_host, hipStream_t s) {
+    for (uint32_t hd = 0; hd < g.kv_heads; ++hd) {
+        const RawPlanes rp = raw_planes(P, g, hd);
+        struct Part {
+            uint8_t* dev;
+            uint64_t off, bytes;
+        } parts[4] = {
+            {reinterpret_cast<uint8_t*>(st.kc) + hd * rp.k_row_bytes, rp.k_rows, rp.k_row_bytes},
+            {g.k_f16 ? nullptr : reinterpret_cast<uint8_t*>(st.ks) + hd * rp.scale_bytes, rp.k_scales,
+             g.k_f16 ? 0 : rp.scale_bytes},
+            {reinterpret_cast<uint8_t*>(st.vc) + hd * rp.v_row_bytes, rp.v_rows, rp.v_row_bytes},
+            {g.v_f16 ? nullptr : reinterpret_cast<uint8_t*>(st.vs) + hd * rp.scale_bytes, rp.v_scales,
+             g.v_f16 ? 0 : rp.scale_bytes},
+        };
+        for (const Part& pt : parts) {
+            if (pt.bytes == 0) continue;
+            const hipError_t e = to_host ? hipMemcpyAsync(raw + pt.off, pt.dev, pt.bytes, hipMemcpyDeviceToHost, s)
+                                         : hipMemcpyAsync(pt.dev, raw + pt.off, pt.bytes, hipMemcpyHostToDevice, s);
+            if (e != hipSuccess) return e;
+        }
+    }
+    return hipSuccess;
 }
 
 int hip_fail(hipError_t e) { return -static_cast<int>(e); }
@@ -130,7 +195,7 @@ extern "C" miikv_status miikv_session_save(const char* path, const char* model_i
     h.gdn_layers = gdn_segment_count / 2;
     h.gdn_state_bytes = sum_bytes(gdn_segment_bytes, gdn_segment_count);
     h.gqa_layers = kv_layer_count;
-    h.kv_quant_mode = MIIKV_SESSION_KV_Q8_0_32;
+    h.kv_quant_mode = static_cast<uint8_t>(miikv_session_kv_mode(g.quant_mode));
     h.kv_bytes = g.layer_bytes * kv_layer_count;
     h.tokens_bytes = static_cast<uint64_t>(P) * sizeof(uint32_t);
     h.created_timestamp = static_cast<uint64_t>(std::time(nullptr));
@@ -147,23 +212,11 @@ extern "C" miikv_status miikv_session_save(const char* path, const char* model_i
     }
     Staging st;
     if (hipError_t e = st.alloc(P, g); e != hipSuccess) return hip_fail(e);
-    const size_t codes = static_cast<size_t>(P) * g.head_dim;
-    const size_t scales = static_cast<size_t>(P) * (g.head_dim / 32);
     for (uint32_t l = 0; l < kv_layer_count; ++l) {
         const int r = miikv_export_canonical(&kv_layers[l], seq, 0, P, st.kc, st.ks, st.vc, st.vs, stream);
         if (r != MIIKV_OK) return r;
-        uint8_t* dst = kv.data() + g.layer_bytes * l;
-        for (uint32_t hd = 0; hd < g.kv_heads; ++hd) {
-            const RawPlanes rp = raw_planes(P, g, hd);
-            hipError_t e = hipMemcpyAsync(dst + rp.k_codes, st.kc + hd * codes, codes, hipMemcpyDeviceToHost, s);
-            if (e == hipSuccess)
-                e = hipMemcpyAsync(dst + rp.k_scales, st.ks + hd * scales, scales * 2, hipMemcpyDeviceToHost, s);
-            if (e == hipSuccess)
-                e = hipMemcpyAsync(dst + rp.v_codes, st.vc + hd * codes, codes, hipMemcpyDeviceToHost, s);
-            if (e == hipSuccess)
-                e = hipMemcpyAsync(dst + rp.v_scales, st.vs + hd * scales, scales * 2, hipMemcpyDeviceToHost, s);
-            if (e != hipSuccess) return hip_fail(e);
-        }
+        if (hipError_t e = move_layer(st, g, P, kv.data() + g.layer_bytes * l, true, s); e != hipSuccess)
+            return hip_fail(e);
         // the staging buffer is reused by the next layer
         if (hipError_t e = hipStreamSynchronize(s); e != hipSuccess) return hip_fail(e);
     }
@@ -221,9 +274,10 @@ extern "C" int miikv_session_load(const char* path, const char* model_id, const 
     const uint32_t P = h.prefix_length;
     Geometry g;
     if (P == 0 || P > tokens_cap || h.gdn_layers * 2 != gdn_segment_count || h.gqa_layers != kv_layer_count ||
-        h.kv_quant_mode != MIIKV_SESSION_KV_Q8_0_32 || h.tokens_bytes != static_cast<uint64_t>(P) * 4 ||
+        h.tokens_bytes != static_cast<uint64_t>(P) * 4 ||
         h.gdn_state_bytes != sum_bytes(gdn_segment_bytes, gdn_segment_count) ||
-        !layers_geometry(kv_layers, kv_layer_count, P, g) || h.kv_bytes != g.layer_bytes * kv_layer_count)
+        !layers_geometry(kv_layers, kv_layer_count, P, g) || h.kv_bytes != g.layer_bytes * kv_layer_count ||
+        h.kv_quant_mode != miikv_session_kv_mode(g.quant_mode))
         return 0;
     std::vector<uint32_t> tokens(P);
     std::vector<uint8_t> gdn(h.gdn_state_bytes), kv(h.kv_bytes);
@@ -244,21 +298,9 @@ extern "C" int miikv_session_load(const char* path, const char* model_id, const 
     }
     Staging st;
     if (hipError_t e = st.alloc(P, g); e != hipSuccess) return hip_fail(e);
-    const size_t codes = static_cast<size_t>(P) * g.head_dim;
-    const size_t scales = static_cast<size_t>(P) * (g.head_dim / 32);
     for (uint32_t l = 0; l < kv_layer_count; ++l) {
-        const uint8_t* src = kv.data() + g.layer_bytes * l;
-        for (uint32_t hd = 0; hd < g.kv_heads; ++hd) {
-            const RawPlanes rp = raw_planes(P, g, hd);
-            hipError_t e = hipMemcpyAsync(st.kc + hd * codes, src + rp.k_codes, codes, hipMemcpyHostToDevice, s);
-            if (e == hipSuccess)
-                e = hipMemcpyAsync(st.ks + hd * scales, src + rp.k_scales, scales * 2, hipMemcpyHostToDevice, s);
-            if (e == hipSuccess)
-                e = hipMemcpyAsync(st.vc + hd * codes, src + rp.v_codes, codes, hipMemcpyHostToDevice, s);
-            if (e == hipSuccess)
-                e = hipMemcpyAsync(st.vs + hd * scales, src + rp.v_scales, scales * 2, hipMemcpyHostToDevice, s);
-            if (e != hipSuccess) return hip_fail(e);
-        }
+        if (hipError_t e = move_layer(st, g, P, kv.data() + g.layer_bytes * l, false, s); e != hipSuccess)
+            return hip_fail(e);
         const int r = miikv_import_canonical(&kv_layers[l], seq, 0, P, st.kc, st.ks, st.vc, st.vs, stream);
         if (r != MIIKV_OK) return r < 0 ? r : 0;
         if (hipError_t e = hipStreamSynchronize(s); e != hipSuccess) return hip_fail(e);

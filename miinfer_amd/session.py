@@ -1,6 +1,7 @@
 """Persistent session files (.miinfer) over the C ABI: save / inspect / load /
 find, the reference's PersistentSession
-(include/miinfer/prefill_v2/persistent_session.hpp:36-67) for q8_0-32 caches.
+(include/miinfer/prefill_v2/persistent_session.hpp:36-67) for caches of every quant mode
+(kv_quant_mode: the reference's 0 for FP16_FP16; 4, 5, 6 for the modes with q8_0-32 planes).
 """
 from __future__ import annotations
 
@@ -14,7 +15,10 @@ from .kv import KvCache, _stream
 from .reuse import RecurrentStates
 
 SESSION_VERSION = 20260928
+KV_FP16_FP16 = 0
 KV_Q8_0_32 = 4
+KV_Q8_0_32_FP16 = 5
+KV_FP16_Q8_0_32 = 6
 
 
 class SessionHeader(ctypes.Structure):

@@ -73,6 +73,43 @@ def test_suffix_config4_full_size_sampled_tokens(gpu, split):
         assert_attention_close(out[tok], expect, f"token {tok}")
 
 
+@pytest.mark.parametrize("split", [True, False])
+def test_suffix_config4_fused_store_full_size(gpu, split):
+    """Config 4 as bench.py times it: miikv_suffix_append_attn stores 512 fp16 suffix rows
+    over an 8192-token prefix (24q/4kv/D256) and attends.  All 512 stored rows (codes and
+    scales of every kv head, over slots that held other bytes) are bit-exact against the
+    oracle's quantisation, and two tokens of every 32-token block of the suffix, token 511
+    among them, match the oracle's attention."""
+    import miinfer_amd as m
+    hq, hk, d, prefix, t = 24, 4, 256, 8192, 512
+    rng = np.random.default_rng(44)
+    cap = prefix + t
+    k = randn_f16(rng, (cap, hk, d))
+    v = randn_f16(rng, (cap, hk, d))
+    cache = m.KvCache.contiguous(hk, d, cap)
+    junk = randn_f16(rng, (t, hk, d)) * np.float16(20)
+    cache.append(_dev(junk, gpu), _dev(junk, gpu), base_position=prefix)  # older bytes in the slots
+    cache.append(_dev(k[:prefix], gpu), _dev(v[:prefix], gpu), base_position=0)
+    q16 = randn_f16(rng, (t, hq, d))
+    out, _ = m.suffix_attention(cache, _dev(q16, gpu), prefix, split=split, k_new=_dev(k[prefix:], gpu),
+                                v_new=_dev(v[prefix:], gpu))
+    torch.cuda.synchronize()
+    kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+    vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+    got = _canon_all(cache, 0, cap)
+    for x, e, name in zip(got, (kc, ks.view(np.int16), vc, vs.view(np.int16)),
+                          ("k codes", "k scales", "v codes", "v scales")):
+        assert np.array_equal(x[:, prefix:], e[:, prefix:]), f"stored suffix {name}"
+        assert np.array_equal(x[:, :prefix], e[:, :prefix]), f"prefix {name}"
+    out = out.cpu().numpy()
+    toks = sorted({32 * j + (7 * j) % 32 for j in range(16)} | {32 * j + 31 - (5 * j) % 16 for j in range(16)}
+                  | {0, 511})
+    for tok in toks:
+        expect = oracle.attention_q8(q16[tok].astype(np.float32), kc, ks, vc, vs, prefix + tok + 1, hq,
+                                     1 / math.sqrt(d))
+        assert_attention_close(out[tok], expect, f"token {tok}")
+
+
 # (t, extra): 100 tokens run on the MFMA path, 3 as a batch of decodes
 @pytest.mark.parametrize("t,extra", [(100, 20), (3, 2)])
 @pytest.mark.parametrize("split", [True, False])

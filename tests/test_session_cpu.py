@@ -161,3 +161,12 @@ def test_load_rejects_random_corruption(tmp_path, seed):
                                        toks.ctypes.data_as(ctypes.c_void_p), 16, ctypes.byref(plen), None)
         assert r == 0 and plen.value == 0, (off, size)
         assert not np.any(toks)
+
+
+def test_session_kv_mode_values():
+    """File kv_quant_mode per view mode: FP16_FP16 keeps the reference's 0 (same raw bytes,
+    kv_cache.hpp:16-21); the modes with q8_0-32 planes (one scale per 32 values, not per
+    row as the reference's 1..3) get 4, 5, 6; unknown modes none."""
+    from miinfer_amd import _lib as L
+    f = L.lib().miikv_session_kv_mode
+    assert [f(m) for m in (L.KV_FP16_FP16, L.KV_Q8_FP16, L.KV_FP16_Q8, L.KV_Q8_Q8, 9)] == [0, 5, 6, 4, 0xff]
