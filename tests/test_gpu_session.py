@@ -19,7 +19,7 @@ def _dev(a, gpu):
 def _export(cache, seq, n):
     out = cache.export_canonical(seq, 0, n)
     torch.cuda.synchronize()
-    return [t.cpu().numpy().tobytes() for t in out]
+    return [None if t is None else t.cpu().numpy().tobytes() for t in out]
 
 
 def _paged(m, gpu, rng, hk, d, pages, pt=256):
