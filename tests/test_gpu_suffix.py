@@ -515,6 +515,34 @@ def test_suffix_mfma_path_rounds_fp32_query_to_fp16(gpu):
         assert_attention_close(o32, oracle.suffix_attention_q8(q32, *ref, prefix, hq, 1 / math.sqrt(d)), "fp32 q")
 
 
+@pytest.mark.parametrize("f32", [True, False])
+def test_suffix_mfma_accuracy_contract(gpu, f32):
+    """The MFMA route's stated accuracy (include/miikv.h, miikv_suffix_attn): its operands
+    are fp16 (the query rounded once, each tile element code * scale rounded once), which
+    keeps outputs within the attention tolerance (max-abs 2e-3, relative 1e-2) for logits
+    of standard deviation up to 2, and within max-abs 1.5e-2 and relative 2e-3 at standard
+    deviation 6; at that sharpness MIIKV_SUFFIX_EXACT is the route within the tolerance
+    (test_suffix_exact_route).  Measured here with queries x1 and x3 at scale 2/sqrt(D)."""
+    import miinfer_amd as m
+    from tests.helpers import attention_errors
+    hq, hk, d, prefix, t = 24, 4, 256, 3000, 256
+    rng = np.random.default_rng(91 + f32)
+    cache, ref = _setup(gpu, rng, hq, hk, d, prefix, t, ((prefix + t + 63) // 64) * 64)
+    scale = 2 / math.sqrt(d)
+    base = rng.standard_normal((t, hq, d))
+    for mult, atol, rtol in ((1.0, 2e-3, 1e-2), (3.0, 1.5e-2, 2e-3)):
+        q = (base * mult).astype(np.float32 if f32 else np.float16)
+        out, _ = m.suffix_attention(cache, _dev(q, gpu), prefix, scale, out=torch.empty((t, hq, d), device=gpu))
+        torch.cuda.synchronize()
+        expect = oracle.suffix_attention_q8(q.astype(np.float32), *ref, prefix, hq, scale)
+        logits_sd = float(np.std(q[:, :6].astype(np.float32).reshape(-1, d) @
+                                 (ref[0][0, :512].astype(np.float32) *
+                                  np.repeat(ref[1][0, :512].view(np.float16).astype(np.float32), 32, axis=1)).T) * scale)
+        max_abs, rel = attention_errors(out.cpu().numpy(), expect)
+        assert max_abs <= atol and rel <= rtol, (mult, logits_sd, max_abs, rel)
+        assert abs(logits_sd - 2 * mult) < 0.3 * mult, logits_sd
+
+
 # (t, q fp32, fused store + gate, device prefill state)
 @pytest.mark.parametrize("t,f32,fused,dev_state", [(96, True, False, False), (512, True, False, False),
                                                    (100, True, True, False), (70, False, False, True),
