@@ -291,6 +291,13 @@ miikv_status miikv_decode_append_attn_noalloc(const miikv_view* view, const uint
  * caches of at most 16384 positions, 6 above); longer ones run on MFMA over fp16
  * tiles expanded into the workspace.  miikv_suffix_workspace_bytes() covers both; a smaller workspace
  * that holds the tiles runs the MFMA path with one split.
+ * Accuracy of the MFMA path: its operands are fp16 (the query rounded once, each key
+ * and value element code * scale rounded once, the probabilities rounded once), which
+ * keeps outputs within max-abs 2e-3 and relative 1e-2 of fp32 attention over the same
+ * cache when the logits (scale * q.k) have a standard deviation up to 2, and within
+ * max-abs 1.5e-2 and relative 2e-3 up to 6.  Sharper attention that needs the
+ * reference's fp32 products takes MIIKV_SUFFIX_EXACT (miikv_suffix_attn_ex), within
+ * max-abs 2e-3 and relative 1e-2 there.
  * Replaces launch_qwen35_splitk_suffix_attention_quant
  * (include/miinfer/qwen3_gpu_primitives.hpp:670-693; kernels
  * gfx906/kernels/qwen3_primitives.hip:6789-7207, 6637-6725). */
