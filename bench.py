@@ -350,19 +350,19 @@ def bench_c4(dev, args) -> int:
 
     # Short suffixes over the same prefix (speculative-verify sizes), through the same
     # entry point: they run as a batch of decodes, several tokens per context pass.
-    short = {}
+    short, short32 = {}, {}
     for ts in (1, 2, 4, 8):
         ws_s = torch.empty(m.suffix_workspace_bytes(cache, hq, ts), dtype=torch.uint8, device=dev)
-        qs = q[:ts].contiguous()
         outs = out[:ts]
-
-        def attn_short(s, ts=ts, ws_s=ws_s, qs=qs, outs=outs):
-            assert L.miikv_suffix_attn(cache.view, P(qs.data_ptr()), _lib.DTYPE_F16, hq,
-                                       ctypes.c_float(1 / math.sqrt(d)), ts, prefix, 0, None,
-                                       P(outs.data_ptr()), None, None, P(ws_s.data_ptr()),
-                                       ws_s.numel(), P(s.cuda_stream)) == 0
-        short[f"T{ts}_us"] = round(sorted(_time_graph(attn_short, max(4, nrep // 24), 3, inner=8)[0]
-                                          for _ in range(3))[1], 2)
+        for dt, qs, res in ((_lib.DTYPE_F16, q[:ts].contiguous(), short),
+                            (_lib.DTYPE_F32, q[:ts].float().contiguous(), short32)):
+            def attn_short(s, ts=ts, ws_s=ws_s, qs=qs, outs=outs, dt=dt):
+                assert L.miikv_suffix_attn(cache.view, P(qs.data_ptr()), dt, hq,
+                                           ctypes.c_float(1 / math.sqrt(d)), ts, prefix, 0, None,
+                                           P(outs.data_ptr()), None, None, P(ws_s.data_ptr()),
+                                           ws_s.numel(), P(s.cuda_stream)) == 0
+            res[f"T{ts}_us"] = round(sorted(_time_graph(attn_short, max(4, nrep // 24), 3, inner=8)[0]
+                                            for _ in range(3))[1], 2)
     # The reference's own call arguments (attention_layer.cpp:297-343): fp32 q_rope,
     # gate and gated output, on the MFMA path.
     q32 = q.float()
@@ -407,6 +407,7 @@ def bench_c4(dev, args) -> int:
                         "GBs": round(prefix * append_bytes(hkv, d) / (us_bulk * 1e-6) / 1e9, 1)},
         "short_suffix": dict(short, note="miikv_suffix_attn with T tokens over the same 8192-token prefix "
                                          "(a batch of decodes, 2 tokens per context pass)"),
+        "short_suffix_f32_query": dict(short32, note="the same with an fp32 query (its low half kept)"),
         "reference_signature": {"us": round(us_ref, 2), "TFLOPs": round(flops / (us_ref * 1e-6) / 1e12, 2),
                                 "note": "miikv_suffix_attn with an fp32 query, gate and gated output (the "
                                         "reference's arguments), MFMA path"},

@@ -106,14 +106,19 @@ constexpr float kRescaleSlack = 6.0f;  // log2 units: p <= 64, and 64 * (65504/1
 
 // Streaming loads of cache codes: each byte is read once per launch, so they are
 // issued nontemporal (measured ~5% faster than cached loads at 32k context).
+// CACHED: row sets of one sequence (a suffix run as decodes) read the same keys, and
+// the workgroups of one XCD run the row sets of one key range together, so the codes
+// are loaded through the L2 for the other row sets to find.
+template <bool CACHED = false>
 __device__ __forceinline__ uint4 load16(const int8_t* p) {
     typedef unsigned int u4v __attribute__((ext_vector_type(4)));
-    const u4v t = __builtin_nontemporal_load(reinterpret_cast<const u4v*>(p));
+    const u4v t = CACHED ? *reinterpret_cast<const u4v*>(p) : __builtin_nontemporal_load(reinterpret_cast<const u4v*>(p));
     return make_uint4(t.x, t.y, t.z, t.w);
 }
+template <bool CACHED = false>
 __device__ __forceinline__ uint2 load8(const int8_t* p) {
     typedef unsigned int u2v __attribute__((ext_vector_type(2)));
-    const u2v t = __builtin_nontemporal_load(reinterpret_cast<const u2v*>(p));
+    const u2v t = CACHED ? *reinterpret_cast<const u2v*>(p) : __builtin_nontemporal_load(reinterpret_cast<const u2v*>(p));
     return make_uint2(t.x, t.y);
 }
 
@@ -341,7 +346,8 @@ constexpr uint32_t decode_waves_per_eu() {
 // per score (a constant DPP shift); the fp16-query register budget and occupancy then
 // hold.  Otherwise (G > 8) the lo parts are a second fragment set and a second MFMA per
 // block.
-template <uint32_t D, bool QF32, bool APPEND, bool KF16 = false, bool VF16 = false, bool QPAIR = false>
+template <uint32_t D, bool QF32, bool APPEND, bool KF16 = false, bool VF16 = false, bool QPAIR = false,
+          bool CACHED = false>
 __global__ void __launch_bounds__(64 * kWavesPerWg)
 __attribute__((amdgpu_waves_per_eu(decode_waves_per_eu<D, QF32 && !QPAIR, KF16, VF16>())))
 decode_kernel(SplitArgs a) {
@@ -378,7 +384,19 @@ decode_kernel(SplitArgs a) {
         }
     }
     uint32_t split, h, b;
-    if (a.batch == 1) {
+    if (a.rowset_order) {
+        // Row sets of one sequence: items (kv head, split, row set), row sets fastest,
+        // each XCD (workgroup i runs on XCD i % 8) a contiguous range of them, so the
+        // workgroups an XCD runs together read the same keys (through its L2).  The
+        // grid is padded to a multiple of 8; items past a row set's splits exit.
+        const uint32_t total = a.max_splits * a.g.kv_heads * a.batch;
+        const uint32_t k = (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8;
+        if (k >= total) return;
+        b = k % a.batch;
+        split = (k / a.batch) % a.max_splits;
+        h = k / a.batch / a.max_splits;
+        if (a.count_ptr != nullptr && b >= *a.count_ptr) return;
+    } else if (a.batch == 1) {
         b = 0;
         h = blockIdx.x / a.max_splits;
         split = blockIdx.x % a.max_splits;
@@ -435,20 +453,20 @@ decode_kernel(SplitArgs a) {
         // Scales first, each ahead of its codes: loads complete in issue order, so the
         // score MFMAs wait only for the K scales and codes while V is still in flight.
         if constexpr (!KF16)
-            st.ks = load_scales<ScaleVec, DecodeTuning<D, kLo>::nt_scales>(geo.k_scales + sc0 + lane * (NB / 2));
+            st.ks = load_scales<ScaleVec, DecodeTuning<D, kLo>::nt_scales && !CACHED>(geo.k_scales + sc0 + lane * (NB / 2));
 #pragma unroll
         for (uint32_t J = 0; J < 2; ++J)
 #pragma unroll
             for (uint32_t cc = 0; cc < NC; ++cc)
 #pragma unroll
                 for (uint32_t e = 0; e < KE; ++e)
-                    st.k[J][cc][e] = load16(kb + KE * (J * 16 * D + cc * 1024 + g4 * 256 + n * 16) + 16 * e);
+                    st.k[J][cc][e] = load16<CACHED>(kb + KE * (J * 16 * D + cc * 1024 + g4 * 256 + n * 16) + 16 * e);
         if constexpr (!VF16)
-            st.vs = load_scales<ScaleVec, DecodeTuning<D, kLo>::nt_scales>(geo.v_scales + sc0 + lane * (NB / 2));
+            st.vs = load_scales<ScaleVec, DecodeTuning<D, kLo>::nt_scales && !CACHED>(geo.v_scales + sc0 + lane * (NB / 2));
 #pragma unroll
         for (uint32_t mt = 0; mt < NM; ++mt) {
-            if constexpr (VF16) st.v[mt] = load16(vb + 2 * ((16 * mt + n) * 32 + g4 * 8));
-            else st.v[mt] = load8(vb + (16 * mt + n) * 32 + g4 * 8);
+            if constexpr (VF16) st.v[mt] = load16<CACHED>(vb + 2 * ((16 * mt + n) * 32 + g4 * 8));
+            else st.v[mt] = load8<CACHED>(vb + (16 * mt + n) * 32 + g4 * 8);
         }
         ld_tok += stride * kChunk;
         ld_tp += stride * kChunk;
@@ -818,8 +836,10 @@ struct Plan {
     uint64_t part_bytes;
 };
 
+// rowsets: row sets of one sequence (a suffix run as decodes), all of about the same
+// length: the host plan is the launch's (no device-side choice), XCD-ordered.
 Plan make_plan(const miikv_view* v, uint32_t q_heads, uint32_t batch, uint32_t max_context,
-               uint32_t cpw_cap = 64) {
+               uint32_t cpw_cap = 64, bool rowsets = false) {
     Plan p;
     const uint64_t chunks = (static_cast<uint64_t>(max_context) + kChunk - 1) / kChunk;
     const uint64_t waves = chunks * v->kv_heads * batch;
@@ -832,8 +852,8 @@ Plan make_plan(const miikv_view* v, uint32_t q_heads, uint32_t batch, uint32_t m
     // A batch: cpw is the floor of the device-side choice (launch_cpw), which
     // can only raise it; the records and the grid are sized for the floor, a
     // quarter of the all-sequences-full value.
-    if (batch > 1) cpw = (cpw + 3) / 4;
-    p.adaptive = batch > 1;
+    if (batch > 1 && !rowsets) cpw = (cpw + 3) / 4;
+    p.adaptive = batch > 1 && !rowsets;
     if (cpw < 1) cpw = 1;
     if (cpw > cpw_cap) cpw = cpw_cap;
     p.cpw = static_cast<uint32_t>(cpw);
@@ -890,6 +910,13 @@ extern "C" miikv_status miikv_workspace_init(void* workspace, uint64_t bytes, vo
 #define MIIKV_ROWSET_MAX_CPW 32
 #endif
 constexpr uint32_t kRowsetMaxCpw = MIIKV_ROWSET_MAX_CPW;
+// Columns a row set of an fp32 query may fill: 8 keeps its lo parts in the spare
+// columns (decode_kernel's QPAIR form); 16 packs twice the tokens with a second
+// fragment set.
+#ifndef MIIKV_ROWSET_COLS_F32
+#define MIIKV_ROWSET_COLS_F32 8
+#endif
+constexpr uint32_t kRowsetColsF32 = MIIKV_ROWSET_COLS_F32;
 #ifndef MIIKV_DECODE_QPAIR
 #define MIIKV_DECODE_QPAIR 1
 #endif
@@ -898,8 +925,20 @@ template <uint32_t D, bool F32, bool APP, bool KF, bool VF>
 void launch_decode_t(dim3 grid, size_t lds, hipStream_t s, const SplitArgs& a) {
     // An fp32 query of up to 8 heads per kv head pairs its lo parts into the spare columns
     // (at D = 256 the second fragment set would cost occupancy; at D = 128 it doubles the
-    // score MFMAs).
-    if (F32 && a.group <= 8 && MIIKV_DECODE_QPAIR)
+    // score MFMAs).  Row sets of one sequence over q8 planes load through the L2.
+    const bool pair = F32 && a.group <= 8 && MIIKV_DECODE_QPAIR;
+    if constexpr (!APP && !KF && !VF) {
+        if (a.rowset_order) {
+            if (pair)
+                hipLaunchKernelGGL((decode_kernel<D, F32, false, false, false, F32, true>), grid, dim3(64 * kWavesPerWg),
+                                   lds, s, a);
+            else
+                hipLaunchKernelGGL((decode_kernel<D, F32, false, false, false, false, true>), grid,
+                                   dim3(64 * kWavesPerWg), lds, s, a);
+            return;
+        }
+    }
+    if (pair)
         hipLaunchKernelGGL((decode_kernel<D, F32, APP, KF, VF, F32>), grid, dim3(64 * kWavesPerWg), lds, s, a);
     else
         hipLaunchKernelGGL((decode_kernel<D, F32, APP, KF, VF, false>), grid, dim3(64 * kWavesPerWg), lds, s, a);
@@ -985,7 +1024,8 @@ static miikv_status decode_impl(const miikv_view* view, const NewRows& rows,
     if (rows.any() && view->quant_mode != MIIKV_KV_Q8_Q8) return MIIKV_EUNSUPPORTED;
     if (rows.k_norm_weight != nullptr && (!std::isfinite(rows.theta) || !std::isfinite(rows.epsilon)))
         return MIIKV_EINVAL;
-    const Plan p = make_plan(view, q_heads * pack, batch, max_context, rs != nullptr ? kRowsetMaxCpw : 64u);
+    const Plan p = make_plan(view, q_heads * pack, batch, max_context, rs != nullptr ? kRowsetMaxCpw : 64u,
+                             rs != nullptr);
     if (workspace == nullptr || workspace_bytes < p.counter_bytes + p.part_bytes) return MIIKV_EWORKSPACE;
     if (p.splits > 65535u || batch > 65535u || static_cast<uint64_t>(batch) * view->kv_heads > 0x7fffffffu)
         return MIIKV_EINVAL;
@@ -1005,6 +1045,7 @@ static miikv_status decode_impl(const miikv_view* view, const NewRows& rows,
     // sized for the host's floor; exact suffix route at config 4: 1372 us at 64,
     // 1000 at 32, 1055 at 16); decode batches of distinct sequences keep 64.
     a.max_cpw = rs != nullptr ? kRowsetMaxCpw : 64u;
+    a.rowset_order = rs != nullptr ? 1u : 0u;
     if (rs != nullptr) {  // row set b: len_add + b * pack (its last token's context)
         a.len_ptr = rs->len_ptr;
         a.len_stride = 0;
@@ -1045,8 +1086,9 @@ static miikv_status decode_impl(const miikv_view* view, const NewRows& rows,
     if (lds > 64 * 1024) return MIIKV_EUNSUPPORTED;
     // One workgroup per possible (sequence, kv head, split) work item, plus one per
     // (sequence, kv head) for the new token of the fused append.
-    const uint64_t wgs = static_cast<uint64_t>(p.splits) * view->kv_heads * batch +
-                         (rows.any() ? static_cast<uint64_t>(view->kv_heads) * batch : 0);
+    uint64_t wgs = static_cast<uint64_t>(p.splits) * view->kv_heads * batch +
+                   (rows.any() ? static_cast<uint64_t>(view->kv_heads) * batch : 0);
+    if (rs != nullptr) wgs = (wgs + 7) / 8 * 8;  // XCD-ordered items: a whole number of rounds over the XCDs
     if (wgs > 0x7fffffffu) return MIIKV_EINVAL;
     a.batch = batch;
     a.slots = p.adaptive ? resident_workgroups(view->head_dim, q_dtype == MIIKV_DTYPE_F32 && (view->head_dim == 128 || 2 * G > 16), view->quant_mode) : 0u;
@@ -1089,20 +1131,27 @@ namespace miikv {
 // token count, 1.
 bool decode_columns_fit(uint32_t G, uint32_t D) { return G <= 16 && decode_lds_bytes(G, D) <= 64 * 1024; }
 
-uint32_t suffix_pack(const miikv_view* view, uint32_t q_heads, uint32_t token_count, bool device_count) {
+// max_cols: 16 (the MFMA's columns), or 8 for an fp32 query, whose lo parts then ride
+// in the other 8 columns (one MFMA per block at the fp16-query register budget).
+uint32_t suffix_pack(const miikv_view* view, uint32_t q_heads, uint32_t token_count, bool device_count,
+                     uint32_t max_cols) {
     const uint32_t G = q_heads / view->kv_heads;
     if (device_count || G == 0 || G > 16) return 1;
-    for (uint32_t p = std::min<uint32_t>(16 / G, token_count); p > 1; --p)
+    for (uint32_t p = std::min<uint32_t>(max_cols / G, token_count); p > 1; --p)
         if (token_count % p == 0 && decode_lds_bytes(p * G, view->head_dim) <= 64 * 1024) return p;
     return 1;
 }
 
 uint64_t suffix_by_decode_bytes(const miikv_view* view, uint32_t q_heads, uint32_t token_count, uint32_t bound) {
-    // the larger of the packed (host token count) and unpacked (device count) plans
-    const uint32_t pk = suffix_pack(view, q_heads, token_count, false);
-    const Plan p1 = make_plan(view, q_heads, token_count, bound, kRowsetMaxCpw);
-    const Plan pp = make_plan(view, q_heads * pk, token_count / pk, bound, kRowsetMaxCpw);
-    return std::max(p1.counter_bytes + p1.part_bytes, pp.counter_bytes + pp.part_bytes);
+    // the largest of the packed plans (fp16 and fp32 queries, host token count) and the
+    // unpacked one (device count)
+    uint64_t most = 0;
+    for (const uint32_t pk : {1u, suffix_pack(view, q_heads, token_count, false, 16),
+                              suffix_pack(view, q_heads, token_count, false, kRowsetColsF32)}) {
+        const Plan p = make_plan(view, q_heads * pk, token_count / pk, bound, kRowsetMaxCpw, true);
+        most = std::max(most, p.counter_bytes + p.part_bytes);
+    }
+    return most;
 }
 
 miikv_status suffix_by_decode(const miikv_view* view, const void* q, uint32_t q_dtype, uint32_t q_heads, float scale,
@@ -1114,7 +1163,13 @@ miikv_status suffix_by_decode(const miikv_view* view, const void* q, uint32_t q_
     rs.len_add = prefill_state ? 1u : base_position + 1u;
     rs.count_ptr = prefill_state ? &prefill_state->token_count : nullptr;
     rs.seq = seq;
-    rs.pack = suffix_pack(view, q_heads, token_count, prefill_state != nullptr);
+    // An fp32 query of 4..16 tokens fills 8 columns per row set, its lo parts in the
+    // other 8 (more row sets at two waves per SIMD: config 4 shape, T = 4 / 8: 26.5 /
+    // 31.7 -> 20.4 / 26.1 us); fewer or more tokens pack 16 columns with a second
+    // fragment set (T = 2: 16.6 against 17.2 us; the exact route at T = 512: 790
+    // against 963 us, where twice the row sets' operand conversions cost more).
+    const bool pair_cols = q_dtype == MIIKV_DTYPE_F32 && token_count >= 4 && token_count <= 16;
+    rs.pack = suffix_pack(view, q_heads, token_count, prefill_state != nullptr, pair_cols ? kRowsetColsF32 : 16u);
     return decode_impl(view, NewRows{}, q, q_dtype, q_heads, scale, token_count, nullptr, nullptr, bound, out, gate,
                        gated_out, nullptr, workspace, workspace_bytes, stream, &rs);
 }

@@ -53,6 +53,7 @@ struct SplitArgs {
     float rope_step;        // theta^(-2/64), from the host
     float epsilon;
     uint32_t q_f32;         // q dtype (scoring the appended token)
+    uint32_t rowset_order;  // row sets of one sequence: XCD-ordered (kv head, split, row set) items
 };
 
 

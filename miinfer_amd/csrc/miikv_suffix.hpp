@@ -23,7 +23,8 @@ constexpr uint32_t kSufMaxSplits = 64;
 constexpr uint32_t kSuffixDecodeMaxRows = 6;
 constexpr uint32_t kSuffixDecodeMaxRowsShort = 12;
 constexpr uint32_t kSuffixDecodeMaxT = 64;
-uint32_t suffix_pack(const miikv_view* view, uint32_t q_heads, uint32_t token_count, bool device_count);
+uint32_t suffix_pack(const miikv_view* view, uint32_t q_heads, uint32_t token_count, bool device_count,
+                     uint32_t max_cols = 16);
 bool decode_columns_fit(uint32_t G, uint32_t D);  // decode_kernel serves G columns at head_dim D
 uint64_t suffix_by_decode_bytes(const miikv_view* view, uint32_t q_heads, uint32_t token_count, uint32_t bound);
 miikv_status suffix_by_decode(const miikv_view* view, const void* q, uint32_t q_dtype, uint32_t q_heads, float scale,

@@ -594,11 +594,13 @@ def test_suffix_exact_route_errors(gpu):
     assert err.value.status == _lib.MIIKV_EUNSUPPORTED
     c4 = m.KvCache.contiguous(4, 256, 1024)
     c4.append(_dev(np.zeros((600, 4, 256), np.float16), gpu), _dev(np.zeros((600, 4, 256), np.float16), gpu))
-    q4 = torch.zeros((64, 24, 256), device=gpu)
-    small = torch.empty(m.suffix_workspace_bytes(c4, 24, 64), dtype=torch.uint8, device=gpu)
-    assert m.suffix_workspace_bytes(c4, 24, 64, exact=True) > small.numel()
+    # 512 tokens over 88: a workspace of just the context's fp16 tiles runs the MFMA
+    # path (one split) but cannot hold the exact route's decode records
+    q4 = torch.zeros((512, 24, 256), device=gpu)
+    small = torch.empty(4 * ((600 + 31) // 32) * 2 * 256 * 32 * 2, dtype=torch.uint8, device=gpu)
+    m.suffix_attention(c4, q4, 88, workspace=small)
     with pytest.raises(_lib.MiikvError) as err:  # never falls back to the MFMA path
-        m.suffix_attention(c4, q4, 536, exact=True, workspace=small)
+        m.suffix_attention(c4, q4, 88, exact=True, workspace=small)
     assert err.value.status == _lib.MIIKV_EWORKSPACE
 
 
