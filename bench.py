@@ -412,8 +412,9 @@ def bench_c4(dev, args) -> int:
                                 "note": "miikv_suffix_attn with an fp32 query, gate and gated output (the "
                                         "reference's arguments), MFMA path"},
         "exact_route": {"us": round(us_exact, 2), "TFLOPs": round(flops / (us_exact * 1e-6) / 1e12, 2),
-                        "note": "miikv_suffix_attn_ex with MIIKV_SUFFIX_EXACT and an fp32 query: every token as a "
-                                "decode (the query's low half kept, block scales in fp32)"},
+                        "note": "miikv_suffix_attn_ex with MIIKV_SUFFIX_EXACT and an fp32 query: the exact-product "
+                                "MFMA kernels (key codes exact with the block scales in fp32, the query's low half in "
+                                "the spare MFMA columns)"},
         "reference_ladder": ladder,
         "chunked_prefill": chunked,
     }), flush=True)

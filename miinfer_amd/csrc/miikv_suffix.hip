@@ -532,6 +532,349 @@ __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
         }
 }
 
+// ---- exact products on MFMA (MIIKV_SUFFIX_EXACT for long suffixes) -------------
+//
+// The reference multiplies an fp32 query with the dequantised keys in fp32.  Here the
+// scores are exact in the same sense as decode's: the key tiles hold the int8 codes
+// as fp16 (exact), each 32-value block's dot product comes out of its own pair of
+// v_mfma_f32_32x32x16_f16 and is multiplied by the block's fp16 scale in fp32, and
+// the query is split into fp16 hi + lo parts, which ride in the MFMA's columns 16..31
+// (column 16 + r holds the lo part of row r) and are added to the hi column by a
+// 16-lane swap.  A wave therefore serves 16 query rows.  The values enter as their
+// codes (fp16, exact), and each 32-value block's scale multiplies the probabilities
+// in fp32, the product rounded to fp16 once, as on the decode path; O^T += V^T P^T
+// runs as v_mfma_f32_16x16x32_f16 over the 16 real columns, one MFMA per 16 dims
+// with the P^T of their block (a wave holds O^T in 64 registers).
+//
+// Step record of the exact tiles (halves): K codes as fp16 in the K^ fragment layout
+// of expand_kernel [D/16][64 lanes][8]; the K block scales [D/32 blocks][2 hh][16],
+// entry (b, hh, 4j + i) the scale of key 8j + 4hh + i, the keys a lane of the score
+// accumulator holds in register order; the V block scales [D/32 blocks][4 g][8 e],
+// entry (b, g, e) the scale of key ex_key(g, e) (0 past the context end); V^T code
+// fragments of the 16x16x32 MFMA [D/16 dim tiles][64 lanes][8]: lane (g, i) = 16g + i
+// holds dim 16m + i of keys ex_key(g, e), e < 8, as fp16.  The key order of a V
+// fragment is the order in which the score accumulator's registers reach the PV B
+// operand: lane 16g + i takes registers 8(g & 1) .. +7 of its column (its 32-lane half
+// hh = g >> 1).
+__host__ __device__ constexpr uint32_t ex_tile_halves(uint32_t D) { return 64 * D + 64 * (D / 32); }
+__device__ __forceinline__ uint32_t ex_key(uint32_t g, uint32_t e) {
+    return 16 * (g & 1) + 8 * (e >> 2) + 4 * (g >> 1) + (e & 3);
+}
+
+// One 32-key step of kv head blockIdx.y into the exact tile layout (q8 planes only);
+// keys at or past the context end become 0.
+template <uint32_t D>
+__global__ void __launch_bounds__(256) expand_exact_kernel(ExpandArgs a) {
+    constexpr uint32_t NB = D / 32;
+    constexpr uint32_t PER = D / 64;  // fragment lanes per thread, per operand
+    __shared__ __align__(16) _Float16 s_vs[NB * kSufStep];  // [block][key]
+    const Geo& geo = a.g;
+    const uint32_t step = a.step0 + blockIdx.x;
+    const uint32_t h = blockIdx.y;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t nkeys = context_keys(a.key_count, a.ps);
+    const uint32_t tok0 = step * kSufStep;
+    if (tok0 >= nkeys) return;
+    const size_t slab = slab_of(geo, a.seq, tok0, h);
+    const uint32_t tp0 = tok0 % geo.page_tokens;
+    const size_t sc0 = (slab * geo.page_tokens + tp0) * NB;
+    const size_t cb = slab * static_cast<size_t>(geo.page_tokens) * D + static_cast<size_t>(tp0) * D;
+    const int8_t* kb = geo.k_codes + cb;
+    const int8_t* vb = geo.v_codes + cb;
+    const uint16_t* ksc = geo.k_scales + sc0;
+    const uint16_t* vsc = geo.v_scales + sc0;
+    if (tid < kSufStep * NB) {
+        const uint32_t key = tid / NB, blk = tid % NB;
+        s_vs[blk * kSufStep + key] = tok0 + key < nkeys ? __builtin_bit_cast(_Float16, vsc[tid]) : (_Float16)0.0f;
+    }
+    __syncthreads();
+    _Float16* out = a.tiles + (static_cast<size_t>(h) * a.steps + step) * ex_tile_halves(D);
+    // K codes: fragment c, lane (n, hh): key n, dims 16c + 8hh .. +7 (offsets as in expand_kernel)
+#pragma unroll
+    for (uint32_t u = 0; u < PER; ++u) {
+        const uint32_t fl = tid + 256 * u;
+        const uint32_t c = fl / 64, l = fl % 64, n = l % 32, hh = l / 32;
+        const uint32_t off = (n / 16) * 16 * D + (c / 4) * 1024 + (2 * (c % 2) + hh) * 256 + (n % 16) * 16 +
+                             ((c % 4) / 2) * 8;
+        const uint2 w = *reinterpret_cast<const uint2*>(kb + off);
+        *reinterpret_cast<half8*>(out + 8 * fl) = tok0 + n < nkeys ? codes8_to_half8(w.x, w.y) : half8{};
+    }
+    // K scales [b][hh][4j + i] = scale of key 8j + 4hh + i, block b (raw fp16)
+    _Float16* osc = out + 32 * D;
+    if (tid < 32 * NB) {
+        const uint32_t b = tid / 32, hh = (tid / 16) & 1, r = tid & 15;
+        const uint32_t key = 8 * (r >> 2) + 4 * hh + (r & 3);
+        osc[tid] = tok0 + key < nkeys ? __builtin_bit_cast(_Float16, ksc[key * NB + b]) : (_Float16)0.0f;
+    }
+    // V block scales [b][g][e] = scale of key ex_key(g, e), block b (0 past the context)
+    _Float16* ovs = osc + 32 * NB;
+    if (tid < 32 * NB) {
+        const uint32_t b = tid / 32, g = (tid / 8) & 3, e = tid & 7;
+        ovs[tid] = s_vs[b * kSufStep + ex_key(g, e)];
+    }
+    // V^T code fragments: dim tile m, lane (g, i): dim 16m + i, keys ex_key(g, 0..7).
+    // Keys ex_key(g, 0..3) are t = 16(g & 1) + 4(g >> 1) + 0..3, i.e. J = g & 1, G = g >> 1
+    // in the cache group's order (code of key 16J + 4G + I of dim d at d*32 + 8G + 4J +
+    // I), and ex_key(g, 4..7) the same with G + 2.  Codes past the context end are read
+    // as they are: their scale is 0.
+    _Float16* ov = ovs + 32 * NB;
+#pragma unroll
+    for (uint32_t u = 0; u < PER; ++u) {
+        const uint32_t fl = tid + 256 * u;
+        const uint32_t m = fl / 64, l = fl % 64, g = l / 16, i = l % 16;
+        const int8_t* vd = vb + (16 * m + i) * 32 + 4 * (g & 1);
+        const uint32_t w0 = *reinterpret_cast<const uint32_t*>(vd + 8 * (g >> 1));
+        const uint32_t w1 = *reinterpret_cast<const uint32_t*>(vd + 8 * (2 + (g >> 1)));
+        *reinterpret_cast<half8*>(ov + 8 * fl) = codes8_to_half8(w0, w1);
+    }
+}
+
+constexpr uint32_t kExWaves = 8;
+constexpr uint32_t kExRows = 16 * kExWaves;  // query rows per workgroup
+constexpr uint32_t kExDist = 2;              // prefetch distance in steps
+constexpr uint32_t kExBufs = kExDist + 1;    // LDS step buffers
+
+template <uint32_t D>
+__global__ void __launch_bounds__(64 * kExWaves) suffix_exact_kernel(SuffixArgs a) {
+    constexpr uint32_t NB = D / 32;          // q8 blocks (score block pairs)
+    constexpr uint32_t NC = D / 16;          // QK k-chunks
+    constexpr uint32_t NM = D / 16;          // PV dim tiles
+    constexpr uint32_t REC = ex_tile_halves(D);
+    constexpr uint32_t KV_CHUNKS = 64 * D * 2 / 1024;  // 1 KiB chunks of K codes + V^T
+    static_assert(KV_CHUNKS % kExWaves == 0, "copy chunks must split evenly over waves");
+    constexpr uint32_t kPer = KV_CHUNKS / kExWaves + 1;  // loads per wave per fetch (+1: the scales)
+    constexpr uint32_t SC_LANES = 128 * NB / 16 / kExWaves;  // 16-byte scale pieces per wave
+    __shared__ __align__(16) _Float16 s_t[kExBufs][REC];
+    static_assert(sizeof(s_t) <= 128u * 1024u, "exact suffix LDS must stay within 128 KiB");
+
+    uint32_t T = a.token_count;
+    uint32_t P = a.base_position;
+    if (a.ps != nullptr) {
+        P = a.ps->base_position;
+        T = min(T, a.ps->token_count);
+    }
+    const uint32_t G = a.group;
+    const uint32_t L = blockIdx.x;
+    const uint32_t per_xcd = gridDim.x / 8;
+    const uint32_t idx = (L % 8) * per_xcd + L / 8;
+    const uint32_t grp = idx / a.row_blocks;
+    if (grp >= a.g.kv_heads * a.splits) return;
+    const uint32_t h = grp % a.g.kv_heads;
+    const uint32_t split = grp / a.g.kv_heads;
+    const uint32_t rb = idx % a.row_blocks;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t wave = tid >> 6;
+    const uint32_t lane = tid & 63;
+    const uint32_t n = lane & 31;   // score column
+    const uint32_t hh = lane >> 5;
+    const uint32_t ci = lane & 15;  // PV column / row of the wave
+    const uint32_t gq = lane >> 4;  // PV lane group
+    const uint32_t rows = T * G;
+    const uint32_t r0 = rb * kExRows;
+    if (r0 >= rows) return;
+
+    // score lane (n, hh): column n, i.e. row n & 15 of the wave, hi part (n < 16) or lo
+    const uint32_t row = r0 + wave * 16 + (n & 15);
+    const bool row_ok = row < rows;
+    const uint32_t t_row = row_ok ? row / G : 0;
+    const uint32_t qh = h * G + (row_ok ? row % G : 0);
+    const uint32_t lim = P + t_row;  // last visible key (inclusive) of this lane's row
+    const uint32_t wave_lim = P + min(r0 + wave * 16, rows - 1) / G;
+
+    const uint32_t last_row = min(r0 + kExRows, rows) - 1;
+    const uint32_t nkeys = P + last_row / G + 1;
+    const uint32_t key_lo = split * a.split_keys;
+    if (key_lo >= nkeys) return;
+    const uint32_t key_hi = min(nkeys, key_lo + a.split_keys);
+    const uint32_t s_begin = key_lo / kSufStep;
+    const uint32_t s_end = (key_hi + kSufStep - 1) / kSufStep;
+
+    // ---- Q^T fragments: column n, dims 16c + 8hh .. +7: hi parts (n < 16) or lo parts
+    half8 qf[NC];
+    {
+        const size_t qrow = (static_cast<size_t>(t_row) * a.q_heads + qh) * D;
+        const bool lo = n >= 16;
+        if (a.q_f32) {
+#pragma unroll
+            for (uint32_t c0 = 0; c0 < NC; c0 += 4) {
+                float4 x[4][2];
+#pragma unroll
+                for (uint32_t j = 0; j < 4; ++j) {
+                    const float* qp = static_cast<const float*>(a.q) + qrow + (c0 + j) * 16 + hh * 8;
+                    x[j][0] = *reinterpret_cast<const float4*>(qp);
+                    x[j][1] = *reinterpret_cast<const float4*>(qp + 4);
+                }
+#pragma unroll
+                for (uint32_t j = 0; j < 4; ++j) {
+                    const float xs[8] = {x[j][0].x, x[j][0].y, x[j][0].z, x[j][0].w,
+                                         x[j][1].x, x[j][1].y, x[j][1].z, x[j][1].w};
+                    half8 v;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const _Float16 hi = static_cast<_Float16>(xs[e]);
+                        v[e] = lo ? static_cast<_Float16>(xs[e] - static_cast<float>(hi)) : hi;
+                    }
+                    qf[c0 + j] = row_ok ? v : half8{};
+                }
+            }
+        } else {
+#pragma unroll
+            for (uint32_t c = 0; c < NC; ++c) {
+                const uint16_t* qp = static_cast<const uint16_t*>(a.q) + qrow + c * 16 + hh * 8;
+                const half8 v = __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(qp));
+                qf[c] = row_ok && !lo ? v : half8{};  // an fp16 query has no lo part
+            }
+        }
+    }
+
+    const char* tiles_h = reinterpret_cast<const char*>(a.tiles + static_cast<size_t>(h) * a.steps * REC);
+    auto fetch = [&](uint32_t s, uint32_t b) {
+        const char* src = tiles_h + static_cast<size_t>(s) * REC * 2;
+        char* dst = reinterpret_cast<char*>(s_t[b]);
+        // K codes (32*D halves) and V^T codes (32*D halves) as 1 KiB chunks, and the K and
+        // V scales between them (128*NB bytes) as 16-byte pieces, SC_LANES per wave
+#pragma unroll
+        for (uint32_t u = 0; u < KV_CHUNKS / kExWaves; ++u) {
+            const uint32_t chunk = wave + kExWaves * u;
+            const uint32_t off = chunk < KV_CHUNKS / 2 ? chunk * 1024 : chunk * 1024 + 128 * NB;
+            __builtin_amdgcn_global_load_lds(src + off + lane * 16, dst + off, 16, 0, 0);
+        }
+        const uint32_t soff = 64 * D + wave * SC_LANES * 16;
+        if (lane < SC_LANES) __builtin_amdgcn_global_load_lds(src + soff + lane * 16, dst + soff, 16, 0, 0);
+    };
+
+    float m_run = -INFINITY;
+    float l_run = 0.0f;
+    float4v O[NM];
+#pragma unroll
+    for (uint32_t m = 0; m < NM; ++m) O[m] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (uint32_t k = 0; k < kExDist; ++k)
+        if (s_begin + k < s_end) fetch(s_begin + k, (s_begin + k) % kExBufs);
+    wait_vmem();
+    __syncthreads();
+
+    for (uint32_t s = s_begin; s < s_end; ++s) {
+        if (s + kExDist < s_end) fetch(s + kExDist, (s + kExDist) % kExBufs);
+        const _Float16* tb = s_t[s % kExBufs];
+        // ---- scores: one pair of MFMAs per q8 block, the block scale applied in fp32
+        float16v S = {};
+        const _Float16* tk = tb + lane * 8;
+        const _Float16* tsc = tb + 32 * D + hh * 16;
+#pragma unroll
+        for (uint32_t b = 0; b < NB; ++b) {
+            float16v c = {};
+            c = mfma_32x32x16(*reinterpret_cast<const half8*>(tk + 512 * (2 * b)), qf[2 * b], c);
+            c = mfma_32x32x16(*reinterpret_cast<const half8*>(tk + 512 * (2 * b + 1)), qf[2 * b + 1], c);
+            const half8 s0 = *reinterpret_cast<const half8*>(tsc + 32 * b);
+            const half8 s1 = *reinterpret_cast<const half8*>(tsc + 32 * b + 8);
+#pragma unroll
+            for (uint32_t r = 0; r < 8; ++r) {
+                S[r] = fmaf(c[r], static_cast<float>(s0[r]), S[r]);
+                S[8 + r] = fmaf(c[8 + r], static_cast<float>(s1[r]), S[8 + r]);
+            }
+        }
+        // hi column + lo column (16 lanes apart): both lanes end with the row's score
+#pragma unroll
+        for (uint32_t r = 0; r < 16; ++r) S[r] = swap16_reduce(S[r], AddOp{});
+        // ---- mask and online softmax of this lane's 16 keys (8j + 4hh + i) of its row
+        const uint32_t key0 = s * kSufStep;
+        if (key0 + kSufStep - 1 > wave_lim || key0 + kSufStep > key_hi) {
+#pragma unroll
+            for (uint32_t r = 0; r < 16; ++r) {
+                const uint32_t key = key0 + 8 * (r / 4) + 4 * hh + (r % 4);
+                if (!(key <= lim && key < key_hi)) S[r] = -INFINITY;
+            }
+        }
+        float cmax = S[0];
+#pragma unroll
+        for (uint32_t r = 1; r < 16; ++r) cmax = fmaxf(cmax, S[r]);
+        cmax = swap32_reduce(cmax, MaxOp{});  // the row's 32 keys (lanes n and n + 32)
+        const float cm = cmax * a.scale_log2;
+        const bool grow = cm > m_run + kSlackS;
+        if (__any(grow)) {
+            const float m_new = grow ? cm : m_run;
+            const float alpha = sfx_exp2(m_run - m_new);
+            m_run = m_new;
+            l_run *= alpha;
+#pragma unroll
+            for (uint32_t m = 0; m < NM; ++m) O[m] *= alpha;
+        }
+        const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+        // PV B operand of lane (gq, ci): its column's registers 8(gq & 1) .. +7
+        const bool upper = (gq & 1) != 0;
+        float pf[8];
+        float psum = 0.0f;
+#pragma unroll
+        for (uint32_t e = 0; e < 8; ++e) {
+            const float x = upper ? S[8 + e] : S[e];
+            pf[e] = sfx_exp2(fmaf(x, a.scale_log2, -m_use));
+            psum += pf[e];
+        }
+        l_run += psum;
+        // ---- O^T += V^T P^T per 16 dims, P^T scaled by their block's V scales (fp32
+        // product, rounded to fp16 once)
+        const _Float16* tvs = tb + 32 * D + 32 * NB + gq * 8;
+        const _Float16* tv = tb + 32 * D + 64 * NB + lane * 8;
+#pragma unroll
+        for (uint32_t b = 0; b < NB; ++b) {
+            const half8 vs = *reinterpret_cast<const half8*>(tvs + 32 * b);
+            half8 pb;
+#pragma unroll
+            for (uint32_t e = 0; e < 8; ++e) pb[e] = static_cast<_Float16>(pf[e] * static_cast<float>(vs[e]));
+            O[2 * b] = mfma_16x16x32(*reinterpret_cast<const half8*>(tv + 512 * (2 * b)), pb, O[2 * b]);
+            O[2 * b + 1] = mfma_16x16x32(*reinterpret_cast<const half8*>(tv + 512 * (2 * b + 1)), pb, O[2 * b + 1]);
+        }
+        if (s + kExDist < s_end) wait_vmem_le<kPer>();
+        else wait_vmem();
+        __syncthreads();
+    }
+
+    // ---- store: PV lane (gq, ci) holds dims 16m + 4gq .. +3 of the wave's row ci
+    l_run = rows_reduce(l_run, AddOp{});  // the 4 lanes of a row hold its 32 keys' weights
+    const uint32_t orow_i = r0 + wave * 16 + ci;
+    if (orow_i >= rows) return;
+    const uint32_t ot = orow_i / G;
+    const uint32_t oqh = h * G + orow_i % G;
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    if (a.splits > 1) {
+        // fp32 records (O / l): an fp16 record would round each split's output once more
+        const uint32_t rows_cap = a.token_count * G;
+        const size_t pr = (static_cast<size_t>(split) * a.g.kv_heads + h) * rows_cap + orow_i;
+        float* po = static_cast<float*>(a.part) + pr * D;
+#pragma unroll
+        for (uint32_t m = 0; m < NM; ++m)
+            *reinterpret_cast<float4*>(po + 16 * m + 4 * gq) =
+                make_float4(O[m][0] * inv, O[m][1] * inv, O[m][2] * inv, O[m][3] * inv);
+        if (gq == 0) {
+            float2* ml = reinterpret_cast<float2*>(static_cast<float*>(a.part) +
+                                                   part_o_halves(a.splits, a.g.kv_heads, rows_cap, D));
+            ml[pr] = make_float2(m_run, l_run);
+        }
+        return;
+    }
+    const size_t orow = (static_cast<size_t>(ot) * a.q_heads + oqh) * D;
+#pragma unroll
+    for (uint32_t m = 0; m < NM; ++m) {
+        float4 v;
+        v.x = O[m][0] * inv;
+        v.y = O[m][1] * inv;
+        v.z = O[m][2] * inv;
+        v.w = O[m][3] * inv;
+        const size_t oi = orow + 16 * m + 4 * gq;
+        if (a.out) *reinterpret_cast<float4*>(a.out + oi) = v;
+        if (a.gate && a.gated_out) {
+            const float4 gv = *reinterpret_cast<const float4*>(a.gate + oi);
+            float4 r;
+            r.x = v.x * (1.0f / (1.0f + expf(-gv.x)));
+            r.y = v.y * (1.0f / (1.0f + expf(-gv.y)));
+            r.z = v.z * (1.0f / (1.0f + expf(-gv.z)));
+            r.w = v.w * (1.0f / (1.0f + expf(-gv.w)));
+            *reinterpret_cast<float4*>(a.gated_out + oi) = r;
+        }
+    }
+}
+
 // Dims per thread of suffix_combine_kernel.
 #ifndef MIIKV_SFX_COMBINE_VEC
 #define MIIKV_SFX_COMBINE_VEC 8
@@ -542,7 +885,7 @@ constexpr uint32_t kCombVec = MIIKV_SFX_COMBINE_VEC;
 // one row.  Token t sees P + t + 1 keys, so splits at or past ceil((P + t + 1) /
 // split_keys) hold no key of its row and are skipped; the rest are merged in
 // split order (out = sum e^{m_s-M} O_s / sum e^{m_s-M} l_s, 0 when the sum is 0).
-template <uint32_t D>
+template <uint32_t D, typename RecT>
 __global__ void __launch_bounds__(256) suffix_combine_kernel(SuffixCombineArgs a) {
     uint32_t T = a.token_count;
     uint32_t P = a.base_position;
@@ -559,11 +902,11 @@ __global__ void __launch_bounds__(256) suffix_combine_kernel(SuffixCombineArgs a
     const uint32_t rows_cap = a.token_count * G;
     const uint32_t t = row / G, g = row % G;
     const uint32_t nsplit = min(a.splits, (P + t + 1 + a.split_keys - 1) / a.split_keys);
-    const _Float16* po = static_cast<const _Float16*>(a.part);
+    const RecT* po = static_cast<const RecT*>(a.part);
     const float2* ml = reinterpret_cast<const float2*>(po + part_o_halves(a.splits, a.kv_heads, rows_cap, D));
     const size_t oi = (static_cast<size_t>(t) * a.q_heads + h * G + g) * D + kCombVec * dv;
     // Records hold O_s / l_s: each split enters with weight l_s e^{m_s - M}.
-    using HalfV = _Float16 __attribute__((ext_vector_type(kCombVec)));
+    using HalfV = RecT __attribute__((ext_vector_type(kCombVec)));
     float M = -INFINITY, Ls = 0.0f;
     float acc[kCombVec] = {};
     // Batches of kU splits: every load of a batch is issued before the first merge.
@@ -664,18 +1007,21 @@ struct SuffixPlan {
 // the expanded tiles of every step, and enough splits to fill the chip (at least
 // 256 keys per split).  Monotone in key_bound, so a plan made with the cache
 // capacity covers any smaller context.
+// exact: the plan of suffix_exact_kernel (its tiles and its rows per workgroup).
 SuffixPlan make_suffix_plan(const miikv_view* v, uint32_t q_heads, uint32_t tokens, uint64_t key_bound,
-                            bool allow_split, uint64_t stride_bound = 0) {
+                            bool allow_split, uint64_t stride_bound = 0, bool exact = false) {
     SuffixPlan p{1, 0, 0, 0, 0};
     const uint32_t G = q_heads / v->kv_heads;
+    const uint32_t rows_per_wg = exact ? kExRows : kSufRows;
     // the tile area holds stride_bound keys per kv head (the capacity for incremental
     // tiles, whose layout must not move between calls), the splits cover key_bound
     p.steps = static_cast<uint32_t>((std::max(key_bound, stride_bound) + kSufStep - 1) / kSufStep);
-    p.tile_bytes = static_cast<uint64_t>(v->kv_heads) * p.steps * tile_halves(v->head_dim) * 2;
+    p.tile_bytes = static_cast<uint64_t>(v->kv_heads) * p.steps *
+                   (exact ? ex_tile_halves(v->head_dim) : tile_halves(v->head_dim)) * 2;
     const uint64_t key_steps = (key_bound + kSufStep - 1) / kSufStep;
     p.split_keys = static_cast<uint32_t>(std::min<uint64_t>(key_steps * kSufStep, 0xffffff00u));
     if (!allow_split) return p;
-    const uint64_t wgs = (static_cast<uint64_t>(tokens) * G + kSufRows - 1) / kSufRows * v->kv_heads;
+    const uint64_t wgs = (static_cast<uint64_t>(tokens) * G + rows_per_wg - 1) / rows_per_wg * v->kv_heads;
     // Splits: as many as keep every workgroup resident in one round (the
     // per-workgroup cost does not shrink with more concurrent workgroups, so a
     // second partial round costs a full one), at least 256 keys each.
@@ -691,7 +1037,7 @@ SuffixPlan make_suffix_plan(const miikv_view* v, uint32_t q_heads, uint32_t toke
     p.splits = splits;
     p.split_keys = split_keys;
     // Records sized for `want` (>= splits): a plan for a shorter context never needs more.
-    p.part_bytes = want * v->kv_heads * tokens * G * part_row_bytes(v->head_dim);
+    p.part_bytes = want * v->kv_heads * tokens * G * (exact ? 4 * v->head_dim + 8 : part_row_bytes(v->head_dim));
     return p;
 }
 
@@ -726,7 +1072,39 @@ extern "C" uint64_t miikv_suffix_workspace_bytes_ex(const miikv_view* view, uint
     const uint64_t cap = view_seq_capacity(view);
     const SuffixPlan tiles = make_suffix_plan(view, q_heads, token_count, cap, false);
     const uint32_t cap32 = static_cast<uint32_t>(std::min<uint64_t>(cap, 0xffffffffu));
-    return std::max(base, tiles.tile_bytes + suffix_by_decode_bytes(view, q_heads, token_count, cap32));
+    const SuffixPlan xp = make_suffix_plan(view, q_heads, token_count, cap, true, 0, true);
+    return std::max({base, tiles.tile_bytes + suffix_by_decode_bytes(view, q_heads, token_count, cap32),
+                     xp.total()});
+}
+
+// The split merge of the MFMA kernels (the records of either kernel have one layout).
+// f32: the exact kernel's fp32 records.
+static void launch_suffix_combine(const miikv_view* view, uint32_t q_heads, uint32_t G, uint32_t token_count,
+                                  uint32_t base_position, const miikv_prefill_state* prefill_state,
+                                  const SuffixPlan& plan, void* part, float* out, const float* gate, float* gated_out,
+                                  hipStream_t s, bool f32 = false) {
+    SuffixCombineArgs c;
+    c.kv_heads = view->kv_heads;
+    c.q_heads = q_heads;
+    c.group = G;
+    c.token_count = token_count;
+    c.base_position = base_position;
+    c.ps = prefill_state;
+    c.split_keys = plan.split_keys;
+    c.splits = plan.splits;
+    c.part = part;
+    c.out = out;
+    c.gate = gate;
+    c.gated_out = gated_out;
+    const uint64_t threads = static_cast<uint64_t>(token_count) * G * (view->head_dim / kCombVec);
+    const dim3 cgrid(static_cast<uint32_t>((threads + 255) / 256), view->kv_heads);
+    if (view->head_dim == 128) {
+        if (f32) hipLaunchKernelGGL((suffix_combine_kernel<128, float>), cgrid, dim3(256), 0, s, c);
+        else hipLaunchKernelGGL((suffix_combine_kernel<128, _Float16>), cgrid, dim3(256), 0, s, c);
+    } else {
+        if (f32) hipLaunchKernelGGL((suffix_combine_kernel<256, float>), cgrid, dim3(256), 0, s, c);
+        else hipLaunchKernelGGL((suffix_combine_kernel<256, _Float16>), cgrid, dim3(256), 0, s, c);
+    }
 }
 
 static miikv_status suffix_impl(const miikv_view* view, const uint16_t* k_new, const uint16_t* v_new, const void* q,
@@ -793,7 +1171,70 @@ static miikv_status suffix_impl(const miikv_view* view, const uint16_t* k_new, c
     // (a workspace sized for the MFMA path alone runs that path)
     const SuffixPlan tile_plan = make_suffix_plan(view, q_heads, token_count, bound, false, stride_bound);
     const uint64_t dec_off = current ? tile_plan.tile_bytes : 0;  // the tiles stay below the records
-    const bool by_decode = exact || suffix_runs_as_decode(view, q_heads, token_count, prefill_state != nullptr);
+    const bool short_suffix = suffix_runs_as_decode(view, q_heads, token_count, prefill_state != nullptr);
+    // MIIKV_SUFFIX_EXACT: a long suffix over q8 planes runs the exact-product MFMA
+    // kernels; short suffixes, other quant modes and chunked prefill (whose tiles keep
+    // the plain layout) run every token as a decode.
+    const bool exact_mfma = exact && !current && !short_suffix && view->quant_mode == MIIKV_KV_Q8_Q8;
+    if (exact_mfma) {
+        if (k_new != nullptr) {  // the suffix's own rows first, with the append rule
+            const miikv_status ast = miikv_append_f16(view, k_new, v_new, token_count, base_position, seq,
+                                                      prefill_state, nullptr, stream);
+            if (ast != MIIKV_OK) return ast;
+        }
+        SuffixPlan xp = make_suffix_plan(view, q_heads, token_count, bound, true, 0, true);
+        if (workspace_bytes < xp.total()) {
+            xp = make_suffix_plan(view, q_heads, token_count, bound, false, 0, true);
+            if (workspace_bytes < xp.total()) return MIIKV_EWORKSPACE;
+        }
+        if (xp.steps > 65535u * 64u) return MIIKV_EINVAL;
+        const uint64_t xblocks = (rows + kExRows - 1) / kExRows;
+        ExpandArgs e;
+        e.g = make_geo(*view);
+        e.seq = seq;
+        e.key_count = bound32;
+        e.ps = prefill_state;
+        e.steps = xp.steps;
+        e.tiles = tiles;
+        e.k_new = nullptr;
+        e.v_new = nullptr;
+        e.token_count = token_count;
+        e.base_position = base_position;
+        e.step0 = 0;
+        e.current = 0;
+        const dim3 egrid(static_cast<uint32_t>((bound + kSufStep - 1) / kSufStep), view->kv_heads);
+        if (view->head_dim == 128) hipLaunchKernelGGL((expand_exact_kernel<128>), egrid, dim3(256), 0, s, e);
+        else hipLaunchKernelGGL((expand_exact_kernel<256>), egrid, dim3(256), 0, s, e);
+        SuffixArgs a;
+        a.g = make_geo(*view);
+        a.q = q;
+        a.q_f32 = q_dtype == MIIKV_DTYPE_F32;
+        a.q_heads = q_heads;
+        a.group = G;
+        a.scale_log2 = scale * kLog2eS;
+        a.token_count = token_count;
+        a.base_position = base_position;
+        a.ps = prefill_state;
+        a.split_keys = xp.split_keys;
+        a.splits = xp.splits;
+        a.row_blocks = static_cast<uint32_t>(xblocks);
+        a.steps = xp.steps;
+        a.tiles = tiles;
+        a.part = static_cast<uint8_t*>(workspace) + xp.tile_bytes;
+        a.out = out;
+        a.gate = gate;
+        a.gated_out = gated_out;
+        const uint64_t xwgs = (static_cast<uint64_t>(view->kv_heads) * xp.splits * xblocks + 7) / 8 * 8;
+        if (xwgs > 0x7fffffffu) return MIIKV_EINVAL;
+        if (view->head_dim == 128)
+            hipLaunchKernelGGL(suffix_exact_kernel<128>, dim3(static_cast<uint32_t>(xwgs)), dim3(64 * kExWaves), 0, s, a);
+        else
+            hipLaunchKernelGGL(suffix_exact_kernel<256>, dim3(static_cast<uint32_t>(xwgs)), dim3(64 * kExWaves), 0, s, a);
+        if (xp.splits > 1) launch_suffix_combine(view, q_heads, G, token_count, base_position, prefill_state, xp,
+                                                 a.part, out, gate, gated_out, s, true);
+        return hip_status(hipGetLastError());
+    }
+    const bool by_decode = exact || short_suffix;
     const bool dec_fits = workspace_bytes >= dec_off + suffix_by_decode_bytes(view, q_heads, token_count, bound32);
     if (exact && !dec_fits) return MIIKV_EWORKSPACE;
     if (by_decode && dec_fits) {
@@ -845,25 +1286,8 @@ static miikv_status suffix_impl(const miikv_view* view, const uint16_t* k_new, c
     const dim3 grid(static_cast<uint32_t>(wgs));
     if (view->head_dim == 128) hipLaunchKernelGGL(suffix_kernel<128>, grid, dim3(64 * kSufWaves), 0, s, a);
     else hipLaunchKernelGGL(suffix_kernel<256>, grid, dim3(64 * kSufWaves), 0, s, a);
-    if (plan.splits > 1) {
-        SuffixCombineArgs c;
-        c.kv_heads = view->kv_heads;
-        c.q_heads = q_heads;
-        c.group = G;
-        c.token_count = token_count;
-        c.base_position = base_position;
-        c.ps = prefill_state;
-        c.split_keys = plan.split_keys;
-        c.splits = plan.splits;
-        c.part = a.part;
-        c.out = out;
-        c.gate = gate;
-        c.gated_out = gated_out;
-        const uint64_t threads = static_cast<uint64_t>(token_count) * G * (view->head_dim / kCombVec);
-        const dim3 cgrid(static_cast<uint32_t>((threads + 255) / 256), view->kv_heads);
-        if (view->head_dim == 128) hipLaunchKernelGGL(suffix_combine_kernel<128>, cgrid, dim3(256), 0, s, c);
-        else hipLaunchKernelGGL(suffix_combine_kernel<256>, cgrid, dim3(256), 0, s, c);
-    }
+    if (plan.splits > 1) launch_suffix_combine(view, q_heads, G, token_count, base_position, prefill_state, plan,
+                                               a.part, out, gate, gated_out, s);
     return hip_status(hipGetLastError());
 }
 

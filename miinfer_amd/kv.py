@@ -426,10 +426,11 @@ def suffix_attention(cache: KvCache, q: torch.Tensor, base_position: int, scale:
     are current from earlier calls, so only the new steps are expanded
     (MIIKV_SUFFIX_TILES_CURRENT).
 
-    exact (MIIKV_SUFFIX_EXACT): every token runs as a decode, keeping an fp32 query's
-    low half and applying the block scales in fp32, instead of the MFMA path's fp16
-    query and tiles; it streams the context once per row set of tokens (slower on
-    long suffixes) and needs suffix_workspace_bytes(..., exact=True)."""
+    exact (MIIKV_SUFFIX_EXACT): the reference's fp32 products -- an fp32 query's low
+    half kept and the key block scales applied in fp32 -- instead of the MFMA path's
+    fp16 query and tiles: long suffixes over q8 planes on the exact-product MFMA kernel,
+    short ones (and chunked prefill, other quant modes) as decodes; needs
+    suffix_workspace_bytes(..., exact=True)."""
     t, q_heads, d = q.shape
     if d != cache.head_dim or not q.is_contiguous() or q.dtype not in (torch.float16,
                                                                         torch.float32):

@@ -413,8 +413,11 @@ def test_suffix_chunked_prefill_current_tiles(gpu, fused, exact):
     expands only its own steps (chunk sizes aligned, unaligned and short, the short
     ones running as decodes while keeping the tiles current), and every chunk's output
     equals a fresh call's over the same cache bit for bit, and the oracle.  With
-    `exact`, odd chunks run with MIIKV_SUFFIX_EXACT (as decodes) and must still leave
-    the tiles current for the MFMA chunks after them."""
+    `exact`, odd chunks run with MIIKV_SUFFIX_EXACT (as decodes: chunked prefill keeps
+    the plain tile layout) and must still leave the tiles current for the MFMA chunks
+    after them; a fresh exact call of a long chunk runs the exact-product MFMA kernel
+    instead, so those two are compared within the attention tolerance, each against the
+    oracle."""
     import miinfer_amd as m
     rng = np.random.default_rng(77 + fused + 2 * exact)
     hq, hk, d, cap = 24, 4, 256, 1024
@@ -442,10 +445,12 @@ def test_suffix_chunked_prefill_current_tiles(gpu, fused, exact):
             got, _ = m.suffix_attention(cache, _dev(q, gpu), base, workspace=ws, tiles_current=True, exact=ex)
         ref, _ = m.suffix_attention(fresh, _dev(q, gpu), base, exact=ex)
         torch.cuda.synchronize()
-        assert torch.equal(got, ref), (base, t, (got - ref).abs().max().item())
+        if not ex:
+            assert torch.equal(got, ref), (base, t, (got - ref).abs().max().item())
         expect = oracle.suffix_attention_q8(q.astype(np.float32), kc[:, :base + t], ks[:, :base + t],
                                             vc[:, :base + t], vs[:, :base + t], base, hq, 1 / math.sqrt(d))
         assert_attention_close(got.cpu().numpy(), expect, f"chunk at {base}")
+        assert_attention_close(ref.cpu().numpy(), expect, f"fresh chunk at {base}")
         base += t
 
 
@@ -581,6 +586,43 @@ def test_suffix_exact_route(gpu, t, f32, fused, dev_state):
         torch.cuda.synchronize()
         assert np.array_equal(got_kc.cpu().numpy(), kc[:, prefix:])
         assert np.array_equal(got_ks.cpu().numpy().view(np.uint16), ks[:, prefix:])
+
+
+@pytest.mark.parametrize("hq,hk,d,paged", [(32, 8, 128, True), (24, 4, 256, True), (8, 2, 128, False)])
+def test_suffix_exact_mfma_kernel_shapes(gpu, hq, hk, d, paged):
+    """Long suffixes with MIIKV_SUFFIX_EXACT run the exact-product MFMA kernel (key codes
+    exact, block scales in fp32, the query's lo half in the spare columns): sharp
+    attention (logits of s.d. ~6) within the tolerance on paged and contiguous caches,
+    head_dim 128 and 256, with a gate, split and single-split workspaces."""
+    import miinfer_amd as m
+    rng = np.random.default_rng(hq + d + paged)
+    prefix, t, pt = 1800, 200, 256
+    n = prefix + t
+    k = randn_f16(rng, (n, hk, d))
+    v = randn_f16(rng, (n, hk, d))
+    kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+    vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+    if paged:
+        npages = (n + pt - 1) // pt
+        table = _dev(rng.permutation(npages + 2)[:npages].astype(np.int32).reshape(1, npages), gpu)
+        cache = m.KvCache.paged_cache(hk, d, npages + 2, table, page_tokens=pt)
+    else:
+        cache = m.KvCache.contiguous(hk, d, ((n + 63) // 64) * 64)
+    cache.append(_dev(k, gpu), _dev(v, gpu))
+    q = (rng.standard_normal((t, hq, d)) * 3).astype(np.float32)
+    gate = rng.standard_normal((t, hq, d)).astype(np.float32)
+    scale = 2 / math.sqrt(d)
+    expect = oracle.suffix_attention_q8(q, kc, ks, vc, vs, prefix, hq, scale)
+    for ws in (None, "tiles"):
+        kw = {}
+        if ws == "tiles":  # just the exact tiles: one split
+            kw["workspace"] = torch.empty(hk * ((n + 31) // 32) * (64 * d + 64 * (d // 32)) * 2, dtype=torch.uint8,
+                                          device=gpu)
+        out, gated = m.suffix_attention(cache, _dev(q, gpu), prefix, scale, gate=_dev(gate, gpu),
+                                        out=torch.empty((t, hq, d), device=gpu), exact=True, **kw)
+        torch.cuda.synchronize()
+        assert_attention_close(out.cpu().numpy(), expect, f"exact {ws}")
+        assert_attention_close(gated.cpu().numpy(), expect / (1 + np.exp(-gate)), f"exact gated {ws}")
 
 
 def test_suffix_exact_route_errors(gpu):
