@@ -34,6 +34,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
+#include <type_traits>
 
 namespace miikv {
 
@@ -536,33 +537,31 @@ __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
 //
 // The reference multiplies an fp32 query with the dequantised keys in fp32.  Here the
 // scores are exact in the same sense as decode's: the key tiles hold the int8 codes
-// as fp16 (exact), each 32-value block's dot product comes out of its own pair of
-// v_mfma_f32_32x32x16_f16 and is multiplied by the block's fp16 scale in fp32, and
-// the query is split into fp16 hi + lo parts, which ride in the MFMA's columns 16..31
-// (column 16 + r holds the lo part of row r) and are added to the hi column by a
-// 16-lane swap.  A wave therefore serves 16 query rows.  The values enter as their
-// codes (fp16, exact), and each 32-value block's scale multiplies the probabilities
-// in fp32, the product rounded to fp16 once, as on the decode path; O^T += V^T P^T
-// runs as v_mfma_f32_16x16x32_f16 over the 16 real columns, one MFMA per 16 dims
-// with the P^T of their block (a wave holds O^T in 64 registers).
+// as fp16 (exact), each 32-value block's dot product comes out of its own
+// v_mfma_f32_16x16x32_f16 (16 keys x 16 query rows) and is multiplied by the block's
+// fp16 scale in fp32, and an fp32 query is split into fp16 hi + lo parts with a second
+// MFMA per block for the lo part.  The values enter as their codes (fp16, exact), and
+// each block's scale multiplies the probabilities in fp32, the product rounded to
+// fp16 once, as on the decode path; O^T += V^T P^T runs as v_mfma_f32_16x16x32_f16,
+// one per 16 dims with the P^T of their block.  A wave serves 16 query rows and holds
+// the query's hi and lo parts (64 registers) and O^T (64 registers).
 //
-// Step record of the exact tiles (halves): K codes as fp16 in the K^ fragment layout
-// of expand_kernel [D/16][64 lanes][8]; the K block scales [D/32 blocks][2 hh][16],
-// entry (b, hh, 4j + i) the scale of key 8j + 4hh + i, the keys a lane of the score
-// accumulator holds in register order; the V block scales [D/32 blocks][4 g][8 e],
-// entry (b, g, e) the scale of key ex_key(g, e) (0 past the context end); V^T code
-// fragments of the 16x16x32 MFMA [D/16 dim tiles][64 lanes][8]: lane (g, i) = 16g + i
-// holds dim 16m + i of keys ex_key(g, e), e < 8, as fp16.  The key order of a V
-// fragment is the order in which the score accumulator's registers reach the PV B
-// operand: lane 16g + i takes registers 8(g & 1) .. +7 of its column (its 32-lane half
-// hh = g >> 1).
+// Step record of the exact tiles (halves):
+//   K codes as fp16 [2 key tiles t][D/32 blocks b][64 lanes][8]: lane (g, i) = 16g + i
+//     holds key 16t + i, dims 32b + 8g .. +7 (the A operand of the score MFMA);
+//   K block scales [t][4 g][D/32 b][4 r]: the scale of key 16t + 4g + r, block b (the
+//     keys a score lane holds);
+//   V block scales [D/32 b][4 g][8 e]: the scale of key ex_key(g, e), block b (0 past
+//     the context end);
+//   V^T codes as fp16 [D/16 dim tiles m][64 lanes][8]: lane (g, i) holds dim 16m + i
+//     of keys ex_key(g, e), e < 8.
+// ex_key(g, e) is the key in score register e % 4 of tile e / 4 of lane group g, so a
+// lane's eight probabilities are directly its PV B operand.
 __host__ __device__ constexpr uint32_t ex_tile_halves(uint32_t D) { return 64 * D + 64 * (D / 32); }
-__device__ __forceinline__ uint32_t ex_key(uint32_t g, uint32_t e) {
-    return 16 * (g & 1) + 8 * (e >> 2) + 4 * (g >> 1) + (e & 3);
-}
+__device__ __forceinline__ uint32_t ex_key(uint32_t g, uint32_t e) { return 16 * (e >> 2) + 4 * g + (e & 3); }
 
 // One 32-key step of kv head blockIdx.y into the exact tile layout (q8 planes only);
-// keys at or past the context end become 0.
+// keys at or past the context end get zero codes and scales.
 template <uint32_t D>
 __global__ void __launch_bounds__(256) expand_exact_kernel(ExpandArgs a) {
     constexpr uint32_t NB = D / 32;
@@ -589,44 +588,54 @@ __global__ void __launch_bounds__(256) expand_exact_kernel(ExpandArgs a) {
     }
     __syncthreads();
     _Float16* out = a.tiles + (static_cast<size_t>(h) * a.steps + step) * ex_tile_halves(D);
-    // K codes: fragment c, lane (n, hh): key n, dims 16c + 8hh .. +7 (offsets as in expand_kernel)
+    // K codes: fragment (t, b), lane (g, i): key 16t + i, dims 32b + 8g .. +7, which sit
+    // in the cache tile at t*16D + (b/2)*1024 + g*256 + i*16 + (b%2)*8
 #pragma unroll
     for (uint32_t u = 0; u < PER; ++u) {
         const uint32_t fl = tid + 256 * u;
-        const uint32_t c = fl / 64, l = fl % 64, n = l % 32, hh = l / 32;
-        const uint32_t off = (n / 16) * 16 * D + (c / 4) * 1024 + (2 * (c % 2) + hh) * 256 + (n % 16) * 16 +
-                             ((c % 4) / 2) * 8;
+        const uint32_t f = fl / 64, l = fl % 64, g = l / 16, i = l % 16;
+        const uint32_t t = f / NB, b = f % NB;
+        const uint32_t off = t * 16 * D + (b / 2) * 1024 + g * 256 + i * 16 + (b % 2) * 8;
         const uint2 w = *reinterpret_cast<const uint2*>(kb + off);
-        *reinterpret_cast<half8*>(out + 8 * fl) = tok0 + n < nkeys ? codes8_to_half8(w.x, w.y) : half8{};
+        *reinterpret_cast<half8*>(out + 8 * fl) = tok0 + 16 * t + i < nkeys ? codes8_to_half8(w.x, w.y) : half8{};
     }
-    // K scales [b][hh][4j + i] = scale of key 8j + 4hh + i, block b (raw fp16)
+    // K scales [t][g][b][r] = scale of key 16t + 4g + r, block b (raw fp16)
     _Float16* osc = out + 32 * D;
     if (tid < 32 * NB) {
-        const uint32_t b = tid / 32, hh = (tid / 16) & 1, r = tid & 15;
-        const uint32_t key = 8 * (r >> 2) + 4 * hh + (r & 3);
+        const uint32_t t = tid / (16 * NB), g = (tid / (4 * NB)) % 4, b = (tid / 4) % NB, r = tid % 4;
+        const uint32_t key = 16 * t + 4 * g + r;
         osc[tid] = tok0 + key < nkeys ? __builtin_bit_cast(_Float16, ksc[key * NB + b]) : (_Float16)0.0f;
     }
-    // V block scales [b][g][e] = scale of key ex_key(g, e), block b (0 past the context)
+    // V scales [b][g][e] = scale of key ex_key(g, e), block b (0 past the context)
     _Float16* ovs = osc + 32 * NB;
     if (tid < 32 * NB) {
         const uint32_t b = tid / 32, g = (tid / 8) & 3, e = tid & 7;
         ovs[tid] = s_vs[b * kSufStep + ex_key(g, e)];
     }
-    // V^T code fragments: dim tile m, lane (g, i): dim 16m + i, keys ex_key(g, 0..7).
-    // Keys ex_key(g, 0..3) are t = 16(g & 1) + 4(g >> 1) + 0..3, i.e. J = g & 1, G = g >> 1
-    // in the cache group's order (code of key 16J + 4G + I of dim d at d*32 + 8G + 4J +
-    // I), and ex_key(g, 4..7) the same with G + 2.  Codes past the context end are read
-    // as they are: their scale is 0.
+    // V^T code fragments: dim tile m, lane (g, i): dim 16m + i, keys ex_key(g, 0..7) =
+    // 4g .. 4g+3 and 16 + 4g .. 16 + 4g + 3, i.e. (J = 0, G = g) and (J = 1, G = g) in
+    // the cache group's order (code of key 16J + 4G + I of dim d at d*32 + 8G + 4J + I):
+    // eight contiguous bytes.  Codes past the context end are read as they are: their
+    // scale is 0.
     _Float16* ov = ovs + 32 * NB;
 #pragma unroll
     for (uint32_t u = 0; u < PER; ++u) {
         const uint32_t fl = tid + 256 * u;
         const uint32_t m = fl / 64, l = fl % 64, g = l / 16, i = l % 16;
-        const int8_t* vd = vb + (16 * m + i) * 32 + 4 * (g & 1);
-        const uint32_t w0 = *reinterpret_cast<const uint32_t*>(vd + 8 * (g >> 1));
-        const uint32_t w1 = *reinterpret_cast<const uint32_t*>(vd + 8 * (2 + (g >> 1)));
-        *reinterpret_cast<half8*>(ov + 8 * fl) = codes8_to_half8(w0, w1);
+        const uint2 w = *reinterpret_cast<const uint2*>(vb + (16 * m + i) * 32 + 8 * g);
+        *reinterpret_cast<half8*>(ov + 8 * fl) = codes8_to_half8(w.x, w.y);
     }
+}
+
+// Two fp16 products (p0 * lo half of w, p1 * hi half of w), each of an fp32 value and
+// an fp16 value rounded to fp16 once (v_fma_mix with a zero addend), packed in one word.
+__device__ __forceinline__ uint32_t mul_round2(float p0, float p1, uint32_t w) {
+    uint32_t d;
+    asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,1,0]\n\t"
+        "v_fma_mixhi_f16 %0, %3, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
+        : "=&v"(d)
+        : "v"(p0), "v"(w), "v"(p1));
+    return d;
 }
 
 constexpr uint32_t kExWaves = 8;
@@ -634,10 +643,9 @@ constexpr uint32_t kExRows = 16 * kExWaves;  // query rows per workgroup
 constexpr uint32_t kExDist = 2;              // prefetch distance in steps
 constexpr uint32_t kExBufs = kExDist + 1;    // LDS step buffers
 
-template <uint32_t D>
+template <uint32_t D, bool QF32>
 __global__ void __launch_bounds__(64 * kExWaves) suffix_exact_kernel(SuffixArgs a) {
-    constexpr uint32_t NB = D / 32;          // q8 blocks (score block pairs)
-    constexpr uint32_t NC = D / 16;          // QK k-chunks
+    constexpr uint32_t NB = D / 32;          // q8 blocks
     constexpr uint32_t NM = D / 16;          // PV dim tiles
     constexpr uint32_t REC = ex_tile_halves(D);
     constexpr uint32_t KV_CHUNKS = 64 * D * 2 / 1024;  // 1 KiB chunks of K codes + V^T
@@ -665,16 +673,13 @@ __global__ void __launch_bounds__(64 * kExWaves) suffix_exact_kernel(SuffixArgs 
     const uint32_t tid = threadIdx.x;
     const uint32_t wave = tid >> 6;
     const uint32_t lane = tid & 63;
-    const uint32_t n = lane & 31;   // score column
-    const uint32_t hh = lane >> 5;
-    const uint32_t ci = lane & 15;  // PV column / row of the wave
-    const uint32_t gq = lane >> 4;  // PV lane group
+    const uint32_t ci = lane & 15;  // the lane's row (column of every MFMA)
+    const uint32_t gq = lane >> 4;  // lane group: keys 4gq .. +3 of each 16-key tile
     const uint32_t rows = T * G;
     const uint32_t r0 = rb * kExRows;
     if (r0 >= rows) return;
 
-    // score lane (n, hh): column n, i.e. row n & 15 of the wave, hi part (n < 16) or lo
-    const uint32_t row = r0 + wave * 16 + (n & 15);
+    const uint32_t row = r0 + wave * 16 + ci;
     const bool row_ok = row < rows;
     const uint32_t t_row = row_ok ? row / G : 0;
     const uint32_t qh = h * G + (row_ok ? row % G : 0);
@@ -689,18 +694,19 @@ __global__ void __launch_bounds__(64 * kExWaves) suffix_exact_kernel(SuffixArgs 
     const uint32_t s_begin = key_lo / kSufStep;
     const uint32_t s_end = (key_hi + kSufStep - 1) / kSufStep;
 
-    // ---- Q^T fragments: column n, dims 16c + 8hh .. +7: hi parts (n < 16) or lo parts
-    half8 qf[NC];
+    // ---- Q^T fragments (B operand of the score MFMA): row ci, dims 32b + 8gq .. +7;
+    // an fp32 query as hi + lo parts
+    half8 qhi[NB];
+    half8 qlo[QF32 ? NB : 1];
     {
         const size_t qrow = (static_cast<size_t>(t_row) * a.q_heads + qh) * D;
-        const bool lo = n >= 16;
-        if (a.q_f32) {
+        if constexpr (QF32) {
 #pragma unroll
-            for (uint32_t c0 = 0; c0 < NC; c0 += 4) {
+            for (uint32_t b0 = 0; b0 < NB; b0 += 4) {
                 float4 x[4][2];
 #pragma unroll
                 for (uint32_t j = 0; j < 4; ++j) {
-                    const float* qp = static_cast<const float*>(a.q) + qrow + (c0 + j) * 16 + hh * 8;
+                    const float* qp = static_cast<const float*>(a.q) + qrow + (b0 + j) * 32 + gq * 8;
                     x[j][0] = *reinterpret_cast<const float4*>(qp);
                     x[j][1] = *reinterpret_cast<const float4*>(qp + 4);
                 }
@@ -708,21 +714,23 @@ __global__ void __launch_bounds__(64 * kExWaves) suffix_exact_kernel(SuffixArgs 
                 for (uint32_t j = 0; j < 4; ++j) {
                     const float xs[8] = {x[j][0].x, x[j][0].y, x[j][0].z, x[j][0].w,
                                          x[j][1].x, x[j][1].y, x[j][1].z, x[j][1].w};
-                    half8 v;
+                    half8 hi8, lo8;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        const _Float16 hi = static_cast<_Float16>(xs[e]);
-                        v[e] = lo ? static_cast<_Float16>(xs[e] - static_cast<float>(hi)) : hi;
+                        const _Float16 hv = static_cast<_Float16>(xs[e]);
+                        hi8[e] = hv;
+                        lo8[e] = static_cast<_Float16>(xs[e] - static_cast<float>(hv));
                     }
-                    qf[c0 + j] = row_ok ? v : half8{};
+                    qhi[b0 + j] = row_ok ? hi8 : half8{};
+                    qlo[b0 + j] = row_ok ? lo8 : half8{};
                 }
             }
         } else {
 #pragma unroll
-            for (uint32_t c = 0; c < NC; ++c) {
-                const uint16_t* qp = static_cast<const uint16_t*>(a.q) + qrow + c * 16 + hh * 8;
+            for (uint32_t b = 0; b < NB; ++b) {
+                const uint16_t* qp = static_cast<const uint16_t*>(a.q) + qrow + b * 32 + gq * 8;
                 const half8 v = __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(qp));
-                qf[c] = row_ok && !lo ? v : half8{};  // an fp16 query has no lo part
+                qhi[b] = row_ok ? v : half8{};
             }
         }
     }
@@ -754,42 +762,42 @@ __global__ void __launch_bounds__(64 * kExWaves) suffix_exact_kernel(SuffixArgs 
     wait_vmem();
     __syncthreads();
 
-    for (uint32_t s = s_begin; s < s_end; ++s) {
+    // One step; MASK: the step holds keys past some row's limit or past the split.
+    auto step = [&](uint32_t s, auto mask_tag) __attribute__((always_inline)) {
+        constexpr bool MASK = decltype(mask_tag)::value;
         if (s + kExDist < s_end) fetch(s + kExDist, (s + kExDist) % kExBufs);
         const _Float16* tb = s_t[s % kExBufs];
-        // ---- scores: one pair of MFMAs per q8 block, the block scale applied in fp32
-        float16v S = {};
-        const _Float16* tk = tb + lane * 8;
-        const _Float16* tsc = tb + 32 * D + hh * 16;
+        // ---- scores of the lane's 8 keys (tile t, keys 16t + 4gq + r): one MFMA per q8
+        // block (two with a lo part), the block scale applied in fp32
+        float pf[8];
 #pragma unroll
-        for (uint32_t b = 0; b < NB; ++b) {
-            float16v c = {};
-            c = mfma_32x32x16(*reinterpret_cast<const half8*>(tk + 512 * (2 * b)), qf[2 * b], c);
-            c = mfma_32x32x16(*reinterpret_cast<const half8*>(tk + 512 * (2 * b + 1)), qf[2 * b + 1], c);
-            const half8 s0 = *reinterpret_cast<const half8*>(tsc + 32 * b);
-            const half8 s1 = *reinterpret_cast<const half8*>(tsc + 32 * b + 8);
+        for (uint32_t t = 0; t < 2; ++t) {
+            const _Float16* tk = tb + t * NB * 512 + lane * 8;
+            const _Float16* tsc = tb + 32 * D + (t * 4 + gq) * 4 * NB;
+            float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (uint32_t r = 0; r < 8; ++r) {
-                S[r] = fmaf(c[r], static_cast<float>(s0[r]), S[r]);
-                S[8 + r] = fmaf(c[8 + r], static_cast<float>(s1[r]), S[8 + r]);
+            for (uint32_t b = 0; b < NB; ++b) {
+                const half8 kf = *reinterpret_cast<const half8*>(tk + 512 * b);
+                float4v c = mfma_16x16x32(kf, qhi[b], float4v{0.0f, 0.0f, 0.0f, 0.0f});
+                if constexpr (QF32) c = mfma_16x16x32(kf, qlo[b], c);
+                const half4 sc = *reinterpret_cast<const half4*>(tsc + 4 * b);
+#pragma unroll
+                for (uint32_t r = 0; r < 4; ++r) acc[r] = fmaf(c[r], static_cast<float>(sc[r]), acc[r]);
+            }
+#pragma unroll
+            for (uint32_t r = 0; r < 4; ++r) pf[4 * t + r] = acc[r];
+        }
+        // ---- mask and online softmax: the row's 32 keys sit in the 4 lanes of its column
+        if constexpr (MASK) {
+            const uint32_t key0 = s * kSufStep;
+#pragma unroll
+            for (uint32_t e = 0; e < 8; ++e) {
+                const uint32_t key = key0 + ex_key(gq, e);
+                if (!(key <= lim && key < key_hi)) pf[e] = -INFINITY;
             }
         }
-        // hi column + lo column (16 lanes apart): both lanes end with the row's score
-#pragma unroll
-        for (uint32_t r = 0; r < 16; ++r) S[r] = swap16_reduce(S[r], AddOp{});
-        // ---- mask and online softmax of this lane's 16 keys (8j + 4hh + i) of its row
-        const uint32_t key0 = s * kSufStep;
-        if (key0 + kSufStep - 1 > wave_lim || key0 + kSufStep > key_hi) {
-#pragma unroll
-            for (uint32_t r = 0; r < 16; ++r) {
-                const uint32_t key = key0 + 8 * (r / 4) + 4 * hh + (r % 4);
-                if (!(key <= lim && key < key_hi)) S[r] = -INFINITY;
-            }
-        }
-        float cmax = S[0];
-#pragma unroll
-        for (uint32_t r = 1; r < 16; ++r) cmax = fmaxf(cmax, S[r]);
-        cmax = swap32_reduce(cmax, MaxOp{});  // the row's 32 keys (lanes n and n + 32)
+        float cmax = fmaxf(fmaxf(fmaxf(pf[0], pf[1]), fmaxf(pf[2], pf[3])), fmaxf(fmaxf(pf[4], pf[5]), fmaxf(pf[6], pf[7])));
+        cmax = rows_reduce(cmax, MaxOp{});
         const float cm = cmax * a.scale_log2;
         const bool grow = cm > m_run + kSlackS;
         if (__any(grow)) {
@@ -801,34 +809,36 @@ __global__ void __launch_bounds__(64 * kExWaves) suffix_exact_kernel(SuffixArgs 
             for (uint32_t m = 0; m < NM; ++m) O[m] *= alpha;
         }
         const float m_use = m_run == -INFINITY ? 0.0f : m_run;
-        // PV B operand of lane (gq, ci): its column's registers 8(gq & 1) .. +7
-        const bool upper = (gq & 1) != 0;
-        float pf[8];
         float psum = 0.0f;
 #pragma unroll
         for (uint32_t e = 0; e < 8; ++e) {
-            const float x = upper ? S[8 + e] : S[e];
-            pf[e] = sfx_exp2(fmaf(x, a.scale_log2, -m_use));
+            pf[e] = sfx_exp2(fmaf(pf[e], a.scale_log2, -m_use));
             psum += pf[e];
         }
         l_run += psum;
-        // ---- O^T += V^T P^T per 16 dims, P^T scaled by their block's V scales (fp32
-        // product, rounded to fp16 once)
+        // ---- O^T += V^T P^T per 16 dims, P^T scaled by their block's V scales (the
+        // product rounded to fp16 once)
         const _Float16* tvs = tb + 32 * D + 32 * NB + gq * 8;
         const _Float16* tv = tb + 32 * D + 64 * NB + lane * 8;
 #pragma unroll
         for (uint32_t b = 0; b < NB; ++b) {
-            const half8 vs = *reinterpret_cast<const half8*>(tvs + 32 * b);
-            half8 pb;
-#pragma unroll
-            for (uint32_t e = 0; e < 8; ++e) pb[e] = static_cast<_Float16>(pf[e] * static_cast<float>(vs[e]));
+            const uint4 vs = *reinterpret_cast<const uint4*>(tvs + 32 * b);
+            const half8 pb = __builtin_bit_cast(half8, make_uint4(mul_round2(pf[0], pf[1], vs.x),
+                                                                   mul_round2(pf[2], pf[3], vs.y),
+                                                                   mul_round2(pf[4], pf[5], vs.z),
+                                                                   mul_round2(pf[6], pf[7], vs.w)));
             O[2 * b] = mfma_16x16x32(*reinterpret_cast<const half8*>(tv + 512 * (2 * b)), pb, O[2 * b]);
             O[2 * b + 1] = mfma_16x16x32(*reinterpret_cast<const half8*>(tv + 512 * (2 * b + 1)), pb, O[2 * b + 1]);
         }
         if (s + kExDist < s_end) wait_vmem_le<kPer>();
         else wait_vmem();
         __syncthreads();
-    }
+    };
+    // Steps wholly at or below every row's limit of this wave and inside the split
+    // need no mask: key0 + 31 <= wave_lim and key0 + 32 <= key_hi.
+    const uint32_t s_plain = max(s_begin, min(s_end, min((wave_lim + 1) / kSufStep, key_hi / kSufStep)));
+    for (uint32_t s = s_begin; s < s_plain; ++s) step(s, std::false_type{});
+    for (uint32_t s = s_plain; s < s_end; ++s) step(s, std::true_type{});
 
     // ---- store: PV lane (gq, ci) holds dims 16m + 4gq .. +3 of the wave's row ci
     l_run = rows_reduce(l_run, AddOp{});  // the 4 lanes of a row hold its 32 keys' weights
@@ -1226,10 +1236,14 @@ static miikv_status suffix_impl(const miikv_view* view, const uint16_t* k_new, c
         a.gated_out = gated_out;
         const uint64_t xwgs = (static_cast<uint64_t>(view->kv_heads) * xp.splits * xblocks + 7) / 8 * 8;
         if (xwgs > 0x7fffffffu) return MIIKV_EINVAL;
-        if (view->head_dim == 128)
-            hipLaunchKernelGGL(suffix_exact_kernel<128>, dim3(static_cast<uint32_t>(xwgs)), dim3(64 * kExWaves), 0, s, a);
-        else
-            hipLaunchKernelGGL(suffix_exact_kernel<256>, dim3(static_cast<uint32_t>(xwgs)), dim3(64 * kExWaves), 0, s, a);
+        const dim3 xgrid(static_cast<uint32_t>(xwgs)), xblock(64 * kExWaves);
+        if (view->head_dim == 128) {
+            if (a.q_f32) hipLaunchKernelGGL((suffix_exact_kernel<128, true>), xgrid, xblock, 0, s, a);
+            else hipLaunchKernelGGL((suffix_exact_kernel<128, false>), xgrid, xblock, 0, s, a);
+        } else {
+            if (a.q_f32) hipLaunchKernelGGL((suffix_exact_kernel<256, true>), xgrid, xblock, 0, s, a);
+            else hipLaunchKernelGGL((suffix_exact_kernel<256, false>), xgrid, xblock, 0, s, a);
+        }
         if (xp.splits > 1) launch_suffix_combine(view, q_heads, G, token_count, base_position, prefill_state, xp,
                                                  a.part, out, gate, gated_out, s, true);
         return hip_status(hipGetLastError());
