@@ -638,7 +638,10 @@ __device__ __forceinline__ uint32_t mul_round2(float p0, float p1, uint32_t w) {
     return d;
 }
 
-constexpr uint32_t kExWaves = 8;
+#ifndef MIIKV_EXACT_WAVES
+#define MIIKV_EXACT_WAVES 8
+#endif
+constexpr uint32_t kExWaves = MIIKV_EXACT_WAVES;
 constexpr uint32_t kExRows = 16 * kExWaves;  // query rows per workgroup
 constexpr uint32_t kExDist = 2;              // prefetch distance in steps
 constexpr uint32_t kExBufs = kExDist + 1;    // LDS step buffers
@@ -649,9 +652,10 @@ __global__ void __launch_bounds__(64 * kExWaves) suffix_exact_kernel(SuffixArgs 
     constexpr uint32_t NM = D / 16;          // PV dim tiles
     constexpr uint32_t REC = ex_tile_halves(D);
     constexpr uint32_t KV_CHUNKS = 64 * D * 2 / 1024;  // 1 KiB chunks of K codes + V^T
-    static_assert(KV_CHUNKS % kExWaves == 0, "copy chunks must split evenly over waves");
-    constexpr uint32_t kPer = KV_CHUNKS / kExWaves + 1;  // loads per wave per fetch (+1: the scales)
-    constexpr uint32_t SC_LANES = 128 * NB / 16 / kExWaves;  // 16-byte scale pieces per wave
+    constexpr uint32_t kChunkLoads = (KV_CHUNKS + kExWaves - 1) / kExWaves;  // per wave (the last maybe empty)
+    constexpr uint32_t kPer = kChunkLoads + 1;  // loads per wave per fetch (+1: the scales)
+    constexpr uint32_t SC_PIECES = 128 * NB / 16;  // 16-byte scale pieces of a step
+    constexpr uint32_t SC_LANES = (SC_PIECES + kExWaves - 1) / kExWaves;  // per wave
     __shared__ __align__(16) _Float16 s_t[kExBufs][REC];
     static_assert(sizeof(s_t) <= 128u * 1024u, "exact suffix LDS must stay within 128 KiB");
 
@@ -741,13 +745,16 @@ __global__ void __launch_bounds__(64 * kExWaves) suffix_exact_kernel(SuffixArgs 
         char* dst = reinterpret_cast<char*>(s_t[b]);
         // K codes (32*D halves) and V^T codes (32*D halves) as 1 KiB chunks, and the K and
         // V scales between them (128*NB bytes) as 16-byte pieces, SC_LANES per wave
+        // Every wave issues kPer loads, so that the wait counts below hold for every wave:
+        // a load past the step's chunks (or pieces) repeats one in range into that one's
+        // own place (the same bytes twice).
 #pragma unroll
-        for (uint32_t u = 0; u < KV_CHUNKS / kExWaves; ++u) {
-            const uint32_t chunk = wave + kExWaves * u;
+        for (uint32_t u = 0; u < kChunkLoads; ++u) {
+            const uint32_t chunk = min(wave + kExWaves * u, KV_CHUNKS - 1);
             const uint32_t off = chunk < KV_CHUNKS / 2 ? chunk * 1024 : chunk * 1024 + 128 * NB;
             __builtin_amdgcn_global_load_lds(src + off + lane * 16, dst + off, 16, 0, 0);
         }
-        const uint32_t soff = 64 * D + wave * SC_LANES * 16;
+        const uint32_t soff = 64 * D + min(wave * SC_LANES, SC_PIECES - SC_LANES) * 16;
         if (lane < SC_LANES) __builtin_amdgcn_global_load_lds(src + soff + lane * 16, dst + soff, 16, 0, 0);
     };
 
