@@ -336,15 +336,17 @@ miikv_status miikv_suffix_append_attn(const miikv_view* view, const uint16_t* k_
  * for the next call, also when a short suffix runs as decodes.  One workspace per
  * (layer, sequence); a workspace of miikv_suffix_workspace_bytes() bytes suffices.
  * The first call of a sequence (base position 0) needs no earlier call.
- * MIIKV_SUFFIX_EXACT: every token runs as a decode (batches of decodes over the
- * sequence, as short suffixes do), which keeps an fp32 query's low half and applies
- * the block scales in fp32 -- the reference's fp32 products
- * (qwen3_primitives.hip:6789-7207) to the decode path's precision -- where the MFMA
- * path takes the query and the dequantised keys as fp16.  It streams the context
- * once per row set of tokens, so it costs several times the MFMA path on long
- * suffixes.  Needs q_heads / kv_heads <= 16 (else MIIKV_EUNSUPPORTED) and a
- * workspace of miikv_suffix_workspace_bytes_ex(view, q_heads, token_count, flags)
- * bytes (else MIIKV_EWORKSPACE; it never falls back to the MFMA path). */
+ * MIIKV_SUFFIX_EXACT: the reference's fp32 products (qwen3_primitives.hip:6789-7207)
+ * to the decode path's precision, where the MFMA path takes the query and the
+ * dequantised keys as fp16: an fp32 query's low half is kept and the key block scales
+ * are applied in fp32.  A long suffix over q8 planes runs on exact-product MFMA
+ * kernels (key codes as exact fp16, one MFMA per 32-value block with its scale in
+ * fp32, a second one for the query's low half; about 2.2x the MFMA path at config 4);
+ * short suffixes, the other quant modes and chunked prefill (TILES_CURRENT) run every
+ * token as a decode (batches of decodes over the sequence).  Needs q_heads / kv_heads
+ * <= 16 (else MIIKV_EUNSUPPORTED) and a workspace of
+ * miikv_suffix_workspace_bytes_ex(view, q_heads, token_count, flags) bytes (else
+ * MIIKV_EWORKSPACE; it never falls back to the fp16 MFMA path). */
 #define MIIKV_SUFFIX_TILES_CURRENT 1u
 #define MIIKV_SUFFIX_EXACT 2u
 /* Workspace of miikv_suffix_attn_ex with `flags`: miikv_suffix_workspace_bytes(),
