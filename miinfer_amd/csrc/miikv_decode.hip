@@ -674,7 +674,7 @@ decode_kernel(SplitArgs a) {
         const bool grow = cmax > m_run + kRescaleSlack;
         if (__any(grow)) {
             const float m_new = grow ? cmax : m_run;
-            const float alpha = fast_exp2(m_run - m_new);
+            const float alpha = grow ? fast_exp2(m_run - cmax) : 1.0f;  // (-inf - -inf would be NaN)
             m_run = m_new;
             l_run *= alpha;
 #pragma unroll
@@ -1030,7 +1030,7 @@ static miikv_status decode_impl(const miikv_view* view, const NewRows& rows,
     if (p.splits > 65535u || batch > 65535u || static_cast<uint64_t>(batch) * view->kv_heads > 0x7fffffffu)
         return MIIKV_EINVAL;
 
-    SplitArgs a;
+    SplitArgs a{};
     a.g = make_geo(*view);
     a.q = q;
     a.q_heads = q_heads;

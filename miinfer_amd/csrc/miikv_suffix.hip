@@ -343,15 +343,14 @@ __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
                 }
             }
         } else {
+            // every load issued unconditionally (qrow is a valid row), then selected
 #pragma unroll
             for (uint32_t c = 0; c < NC; ++c) {
-                half8 v = {};
-                if (row_ok) {
-                    const uint16_t* qp = static_cast<const uint16_t*>(a.q) + qrow + c * 16 + hh * 8;
-                    v = __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(qp));
-                }
-                qf[c] = v;
+                const uint16_t* qp = static_cast<const uint16_t*>(a.q) + qrow + c * 16 + hh * 8;
+                qf[c] = __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(qp));
             }
+#pragma unroll
+            for (uint32_t c = 0; c < NC; ++c) qf[c] = row_ok ? qf[c] : half8{};
         }
     }
 
@@ -412,7 +411,7 @@ __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
         const bool grow = cm > m_run + kSlackS;
         if (__any(grow)) {
             const float m_new = grow ? cm : m_run;
-            const float alpha = sfx_exp2(m_run - m_new);
+            const float alpha = grow ? sfx_exp2(m_run - cm) : 1.0f;  // (-inf - -inf would be NaN)
             m_run = m_new;
             l_run *= alpha;
 #pragma unroll
@@ -809,7 +808,7 @@ __global__ void __launch_bounds__(64 * kExWaves) suffix_exact_kernel(SuffixArgs 
         const bool grow = cm > m_run + kSlackS;
         if (__any(grow)) {
             const float m_new = grow ? cm : m_run;
-            const float alpha = sfx_exp2(m_run - m_new);
+            const float alpha = grow ? sfx_exp2(m_run - cm) : 1.0f;  // (-inf - -inf would be NaN)
             m_run = m_new;
             l_run *= alpha;
 #pragma unroll
@@ -1100,7 +1099,7 @@ static void launch_suffix_combine(const miikv_view* view, uint32_t q_heads, uint
                                   uint32_t base_position, const miikv_prefill_state* prefill_state,
                                   const SuffixPlan& plan, void* part, float* out, const float* gate, float* gated_out,
                                   hipStream_t s, bool f32 = false) {
-    SuffixCombineArgs c;
+    SuffixCombineArgs c{};
     c.kv_heads = view->kv_heads;
     c.q_heads = q_heads;
     c.group = G;
@@ -1162,7 +1161,7 @@ static miikv_status suffix_impl(const miikv_view* view, const uint16_t* k_new, c
     const uint64_t stride_bound = current ? cap : 0;
     const uint32_t host_step0 = current && prefill_state == nullptr ? base_position / kSufStep : 0u;
     auto expand = [&](const SuffixPlan& plan, bool append) {
-        ExpandArgs e;
+        ExpandArgs e{};
         e.g = make_geo(*view);
         e.seq = seq;
         e.key_count = bound32;
@@ -1206,7 +1205,7 @@ static miikv_status suffix_impl(const miikv_view* view, const uint16_t* k_new, c
         }
         if (xp.steps > 65535u * 64u) return MIIKV_EINVAL;
         const uint64_t xblocks = (rows + kExRows - 1) / kExRows;
-        ExpandArgs e;
+        ExpandArgs e{};
         e.g = make_geo(*view);
         e.seq = seq;
         e.key_count = bound32;
@@ -1222,7 +1221,7 @@ static miikv_status suffix_impl(const miikv_view* view, const uint16_t* k_new, c
         const dim3 egrid(static_cast<uint32_t>((bound + kSufStep - 1) / kSufStep), view->kv_heads);
         if (view->head_dim == 128) hipLaunchKernelGGL((expand_exact_kernel<128>), egrid, dim3(256), 0, s, e);
         else hipLaunchKernelGGL((expand_exact_kernel<256>), egrid, dim3(256), 0, s, e);
-        SuffixArgs a;
+        SuffixArgs a{};
         a.g = make_geo(*view);
         a.q = q;
         a.q_f32 = q_dtype == MIIKV_DTYPE_F32;
@@ -1282,7 +1281,7 @@ static miikv_status suffix_impl(const miikv_view* view, const uint16_t* k_new, c
 
     expand(plan, k_new != nullptr);
 
-    SuffixArgs a;
+    SuffixArgs a{};
     a.g = make_geo(*view);
     a.q = q;
     a.q_f32 = q_dtype == MIIKV_DTYPE_F32;

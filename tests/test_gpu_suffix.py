@@ -36,7 +36,10 @@ def _setup(gpu, rng, hq, hk, d, prefix, t, cap):
                                               (8, 8, 128, 3000, 130),
                                               # more query heads per kv head than decode's
                                               # 16 MFMA columns: the MFMA path only
-                                              (34, 2, 128, 300, 9), (40, 2, 256, 100, 20)])
+                                              (34, 2, 128, 300, 9), (40, 2, 256, 100, 20),
+                                              # split plans evenly divided over the
+                                              # workgroup slots, ranges across row blocks
+                                              (24, 4, 256, 2000, 100), (12, 2, 128, 600, 300)])
 @pytest.mark.parametrize("split", [True, False])
 def test_suffix_small(gpu, hq, hk, d, prefix, t, split):
     import miinfer_amd as m
