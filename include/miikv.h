@@ -264,9 +264,13 @@ miikv_status miikv_decode_append_attn_f32(const miikv_view* view, const float* k
  * any context needs ~1.1 MB, 16 sequences of 24q/4kv/D256 up to 64k ~13 MB); a
  * geometry whose
  * miikv_decode_workspace_bytes() exceeds it returns MIIKV_EWORKSPACE.  Nothing is
- * allocated (the array's address is looked up once per device).  All calls on one
- * GPU share that array: calls that overlap on one GPU (other streams, other
- * threads) race and must be serialised by the caller. */
+ * allocated (the array's address is looked up, and one event made, once per device
+ * at the first call).  All calls on one GPU share that array, so the library orders
+ * them: one host lock covers each call's enqueue, and a call on another stream than
+ * the previous call's waits for an event recorded after that call's kernels.  Inside
+ * a stream capture that wait and record are left out (the graph's order applies):
+ * replays of captured graphs that overlap on one GPU (several streams at once) race
+ * on the array and must be serialised by the caller. */
 uint64_t miikv_decode_scratch_max_bytes(void);
 miikv_status miikv_decode_append_attn_noalloc(const miikv_view* view, const uint16_t* k_new,
                                               const uint16_t* v_new, const void* q, uint32_t q_dtype,

@@ -1235,29 +1235,43 @@ extern "C" miikv_status miikv_decode_append_attn_f32(const miikv_view* view, con
 // workspace.  Every GPU the library runs on holds its own copy until the process
 // ends; host code uses its per-device address from hipGetSymbolAddress, never the
 // array's name (a host-side stand-in that is not a device address).
+// Calls are ordered on the GPU: one host lock covers each call's enqueue, and a
+// call on another stream than the previous call's first waits for an event the
+// previous call recorded after its kernels (both made once per device, at the first
+// call).  Inside a stream capture neither the wait nor the record is issued: the
+// graph's own order applies, and replays of such graphs on several streams at once
+// race on the array.
 namespace {
 constexpr uint64_t kScratchBytes = 16ull << 20;
 __device__ __align__(256) uint8_t scratch[kScratchBytes];
 constexpr int kMaxDevices = 64;
-void* g_scratch_ptr[kMaxDevices] = {};
+struct ScratchDevice {
+    void* ptr = nullptr;          // the device address of `scratch`
+    hipEvent_t done = nullptr;    // recorded after the last uncaptured call's kernels
+    hipStream_t stream = nullptr; // that call's stream
+    bool recorded = false;
+};
+ScratchDevice g_scratch[kMaxDevices];
 std::mutex g_scratch_mutex;
 
-// Device address of this device's `scratch`, looked up once per device (with that
-// device current).  Returns a HIP status.
-int scratch_for_current_device(void** out) {
+// This device's scratch state, set up once per device (with that device current);
+// the caller holds g_scratch_mutex.  Returns a status.
+int scratch_for_current_device(ScratchDevice** out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_status(e);
     if (dev < 0 || dev >= kMaxDevices) return MIIKV_EUNSUPPORTED;
-    std::lock_guard<std::mutex> lock(g_scratch_mutex);
-    if (g_scratch_ptr[dev] == nullptr) {
+    ScratchDevice& sd = g_scratch[dev];
+    if (sd.ptr == nullptr) {
         void* ptr = nullptr;
         e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
         if (e != hipSuccess) return hip_status(e);
         if (ptr == nullptr) return MIIKV_EUNSUPPORTED;
-        g_scratch_ptr[dev] = ptr;
+        e = hipEventCreateWithFlags(&sd.done, hipEventDisableTiming);
+        if (e != hipSuccess) return hip_status(e);
+        sd.ptr = ptr;
     }
-    *out = g_scratch_ptr[dev];
+    *out = &sd;
     return MIIKV_OK;
 }
 }  // namespace
@@ -1275,12 +1289,29 @@ extern "C" miikv_status miikv_decode_append_attn_noalloc(const miikv_view* view,
     const uint64_t need = miikv_decode_workspace_bytes(view, q_heads, batch, max_context);
     if (need == 0) return MIIKV_EINVAL;
     if (need > kScratchBytes) return MIIKV_EWORKSPACE;  // beyond the fixed scratch: use miikv_decode_append_attn
-    void* ptr = nullptr;
-    const int st = scratch_for_current_device(&ptr);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    ScratchDevice* sd = nullptr;
+    const int st = scratch_for_current_device(&sd);
     if (st != MIIKV_OK) return st;
+    hipStream_t hs = static_cast<hipStream_t>(stream);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(hs, &cap);
+    if (e != hipSuccess) return hip_status(e);
+    const bool capturing = cap != hipStreamCaptureStatusNone;
+    if (!capturing && sd->recorded && sd->stream != hs) {
+        e = hipStreamWaitEvent(hs, sd->done, 0);
+        if (e != hipSuccess) return hip_status(e);
+    }
     NewRows rows;
     rows.k16 = k_new;
     rows.v16 = v_new;
-    return decode_impl(view, rows, q, q_dtype, q_heads, scale, batch, d_lengths, decode_state, max_context,
-                       out, gate, gated_out, gated_q8_1, ptr, kScratchBytes, stream);
+    const miikv_status ds = decode_impl(view, rows, q, q_dtype, q_heads, scale, batch, d_lengths, decode_state,
+                                        max_context, out, gate, gated_out, gated_q8_1, sd->ptr, kScratchBytes,
+                                        stream);
+    if (ds != MIIKV_OK || capturing) return ds;
+    e = hipEventRecord(sd->done, hs);
+    if (e != hipSuccess) return hip_status(e);
+    sd->stream = hs;
+    sd->recorded = true;
+    return MIIKV_OK;
 }

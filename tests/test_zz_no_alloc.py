@@ -17,7 +17,7 @@ def _dev(a, gpu):
     return torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
 
 
-def _run(cache, kn, vn, q, lens, max_ctx, noalloc, gpu, gate=None):
+def _run(cache, kn, vn, q, lens, max_ctx, noalloc, gpu, gate=None, sync=True):
     import miinfer_amd as m
     from miinfer_amd import _lib
     L = _lib.lib()
@@ -38,7 +38,8 @@ def _run(cache, kn, vn, q, lens, max_ctx, noalloc, gpu, gate=None):
         ws = m.DecodeWorkspace(cache, hq, batch, max_ctx)
         st = L.miikv_decode_append_attn(*args, P(ws.buf.data_ptr()), ws.bytes, s)
     assert st == 0, st
-    torch.cuda.synchronize()
+    if sync:
+        torch.cuda.synchronize()
     return out, gated, q81
 
 
@@ -124,3 +125,23 @@ def test_noalloc_rejects_geometry_beyond_scratch(gpu):
                                             P(lens.data_ptr()), None, 512 * pt, P(out.data_ptr()), None, None,
                                             None, None)
     assert st == _lib.MIIKV_EWORKSPACE
+
+
+def test_noalloc_calls_on_two_streams_are_ordered(gpu):
+    """Two calls on two streams, enqueued back to back without a host sync: the
+    second waits for the first's kernels (they share the scratch array), so both
+    match the workspace entry point."""
+    rng = np.random.default_rng(17)
+    big = _contiguous_case(gpu, rng, 32, 8, 128, 32768, 32768)
+    small = _contiguous_case(gpu, rng, 32, 8, 128, 2000, 4096)
+    want_big = _run(big[0][0], *big[1:], 32768, False, gpu)
+    want_small = _run(small[0][0], *small[1:], 4096, False, gpu)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for _ in range(3):
+        with torch.cuda.stream(s1):
+            got_big = _run(big[0][1], *big[1:], 32768, True, gpu, sync=False)
+        with torch.cuda.stream(s2):
+            got_small = _run(small[0][1], *small[1:], 4096, True, gpu, sync=False)
+        torch.cuda.synchronize()
+        assert torch.equal(got_big[0], want_big[0])
+        assert torch.equal(got_small[0], want_small[0])
