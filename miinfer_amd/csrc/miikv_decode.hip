@@ -148,7 +148,8 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // Packed work items of a batch: sequence b owns ceil(L_b / split tokens) * kv_heads
 // items (none past *count_ptr).  Every workgroup scans the per-sequence counts
 // (256 sequences per pass, Hillis-Steele in LDS) and finds the item at index
-// `id`; false if the batch holds fewer items.  Called by all 256 threads.
+// `id`; false if the batch holds fewer items.  Called by every thread of the
+// workgroup (barriers inside); the first 256 threads do the scan.
 __device__ bool locate_item(const SplitArgs& a, uint32_t cpw, uint32_t id, uint32_t& b_out, uint32_t& h_out,
                             uint32_t& split_out) {
     __shared__ uint32_t s_scan[256];
@@ -159,21 +160,22 @@ __device__ bool locate_item(const SplitArgs& a, uint32_t cpw, uint32_t id, uint3
     const uint32_t count = a.count_ptr ? min(a.batch, *a.count_ptr) : a.batch;
     if (tid == 0) s_hit[0] = 0xffffffffu;
     uint32_t base = 0;
+    const bool scans = tid < 256;
     for (uint32_t b0 = 0; b0 < count; b0 += 256) {
         const uint32_t bb = b0 + tid;
-        const uint32_t nsplit = bb < count ? (split_length(a, bb) + tps - 1) / tps : 0;
+        const uint32_t nsplit = scans && bb < count ? (split_length(a, bb) + tps - 1) / tps : 0;
         const uint32_t n = nsplit * H;
-        s_scan[tid] = n;
+        if (scans) s_scan[tid] = n;
         __syncthreads();
         for (uint32_t off = 1; off < 256; off <<= 1) {
-            const uint32_t add = tid >= off ? s_scan[tid - off] : 0;
+            const uint32_t add = scans && tid >= off ? s_scan[tid - off] : 0;
             __syncthreads();
-            s_scan[tid] += add;
+            if (scans) s_scan[tid] += add;
             __syncthreads();
         }
-        const uint32_t incl = base + s_scan[tid];
+        const uint32_t incl = base + (scans ? s_scan[tid] : 0);
         const uint32_t excl = incl - n;
-        if (id >= excl && id < incl) {
+        if (scans && id >= excl && id < incl) {
             const uint32_t rem = id - excl;
             s_hit[0] = bb;
             s_hit[1] = rem / nsplit;

@@ -73,16 +73,16 @@ __device__ __forceinline__ uint32_t split_length(const SplitArgs& a, uint32_t b)
 // are only known on the device, so every workgroup of both kernels derives the
 // same value from them: the smallest cpw (>= the host's, which sized the records)
 // for which the work items, at most sum(L_b) * H / (4 waves * 32 * cpw) + count * H,
-// fit in one round of `slots` resident workgroups.  Called by all threads of a
-// 256-thread block (barriers inside).
+// fit in one round of `slots` resident workgroups.  Called by every thread of the
+// workgroup (barriers inside); the first 256 threads do the sum.
 __device__ uint32_t launch_cpw(const SplitArgs& a) {
     if (a.batch == 1 || a.slots == 0) return a.cpw;
     __shared__ unsigned long long s_sum[256];
     const uint32_t tid = threadIdx.x;
     const uint32_t count = a.count_ptr ? min(a.batch, *a.count_ptr) : a.batch;
     unsigned long long sum = 0;
-    for (uint32_t bb = tid; bb < count; bb += 256) sum += split_length(a, bb);
-    s_sum[tid] = sum;
+    for (uint32_t bb = tid; bb < count && tid < 256; bb += 256) sum += split_length(a, bb);
+    if (tid < 256) s_sum[tid] = sum;
     __syncthreads();
     for (uint32_t off = 128; off > 0; off >>= 1) {
         if (tid < off) s_sum[tid] += s_sum[tid + off];
