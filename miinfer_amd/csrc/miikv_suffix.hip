@@ -283,15 +283,27 @@ __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
     // XCD-aware order: workgroup L runs on XCD L % 8.  Each XCD gets an equal,
     // contiguous range of the (group, row block) sequence, group-major, so the
     // row blocks of one (kv head, split) group, which read the same tiles, share
-    // an L2.  The grid is padded to a multiple of 8 workgroups.
+    // an L2; with rows_together the sequence is (kv head, row block, split).  The
+    // grid is padded to a multiple of 8 workgroups.
     const uint32_t L = blockIdx.x;
     const uint32_t per_xcd = gridDim.x / 8;
     const uint32_t idx = (L % 8) * per_xcd + L / 8;
-    const uint32_t grp = idx / a.row_blocks;
-    if (grp >= a.g.kv_heads * a.splits) return;
-    const uint32_t h = grp % a.g.kv_heads;
-    const uint32_t split = grp / a.g.kv_heads;
-    const uint32_t rb = idx % a.row_blocks;
+    uint32_t h, split, rb;
+    if (a.rows_together) {
+        // the splits of one row block next to each other: an XCD's workgroups share
+        // their query rows through its L2 (and each tile range among fewer of them)
+        const uint32_t gi = idx / a.splits;
+        split = idx % a.splits;
+        h = gi / a.row_blocks;
+        rb = gi % a.row_blocks;
+        if (h >= a.g.kv_heads) return;
+    } else {
+        const uint32_t grp = idx / a.row_blocks;
+        if (grp >= a.g.kv_heads * a.splits) return;
+        h = grp % a.g.kv_heads;
+        split = grp / a.g.kv_heads;
+        rb = idx % a.row_blocks;
+    }
     const uint32_t tid = threadIdx.x;
     const uint32_t wave = tid >> 6;
     const uint32_t lane = tid & 63;
@@ -1300,6 +1312,11 @@ static miikv_status suffix_impl(const miikv_view* view, const uint16_t* k_new, c
     a.out = out;
     a.gate = gate;
     a.gated_out = gated_out;
+    // Short splits: the splits of a row block on one XCD (config 4, 55 steps per
+    // split: 135.0 -> 131.7 us; the ladder at P = 4096 3.5% faster); long ones keep
+    // the (kv head, split)-major order, whose tiles more row blocks share (P = 65536:
+    // 0.3% slower the other way, P = 32768 level).
+    a.rows_together = plan.splits > 1 && plan.split_keys <= 128 * kSufStep ? 1u : 0u;
     const uint64_t groups = static_cast<uint64_t>(view->kv_heads) * plan.splits;
     const uint64_t wgs = (groups * blocks + 7) / 8 * 8;
     if (wgs > 0x7fffffffu) return MIIKV_EINVAL;

@@ -75,6 +75,7 @@ struct SuffixArgs {
     float* out;
     const float* gate;
     float* gated_out;
+    uint32_t rows_together;  // suffix_kernel order: (kv head, row block, split) when set
 };
 
 // Partial records of split-K, laid out so that a wave's 32 rows write one
