@@ -391,7 +391,9 @@ __global__ void __launch_bounds__(64 * kSufWaves) suffix_kernel(SuffixArgs a) {
     constexpr uint32_t kPer = CHUNKS / kSufWaves;  // loads per wave per fetch
     for (uint32_t k = 0; k < kDist; ++k)
         if (s_begin + k < s_end) fetch(s_begin + k, (s_begin + k) % kSufBufs);
-    wait_vmem();
+    // the query and the first step's tile; the later prefetches may stay in flight
+    if (kDist > 1 && s_begin + 1 < s_end) wait_vmem_le<(kDist - 1) * kPer>();
+    else wait_vmem();
     __syncthreads();
 
     // ---- S^T = K^ Q^T of step s
