@@ -1,6 +1,6 @@
 """Decode attention over a 32k-token q8_0 KV cache on one MI355X.
 
-Workload (BASELINE config 2 at its largest context): Qwen3-8B-shaped GQA layer,
+Workload (the headline benchmark's config 2 at its largest context): Qwen3-8B-shaped GQA layer,
 32 query heads, 8 KV heads, head_dim 128, batch 1, context 32768.  One step =
 one layer-token: quantize-append one fp16 K/V row per KV head into the q8_0
 cache (at position 32767), then single-token attention over the 32768 cached
@@ -58,7 +58,7 @@ def _cpu_case(ctx, seed, threads, warmup, reps):
 
 
 def cpu_baseline() -> dict:
-    """BASELINE config 1 on the host CPU: the oracle's C restatement of the reference
+    """Config 1 of the headline benchmark on the host CPU: the oracle's C restatement of the reference
     CPU attention path (fp32 loop over a dequantised cache, double-denominator softmax),
     32q/8kv/D128, one fp16 query, context 4096; plus the GPU headline's context (32768)."""
     nproc = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
