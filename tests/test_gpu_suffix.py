@@ -628,6 +628,37 @@ def test_suffix_exact_mfma_kernel_shapes(gpu, hq, hk, d, paged):
         assert_attention_close(gated.cpu().numpy(), expect / (1 + np.exp(-gate)), f"exact gated {ws}")
 
 
+def test_suffix_exact_config4_full_size(gpu):
+    """Config 4 as bench.py times the exact route: miikv_suffix_append_attn_ex with
+    MIIKV_SUFFIX_EXACT stores 512 rows over an 8192-token prefix (24q/4kv/D256) and
+    attends with an fp32 query at logits of s.d. ~6 (queries x3, scale x2); two tokens of
+    every 32-token block of the suffix, token 511 among them, against the oracle, and the
+    stored rows bit-exact."""
+    import miinfer_amd as m
+    hq, hk, d, prefix, t = 24, 4, 256, 8192, 512
+    rng = np.random.default_rng(45)
+    cap = prefix + t
+    k = randn_f16(rng, (cap, hk, d))
+    v = randn_f16(rng, (cap, hk, d))
+    cache = m.KvCache.contiguous(hk, d, cap)
+    cache.append(_dev(k[:prefix], gpu), _dev(v[:prefix], gpu), base_position=0)
+    q = (rng.standard_normal((t, hq, d)) * 3).astype(np.float32)
+    scale = 2 / math.sqrt(d)
+    out, _ = m.suffix_attention(cache, _dev(q, gpu), prefix, scale, k_new=_dev(k[prefix:], gpu),
+                                v_new=_dev(v[prefix:], gpu), exact=True)
+    torch.cuda.synchronize()
+    kc, ks = oracle.quantize_rows(k.transpose(1, 0, 2))
+    vc, vs = oracle.quantize_rows(v.transpose(1, 0, 2))
+    got_kc, got_ks, got_vc, got_vs = cache.export_canonical(0, prefix, t)
+    torch.cuda.synchronize()
+    assert np.array_equal(got_kc.cpu().numpy(), kc[:, prefix:])
+    assert np.array_equal(got_vc.cpu().numpy(), vc[:, prefix:])
+    out = out.cpu().numpy()
+    for tok in sorted({x for b in range(0, t, 32) for x in (b, b + 17)} | {t - 1}):
+        expect = oracle.attention_q8(q[tok], kc, ks, vc, vs, prefix + tok + 1, hq, scale)
+        assert_attention_close(out[tok], expect, f"exact token {tok}")
+
+
 def test_suffix_exact_route_errors(gpu):
     import miinfer_amd as m
     from miinfer_amd import _lib
